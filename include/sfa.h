@@ -1,0 +1,130 @@
+/*
+ * sfa.h — C ABI of libsfa.so, the MI355X (gfx950) top-k sparse flash attention.
+ *
+ * The boundary replaces the three kernel launches of the reference's autograd
+ * host launcher `SparseFlashAttentionTriton` (lilac-me/ops SFA.py:69-306):
+ *
+ *   sfa_fwd  <- `_attn_fwd[grid](...)`            SFA.py:122-159 (forward, SFA.py:75-164)
+ *   sfa_bwd  <- `_attn_bwd_dq_dsink[grid](...)`   SFA.py:199-251
+ *             + `_attn_bwd_dk_dv[grid](...)`      SFA.py:266-298 (backward, SFA.py:166-306)
+ *
+ * plus the workspace sizing the reference does inline with torch.empty
+ * (SFA.py:117-120, 188-194, 253-261) and its ValueError paths
+ * (SFA.py:52-53, 63-64).
+ *
+ * Conventions
+ *  - Layout is BSHD with element strides for the batch, sequence and head
+ *    dimensions; the last (feature) dimension must be contiguous.
+ *      q   [B, Sq,  Hq,  Dqk]     k [B, Skv, Hkv, Dqk]     v [B, Skv, Hkv, Dv]
+ *      idx [B, Sq,  Hkv, topk]  int32, -1 (or any out-of-range value) = padding
+ *      out [B, Sq,  Hq,  Dv]      lse [B, Sq, Hq] float32, natural log
+ *    `v` may alias `k` (e.g. MLA: v = k[..., :Dv]); inputs are never written.
+ *    Query head h reads KV head h / (Hq / Hkv).
+ *  - A slot is valid iff 0 <= idx < bound, bound = kv_lens[b] (if non-NULL,
+ *    clamped to Skv) else Skv.  Invalid slots contribute exactly nothing; a
+ *    row with no valid slot gives out = 0 and lse = -inf.
+ *  - `sink` (optional, float32 [Hq]) adds exp(sink[h]) to every softmax
+ *    denominator as SFA.py:469-474 does; NULL means no sink.
+ *  - All pointers are device pointers.  The library never allocates, frees
+ *    or synchronises: scratch comes from the caller through `workspace`,
+ *    whose size the *_workspace_size functions give for the same arguments.
+ *    All work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *  - Return value: 0 on success, a negative SFA_E* code otherwise; the
+ *    message for the calling thread is available from sfa_last_error().
+ */
+#ifndef SFA_H_
+#define SFA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFA_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define SFA_API __attribute__((visibility("default")))
+#else
+#define SFA_API
+#endif
+
+/* Element types of q, k, v, out, dout, dq, dk, dv. */
+enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1 };
+
+/* How the backward produces dK/dV. */
+enum {
+  SFA_DKV_AUTO = 0,    /* library default (fp32 atomics)                                */
+  SFA_DKV_ATOMIC = 1,  /* fp32 atomic adds into a workspace accumulator (SFA.py:853)    */
+  SFA_DKV_CSR = 2      /* deterministic: per-key CSR of referencing queries + reduction */
+};
+
+/* Error codes. */
+enum {
+  SFA_OK = 0,
+  SFA_E_INVALID = -1,   /* bad shape / stride / dtype / null pointer (ValueError) */
+  SFA_E_WORKSPACE = -2, /* workspace missing or too small                        */
+  SFA_E_UNSUPPORTED = -3,
+  SFA_E_HIP = -4        /* a HIP runtime call failed (RuntimeError)               */
+};
+
+typedef struct sfa_fwd_args {
+  int32_t dtype;                 /* SFA_DTYPE_*                                       */
+  int32_t B, Sq, Skv, Hq, Hkv, Dqk, Dv, topk;
+  float scale;                   /* softmax scale; <= 0 means 1/sqrt(Dqk) (SFA.py:181-182) */
+  const void* q;   int64_t q_sb, q_ss, q_sh;
+  const void* k;   int64_t k_sb, k_ss, k_sh;
+  const void* v;   int64_t v_sb, v_ss, v_sh;
+  const int32_t* idx; int64_t i_sb, i_ss, i_sh;   /* slot stride is 1 */
+  const int32_t* kv_lens;        /* [B] or NULL                                        */
+  const float* sink;             /* [Hq] or NULL                                       */
+  void* out;       int64_t o_sb, o_ss, o_sh;
+  float* lse;      int64_t l_sb, l_ss, l_sh;      /* head stride of lse             */
+  int32_t num_splits;            /* split-k over the top-k set; 0 = library choice      */
+  int32_t flags;                 /* reserved, must be 0                                 */
+} sfa_fwd_args;
+
+typedef struct sfa_bwd_args {
+  sfa_fwd_args fwd;              /* the forward's arguments; out/lse are read here      */
+  const void* dout; int64_t do_sb, do_ss, do_sh;
+  void* dq;        int64_t dq_sb, dq_ss, dq_sh;
+  void* dk;        int64_t dk_sb, dk_ss, dk_sh;
+  void* dv;        int64_t dv_sb, dv_ss, dv_sh;
+  const float* dlse;             /* gradient w.r.t. lse, float32, lse's strides; NULL = 0 */
+  float* dsink;                  /* [Hq] float32, written (not accumulated); NULL if no sink */
+  int32_t dkv_mode;              /* SFA_DKV_*                                           */
+  int32_t flags;                 /* reserved, must be 0                                 */
+} sfa_bwd_args;
+
+/* Library ABI version (SFA_ABI_VERSION of the build). */
+SFA_API int sfa_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+SFA_API const char* sfa_last_error(void);
+
+/* Bytes of device workspace sfa_fwd needs for `a` (0 when none).
+ * Replaces the per-launch workspaces of SFA.py:117-120; only the split-k
+ * partial results of the decode shape remain. */
+SFA_API size_t sfa_fwd_workspace_size(const sfa_fwd_args* a);
+
+/* Forward: out = softmax(scale * q k[idx]^T) v[idx], lse = log-sum-exp.
+ * Replaces `_attn_fwd` (SFA.py:483-587 via SFA.py:122-159). */
+SFA_API int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace sfa_bwd needs for `a` (fp32 dK/dV accumulators,
+ * delta, and the CSR arrays in SFA_DKV_CSR mode).
+ * Replaces the workspaces of SFA.py:184-194 and SFA.py:253-261. */
+SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
+
+/* Backward: dq, dk, dv (and dsink if requested) from dout, out and lse.
+ * Replaces `_attn_bwd_dq_dsink` (SFA.py:856-1002 via SFA.py:199-251) and
+ * `_attn_bwd_dk_dv` (SFA.py:1005-1145 via SFA.py:266-298).  dq/dk/dv are
+ * fully overwritten (no accumulation into existing contents). */
+SFA_API int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SFA_H_ */

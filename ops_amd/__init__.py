@@ -1,0 +1,13 @@
+"""ops_amd — MI355X (gfx950) top-k sparse flash attention.
+
+Public API (BSHD, see ``ops_amd.sfa``)::
+
+    out, lse = ops_amd.sparse_flash_attention(q, k, v, topk_idxs, sm_scale=None,
+                                              kv_lens=None, attn_sink=None)
+
+The HIP kernels live in ``libsfa.so`` (``python -m ops_amd.build``), reached
+through the C ABI declared in ``include/sfa.h``.
+"""
+from .sfa import SparseFlashAttention, sfa_backward, sfa_forward, sparse_flash_attention
+
+__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward"]

@@ -1,0 +1,56 @@
+"""Build libsfa.so (HIP, gfx950) in-tree with hipcc.
+
+``python -m ops_amd.build`` compiles every ``csrc/*.hip`` into
+``ops_amd/libsfa.so``.  Flags: -O3, gfx950 only, and packed-fp32 ops disabled
+(``-Xclang -target-feature -Xclang -packed-fp32-ops``) so hipcc never emits
+v_pk_{add,mul,fma}_f32.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libsfa.so"
+ARCH = os.environ.get("SFA_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fvisibility=hidden", "-Wno-unused-result",
+    # MFMA builtins in VGPR form: the large O^T accumulators are pinned to
+    # AGPRs explicitly, everything else stays in VGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if c and (os.path.sep not in c or os.path.exists(c)):
+            return c
+    return "hipcc"
+
+
+def sources():
+    return sorted(str(p) for p in CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False, extra=None) -> Path:
+    """Compile the library; raises CalledProcessError on a compile failure."""
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(extra or []), "-I", str(HERE.parent / "include"), *sources(), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise subprocess.CalledProcessError(res.returncode, cmd, res.stdout, res.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

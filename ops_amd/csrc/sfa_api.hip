@@ -1,0 +1,237 @@
+// C ABI of libsfa.so (declared in include/sfa.h): argument validation,
+// workspace sizing and kernel dispatch.  The library never allocates, frees
+// or synchronises; all work goes onto the caller's stream.
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "sfa_common.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SFA_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+constexpr int kMaxHeadDim = 1024;
+constexpr int kGenericMaxTopk = 12288;  // scores of one row stay in 64 KiB of LDS
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Validation shared by forward and backward (SFA.py:52-53, 63-64 raise
+// ValueError for an empty or non-positive top-k; this boundary also checks
+// everything the kernels assume).
+int check_fwd(const sfa_fwd_args* a) {
+  if (a == nullptr) return fail(SFA_E_INVALID, "null argument struct");
+  if (a->dtype != SFA_DTYPE_F32 && a->dtype != SFA_DTYPE_BF16) return fail(SFA_E_INVALID, "unknown dtype %d", a->dtype);
+  if (a->B <= 0 || a->Sq <= 0 || a->Skv <= 0 || a->Hq <= 0 || a->Hkv <= 0)
+    return fail(SFA_E_INVALID, "B, Sq, Skv, Hq, Hkv must be positive");
+  if (a->topk <= 0) return fail(SFA_E_INVALID, "topk must be positive (got %d)", a->topk);
+  if (a->Hq % a->Hkv != 0) return fail(SFA_E_INVALID, "Hq (%d) must be a multiple of Hkv (%d)", a->Hq, a->Hkv);
+  if (a->Dqk <= 0 || a->Dv <= 0 || a->Dqk > kMaxHeadDim || a->Dv > kMaxHeadDim)
+    return fail(SFA_E_INVALID, "head dims must be in [1, %d]", kMaxHeadDim);
+  if (!a->q || !a->k || !a->v || !a->idx || !a->out || !a->lse) return fail(SFA_E_INVALID, "null tensor pointer");
+  if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if (a->num_splits < 0) return fail(SFA_E_INVALID, "num_splits must be >= 0");
+  if (!(a->scale == a->scale) || isinf(a->scale)) return fail(SFA_E_INVALID, "scale must be finite");
+  return SFA_OK;
+}
+
+sfa::Params to_params(const sfa_fwd_args* a) {
+  sfa::Params p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.k = a->k; p.v = a->v; p.idx = a->idx; p.kv_lens = a->kv_lens; p.sink = a->sink;
+  p.out = a->out; p.lse = a->lse;
+  p.q_sb = a->q_sb; p.q_ss = a->q_ss; p.q_sh = a->q_sh;
+  p.k_sb = a->k_sb; p.k_ss = a->k_ss; p.k_sh = a->k_sh;
+  p.v_sb = a->v_sb; p.v_ss = a->v_ss; p.v_sh = a->v_sh;
+  p.i_sb = a->i_sb; p.i_ss = a->i_ss; p.i_sh = a->i_sh;
+  p.o_sb = a->o_sb; p.o_ss = a->o_ss; p.o_sh = a->o_sh;
+  p.l_sb = a->l_sb; p.l_ss = a->l_ss; p.l_sh = a->l_sh;
+  p.B = a->B; p.Sq = a->Sq; p.Skv = a->Skv; p.Hq = a->Hq; p.Hkv = a->Hkv;
+  p.Dqk = a->Dqk; p.Dv = a->Dv; p.topk = a->topk; p.G = a->Hq / a->Hkv;
+  p.scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->Dqk);
+  p.scale_log2 = p.scale * sfa::kLog2e;
+  p.num_splits = 1;
+  p.split_len = a->topk;
+  return p;
+}
+
+// MFMA eligibility beyond the kernel-variant shape: 16-byte aligned rows.
+bool mfma_layout_ok(const sfa_fwd_args* a) {
+  if (a->dtype != SFA_DTYPE_BF16) return false;
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->out)) return false;
+  const int64_t s[] = {a->q_sb, a->q_ss, a->q_sh, a->k_sb, a->k_ss, a->k_sh, a->v_sb, a->v_ss, a->v_sh,
+                       a->o_sb, a->o_ss, a->o_sh};
+  for (int64_t x : s)
+    if (x % 8 != 0) return false;
+  return true;
+}
+
+struct FwdPlan {
+  bool mfma;
+  int num_splits;
+  int split_len;
+  size_t part_o_bytes;
+  size_t part_lse_bytes;
+};
+
+constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
+constexpr int kIdxCap = 2048;
+
+FwdPlan plan_fwd(const sfa_fwd_args* a) {
+  FwdPlan pl{};
+  sfa::Params p = to_params(a);
+  pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p);
+  int splits = 1;
+  if (pl.mfma) {
+    const int nk = sfa::fwd_mfma_tile_keys(p);
+    const int64_t items = (int64_t)a->B * a->Sq * a->Hkv;
+    if (a->num_splits > 0) {
+      splits = a->num_splits;
+    } else if (items < kTargetWorkgroups / 2) {
+      // decode-like: too few work items to fill the chip -> split the top-k set
+      splits = (int)((kTargetWorkgroups / 2 + items - 1) / items);
+    }
+    // each split must fit the staged index window and hold at least one tile
+    const int min_splits = (a->topk + kIdxCap - 1) / kIdxCap;
+    if (splits < min_splits) splits = min_splits;
+    int max_splits = (a->topk + nk - 1) / nk;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    int len = (a->topk + splits - 1) / splits;
+    len = (len + nk - 1) / nk * nk;
+    splits = (a->topk + len - 1) / len;
+    pl.split_len = len;
+  } else {
+    if (a->num_splits > 1) splits = 1;  // the generic kernel is not split
+    pl.split_len = a->topk;
+  }
+  pl.num_splits = splits;
+  if (splits > 1) {
+    const size_t rows = (size_t)a->B * a->Sq * a->Hq;
+    pl.part_o_bytes = align_up((size_t)splits * rows * a->Dv * sizeof(float), 256);
+    pl.part_lse_bytes = align_up((size_t)splits * rows * sizeof(float), 256);
+  }
+  return pl;
+}
+
+int check_generic_fwd(const sfa_fwd_args* a) {
+  if (a->topk > kGenericMaxTopk)
+    return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d for this head-dim / group / dtype combination", a->topk,
+                kGenericMaxTopk);
+  return SFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sfa_abi_version(void) { return SFA_ABI_VERSION; }
+
+const char* sfa_last_error(void) { return g_err; }
+
+size_t sfa_fwd_workspace_size(const sfa_fwd_args* a) {
+  if (check_fwd(a) != SFA_OK) return 0;
+  const FwdPlan pl = plan_fwd(a);
+  return pl.part_o_bytes + pl.part_lse_bytes;
+}
+
+int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_fwd(a);
+  if (rc != SFA_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const FwdPlan pl = plan_fwd(a);
+  sfa::Params p = to_params(a);
+  hipError_t e;
+  if (pl.mfma) {
+    p.num_splits = pl.num_splits;
+    p.split_len = pl.split_len;
+    if (pl.num_splits > 1) {
+      if (workspace == nullptr || workspace_bytes < pl.part_o_bytes + pl.part_lse_bytes)
+        return fail(SFA_E_WORKSPACE, "sfa_fwd needs %zu workspace bytes (got %zu)", pl.part_o_bytes + pl.part_lse_bytes,
+                    workspace_bytes);
+      p.part_o = (float*)workspace;
+      p.part_lse = (float*)((char*)workspace + pl.part_o_bytes);
+    }
+    e = sfa::launch_fwd_mfma(p, s);
+    if (e != hipSuccess) return hip_fail(e, "sfa_fwd (mfma)");
+    if (pl.num_splits > 1) {
+      e = sfa::launch_combine(p, a->dtype, s);
+      if (e != hipSuccess) return hip_fail(e, "sfa_fwd (combine)");
+    }
+    return SFA_OK;
+  }
+  rc = check_generic_fwd(a);
+  if (rc != SFA_OK) return rc;
+  e = sfa::launch_fwd_generic(p, a->dtype, s);
+  if (e != hipSuccess) return hip_fail(e, "sfa_fwd (generic)");
+  return SFA_OK;
+}
+
+size_t sfa_bwd_workspace_size(const sfa_bwd_args* a) {
+  if (a == nullptr || check_fwd(&a->fwd) != SFA_OK) return 0;
+  const sfa_fwd_args& f = a->fwd;
+  const size_t dk = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dqk * sizeof(float), 256);
+  const size_t dv = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dv * sizeof(float), 256);
+  const size_t delta = align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
+  return dk + dv + delta;
+}
+
+int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (a == nullptr) return fail(SFA_E_INVALID, "null argument struct");
+  int rc = check_fwd(&a->fwd);
+  if (rc != SFA_OK) return rc;
+  const sfa_fwd_args& f = a->fwd;
+  if (!a->dout || !a->dq || !a->dk || !a->dv) return fail(SFA_E_INVALID, "null gradient pointer");
+  if (f.sink && !a->dsink) return fail(SFA_E_INVALID, "dsink is required when sink is given");
+  if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if (a->dkv_mode != SFA_DKV_AUTO && a->dkv_mode != SFA_DKV_ATOMIC && a->dkv_mode != SFA_DKV_CSR)
+    return fail(SFA_E_INVALID, "unknown dkv_mode %d", a->dkv_mode);
+  if (a->dkv_mode == SFA_DKV_CSR) return fail(SFA_E_UNSUPPORTED, "SFA_DKV_CSR is not available in this build");
+  const size_t need = sfa_bwd_workspace_size(a);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(SFA_E_WORKSPACE, "sfa_bwd needs %zu workspace bytes (got %zu)", need, workspace_bytes);
+  if (f.topk > kGenericMaxTopk) return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d", f.topk, kGenericMaxTopk);
+
+  hipStream_t s = (hipStream_t)stream;
+  sfa::Params p = to_params(&f);
+  p.dout = a->dout; p.do_sb = a->do_sb; p.do_ss = a->do_ss; p.do_sh = a->do_sh;
+  p.dq = a->dq; p.dq_sb = a->dq_sb; p.dq_ss = a->dq_ss; p.dq_sh = a->dq_sh;
+  const size_t nk = (size_t)f.B * f.Skv * f.Hkv * f.Dqk, nv = (size_t)f.B * f.Skv * f.Hkv * f.Dv;
+  p.dk_acc = (float*)workspace;
+  p.dv_acc = (float*)((char*)workspace + align_up(nk * sizeof(float), 256));
+  p.delta = (float*)((char*)p.dv_acc + align_up(nv * sizeof(float), 256));
+  p.dsink = a->dsink;
+  p.dlse = a->dlse;
+
+  hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
+  if (e == hipSuccess) e = sfa::launch_zero_f32(p.dv_acc, nv, s);
+  if (e == hipSuccess && p.dsink) e = sfa::launch_zero_f32(p.dsink, (size_t)f.Hq, s);
+  if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
+  if (e == hipSuccess) e = sfa::launch_bwd_generic(p, f.dtype, s);
+  if (e == hipSuccess)
+    e = sfa::launch_bwd_finish(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, a->dv, a->dv_sb, a->dv_ss, a->dv_sh,
+                               s);
+  if (e != hipSuccess) return hip_fail(e, "sfa_bwd");
+  return SFA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Shared definitions of the gfx950 sparse flash attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sfa.h"
+
+namespace sfa {
+
+constexpr float kLog2e = 1.4426950408889634f;  // base-2 softmax, SFA.py:13
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Internal launch parameters shared by every kernel (passed by value as
+// kernel arguments).  Element strides; feature dimension contiguous.
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* idx;
+  const int32_t* kv_lens;
+  const float* sink;
+  void* out;
+  float* lse;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t i_sb, i_ss, i_sh;
+  int64_t o_sb, o_ss, o_sh;
+  int64_t l_sb, l_ss, l_sh;
+  int B, Sq, Skv, Hq, Hkv, Dqk, Dv, topk, G;
+  float scale;        // softmax scale
+  float scale_log2;   // scale * log2(e): scores in base-2 units
+  // split-k partial results (forward, num_splits > 1)
+  int num_splits;
+  int split_len;      // slots per split (multiple of the key tile)
+  float* part_o;      // [num_splits][B*Sq*Hq][Dv], normalised by the split's own sum
+  float* part_lse;    // [num_splits][B*Sq*Hq], base-2 log-sum-exp of the split (-inf if empty)
+  // backward
+  const void* dout;
+  int64_t do_sb, do_ss, do_sh;
+  void* dq;
+  int64_t dq_sb, dq_ss, dq_sh;
+  float* dk_acc;      // [B, Skv, Hkv, Dqk] fp32 accumulators
+  float* dv_acc;      // [B, Skv, Hkv, Dv]  fp32 accumulators
+  float* delta;       // [B*Sq*Hq] Σ O·dO − dlse
+  const float* dlse;  // gradient w.r.t. lse (lse's strides) or nullptr
+  float* dsink;       // [Hq] (accumulated; zeroed by the launcher)
+};
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) { return static_cast<float>(x); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) { return static_cast<T>(x); }
+
+__device__ __forceinline__ int bound_of(const Params& p, int b) {
+  if (p.kv_lens == nullptr) return p.Skv;
+  int n = p.kv_lens[b];
+  return n < p.Skv ? n : p.Skv;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+// Buffer resource over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads 0
+
+}  // namespace sfa
+
+// Launchers implemented in the .hip translation units; return a HIP error.
+namespace sfa {
+hipError_t launch_fwd_generic(const Params& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_generic(const Params& p, int dtype, hipStream_t s);
+hipError_t launch_zero_f32(float* ptr, size_t n, hipStream_t s);
+hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss, int64_t dk_sh,
+                             void* dv, int64_t dv_sb, int64_t dv_ss, int64_t dv_sh, hipStream_t s);
+hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
+// MFMA paths: return hipErrorNotSupported when the shape has no variant.
+hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);
+bool fwd_mfma_supported(const Params& p);
+int fwd_mfma_tile_keys(const Params& p);
+}  // namespace sfa

@@ -1,0 +1,529 @@
+// gfx950 MFMA forward of top-k sparse flash attention (bf16 in, fp32 accumulate).
+//
+// Reference: `_attn_fwd` / `_inner_fwd` (lilac-me/ops SFA.py:309-587).  The
+// math is the same (gather the top-k rows, masked base-2 online softmax, P·V,
+// sink, LSE); the schedule is MI355X-native:
+//
+//  * One workgroup owns one (batch, query, kv-head[, split]) work item and
+//    all G = Hq/Hkv query heads of it, so every gathered KV row is used by all
+//    G heads (the reference re-gathers per 32-head tile, SFA.py:557).
+//  * Waves are arranged NSLICE (head slices of T heads) x NSPLITW (key
+//    sub-ranges).  A wave computes S^T = K·Q^T for its heads over 32 keys
+//    per tile: keys are MFMA rows, heads MFMA columns.  The fp32 S^T
+//    accumulator layout then already is the B-operand layout of
+//    O^T = V^T·P^T (contraction over keys), so P never leaves registers, and
+//    every lane owns exactly one head: row max / sum and the rescale of the
+//    O^T accumulator are per-lane scalars.
+//  * V^T operands are read from the row-major LDS tile with
+//    ds_read_b64_tr_b16 (gfx950 transposing LDS read).
+//  * KV rows are gathered straight into LDS with buffer_load_dwordx4 ... lds
+//    (no VGPR staging), double-buffered one tile ahead.  Invalid slots use an
+//    out-of-range buffer offset, so the hardware writes zeros.  LDS rows are
+//    padded by one 16-byte slot (row pitch = odd number of slots), which
+//    makes the MFMA operand reads bank-conflict free and keeps every operand
+//    address a per-lane base plus an immediate offset.
+//  * Online softmax with a lazy rescale: the running max used for the
+//    exponentials is only raised when a tile's max exceeds it by more than
+//    kRescaleSlack (base-2 units).  Exponentials then stay <= 2^kRescaleSlack,
+//    and the final normalisation uses the same stale max, so the result is
+//    the exact softmax.
+//  * Split-k over the top-k slots (decode) writes normalised fp32 partial
+//    outputs plus their base-2 LSE; sfa::launch_combine merges them.
+//
+// MFMA register layouts used (gfx950, bf16, 8 values per lane; T = 16 or 32):
+//   A[m][k]: lane l holds m = l % T, k = 8*(l / T) + j        (j = 0..7)
+//   B[k][n]: lane l holds n = l % T, k = 8*(l / T) + j
+//   C[m][n]: lane l holds n = l % T, m = 4*LG*(e/4) + 4*(l/T) + e%4,
+//            e = 0..T*T/64-1, LG = 64/T.
+
+#include <type_traits>
+
+#include "sfa_common.h"
+
+namespace sfa {
+namespace {
+
+constexpr float kRescaleSlack = 8.0f;
+constexpr int kIdxCap = 2048;  // slots staged in LDS per work item
+#ifndef MLA_QREG
+#define MLA_QREG 18
+#endif
+
+template <int T_, int DQK_, int DV_, int NSLICE_, int NSPLITW_, bool VK_, int QREG_>
+struct FwdCfg {
+  static constexpr int T = T_;
+  static constexpr int DQK = DQK_;
+  static constexpr int DV = DV_;
+  static constexpr int NSLICE = NSLICE_;
+  static constexpr int NSPLITW = NSPLITW_;
+  static constexpr bool VK = VK_;           // v rows are the first DV dims of the k rows
+  static constexpr int kWaves = NSLICE * NSPLITW;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int LG = 64 / T;         // lane groups
+  static constexpr int KD = 8 * LG;         // MFMA contraction length
+  static constexpr int CPL = T * T / 64;    // accumulator values per lane
+  static constexpr int MT = 32 / T;         // S^T MFMA tiles per 32-key wave tile
+  static constexpr int NKT = 32 * NSPLITW;  // keys per workgroup tile
+  static constexpr int QSTEPS = DQK / KD;
+  static constexpr int QREG = QREG_;        // contraction steps whose Q^T operand stays in VGPRs
+  static constexpr int QL = QSTEPS - QREG;  // steps whose Q^T operand is read from LDS
+  static constexpr int QLP = QL * LG + 1;   // LDS pitch (16-byte slots) of a head's LDS-resident q dims
+  static constexpr int QBUF = QL > 0 ? NSLICE * T * QLP : 1;
+  static constexpr int OT = DV / T;
+  static constexpr int CHK = DQK / 8;       // 16-byte chunks per k row
+  static constexpr int CHV = DV / 8;
+  static constexpr int PK = CHK + 1;        // LDS row pitch in 16-byte slots (odd)
+  static constexpr int PV = CHV + 1;
+  static constexpr int KBUF = NKT * PK;     // 16-byte slots per k tile
+  static constexpr int VBUF = VK ? 0 : NKT * PV;
+  static constexpr int GK = (KBUF + kThreads - 1) / kThreads;  // gather instructions per thread (k)
+  static constexpr int GV = (VBUF + kThreads - 1) / kThreads;  // gather instructions per thread (v)
+  static_assert(DQK % KD == 0 && DV % T == 0, "head dims must tile the MFMA");
+  static_assert(!VK || DV <= DQK, "v must be a prefix of k");
+  static_assert(CHK % 2 == 0 && CHV % 2 == 0, "rows need an even number of 16-byte chunks");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+template <int T>
+struct Mfma;
+
+template <>
+struct Mfma<32> {
+  typedef f32x16 acc_t;
+  static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // Accumulate into an AGPR-resident accumulator.  Written as inline asm so
+  // the O^T accumulators (256 registers per lane) are pinned to the AGPR file
+  // while the S^T MFMAs keep theirs in VGPRs.  The leading s_nop provides the
+  // 2 wait states a VALU write of srcA/srcB needs before an MFMA reads it
+  // (the compiler does not model hazards inside inline asm).
+  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+  // c *= s on an AGPR-resident accumulator without moving it to VGPRs.
+  static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float x = c[e];
+      float tmp;
+      asm volatile(
+          "v_accvgpr_read_b32 %1, %0\n\t"
+          "v_mul_f32 %1, %1, %2\n\t"
+          "v_accvgpr_write_b32 %0, %1"
+          : "+a"(x), "=&v"(tmp)
+          : "v"(s));
+      c[e] = x;
+    }
+  }
+  // Wait states between the last asm MFMA writing `c` and any later read of it
+  // (an XDL result needs up to 18 before VALU reads; 3 x 8 + margin).
+  static __device__ __forceinline__ void drain(acc_t& c) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(c));
+  }
+};
+
+template <>
+struct Mfma<16> {
+  typedef f32x4 acc_t;
+  static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c) { c = mma(a, b, c); }
+  static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) { c *= s; }
+  static __device__ __forceinline__ void drain(acc_t&) {}
+};
+
+// LDS reads through pointers derived from the __shared__ arrays themselves, so
+// the compiler keeps per-array alias information and does not make the reads
+// of one tile buffer wait for the DMA still filling the other.
+__device__ __forceinline__ bf16x8 lds_read_b128(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+__device__ __forceinline__ bf16x4 lds_read_tr16(const void* base, uint32_t byte_off) {
+  typedef __attribute__((address_space(3))) const char lds_cchar;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (lds_bf16x4*)((lds_cchar*)(base) + byte_off));
+}
+
+template <class C>
+__global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
+  constexpr int T = C::T;
+  using M = Mfma<T>;
+  typedef typename M::acc_t acc_t;
+
+  __shared__ int s_idx[kIdxCap];
+  __shared__ u32x4 s_k0[C::KBUF];
+  __shared__ u32x4 s_k1[C::KBUF];
+  __shared__ u32x4 s_v0[C::VK ? 1 : C::VBUF];
+  __shared__ u32x4 s_v1[C::VK ? 1 : C::VBUF];
+  __shared__ u32x4 s_q[C::QBUF];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slice = wave % C::NSLICE;
+  const int ks = wave / C::NSLICE;
+
+  // ---- work item -------------------------------------------------------
+  int wi = blockIdx.x;
+  const int split = wi % p.num_splits;
+  wi /= p.num_splits;
+  const int g = wi % p.Hkv;
+  wi /= p.Hkv;
+  const int t = wi % p.Sq;
+  const int b = wi / p.Sq;
+  const int slot0 = split * p.split_len;
+  int nslots = p.topk - slot0;
+  if (nslots > p.split_len) nslots = p.split_len;
+  if (nslots < 0) nslots = 0;
+  const int ntiles = (nslots + C::NKT - 1) / C::NKT;
+
+  // ---- stage indices (invalid -> -1) --------------------------------------
+  {
+    const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
+    const int bound = bound_of(p, b);
+    for (int i = tid; i < ntiles * C::NKT; i += C::kThreads) {
+      const int id = (i < nslots) ? irow[i] : -1;
+      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
+    }
+  }
+
+  // ---- Q^T B operands in registers ------------------------------------
+  const int hl = slice * T + (lane % T);  // head within the group
+  const bool hvalid = hl < p.G;
+  bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
+  {
+    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
+                       (int64_t)(g * p.G + (hvalid ? hl : 0)) * p.q_sh + 8 * (lane / T);
+#pragma unroll
+    for (int s = 0; s < C::QREG; ++s) {
+      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + s * C::KD);
+      if (!hvalid) x = bf16x8{};
+      qb[s] = x;
+    }
+    // the remaining steps' operands go to LDS: head hl's row holds its chunks
+    // (step s, lane group j) at slot (s - QREG) * LG + j
+#pragma unroll
+    for (int s = C::QREG; s < C::QSTEPS; ++s) {
+      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + s * C::KD);
+      if (!hvalid) x = bf16x8{};
+      *reinterpret_cast<bf16x8*>(&s_q[hl * C::QLP + (s - C::QREG) * C::LG + lane / T]) = x;
+    }
+  }
+
+  // ---- gather setup --------------------------------------------------------
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
+  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
+  const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
+
+  // Slot u of a tile holds 16-byte chunk (u % pitch) of row u / pitch; the pad
+  // slot of each row (chunk == CH) is loaded from an out-of-range offset (0).
+  // Thread tid owns slots tid, tid + kThreads, ...: its (row, chunk) walk is
+  // advanced incrementally from two registers made opaque per call, so the
+  // compiler cannot hoist one offset per instruction out of the tile loop.
+  auto gather_rows = [&](const int* ib, u32x4* dst, const __amdgpu_buffer_rsrc_t& rs, uint32_t row_bytes,
+                         auto pitch_c, auto ch_c) {
+    constexpr int PITCH = decltype(pitch_c)::value;
+    constexpr int CH = decltype(ch_c)::value;
+    constexpr int NSLOT = C::NKT * PITCH;
+    constexpr int NIT = (NSLOT + C::kThreads - 1) / C::kThreads;
+    constexpr int DR = C::kThreads / PITCH, DC = C::kThreads % PITCH;
+    int r = tid / PITCH, c = tid - (tid / PITCH) * PITCH;
+    asm volatile("" : "+v"(r), "+v"(c));
+    int ids[NIT], cs[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const bool live = (NSLOT % C::kThreads == 0) || (it * C::kThreads + tid < NSLOT);
+      ids[it] = live ? ib[r] : -1;
+      cs[it] = c;
+      c += DC;
+      r += DR;
+      if (c >= PITCH) {
+        c -= PITCH;
+        r += 1;
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      if ((NSLOT % C::kThreads == 0) || (it * C::kThreads + tid < NSLOT)) {
+        const uint32_t off = (ids[it] >= 0 && cs[it] < CH)
+                                 ? __umul24((uint32_t)ids[it], row_bytes) + (uint32_t)cs[it] * 16u
+                                 : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + it * C::kThreads + wave * 64), 16, off, 0, 0,
+                                                 0);
+      }
+    }
+  };
+  auto gather = [&](int tile, u32x4* kdst, u32x4* vdst) {
+    const int* ib = s_idx + tile * C::NKT;
+    gather_rows(ib, kdst, rk, krow_bytes, std::integral_constant<int, C::PK>{}, std::integral_constant<int, C::CHK>{});
+    if constexpr (!C::VK)
+      gather_rows(ib, vdst, rv, vrow_bytes, std::integral_constant<int, C::PV>{},
+                  std::integral_constant<int, C::CHV>{});
+  };
+
+  // ---- accumulators ----------------------------------------------------
+  acc_t oacc[C::OT];
+#pragma unroll
+  for (int i = 0; i < C::OT; ++i) oacc[i] = acc_t{};
+  float m_used = kNegInf;  // running max (base 2) the exponentials are taken against
+  float l_part = 0.f;      // this lane's share of the row sum
+
+  const int hq = lane / T;  // lane group: which k-slice of the MFMA operands
+  const int lt = lane % T;
+
+  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt) {
+    // validity of this wave's 32 keys
+    const int myid = s_idx[tile * C::NKT + ks * 32 + (lane & 31)];
+    const uint32_t vmask = (uint32_t)__ballot(myid >= 0);
+
+    // S^T = K Q^T
+    acc_t sacc[C::MT];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) sacc[mt] = acc_t{};
+    const uint32_t q_off = (uint32_t)(hl * C::QLP + hq) * 16u;
+#pragma unroll
+    for (int s = 0; s < C::QSTEPS; ++s) {
+      bf16x8 bq;
+      if (s < C::QREG)
+        bq = qb[s < C::QREG ? s : 0];
+      else
+        bq = lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u);
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt) {
+        const int row = ks * 32 + mt * T + lt;
+        const int chunk = s * C::LG + hq;
+        const bf16x8 a = lds_read_b128(kt, (uint32_t)(row * C::PK + chunk) * 16u);
+        sacc[mt] = M::mma(a, bq, sacc[mt]);
+      }
+    }
+
+    // masked scores in base-2 units
+    float sv[C::MT * C::CPL];
+    float tmax = kNegInf;
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) {
+#pragma unroll
+      for (int e = 0; e < C::CPL; ++e) {
+        const int key = mt * T + 4 * C::LG * (e / 4) + 4 * hq + (e % 4);
+        const bool valid = (vmask >> key) & 1u;
+        const float x = valid ? sacc[mt][e] * p.scale_log2 : kNegInf;
+        sv[mt * C::CPL + e] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    }
+#pragma unroll
+    for (int o = T; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+
+    // lazy rescale
+    const float m_new = fmaxf(m_used, tmax);
+    if (__any(m_new > m_used + kRescaleSlack)) {
+      const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_used - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < C::OT; ++i) M::scale_agpr(oacc[i], alpha);
+      m_used = m_new;
+    }
+
+    // P^T (fp32 -> bf16) as the B operand of O^T = V^T P^T
+    constexpr int KSTEPS = (C::MT * C::CPL) / 8;  // O^T contraction steps per 32 keys
+    bf16x8 pb[KSTEPS];
+#pragma unroll
+    for (int i = 0; i < C::MT * C::CPL; ++i) {
+      const float x = sv[i];
+      const float e = (x == kNegInf) ? 0.f : exp2f(x - m_used);
+      l_part += e;
+      pb[i / 8][i % 8] = (bf16)e;
+    }
+
+    // O^T += V^T P^T
+    constexpr int VP = C::VK ? C::PK : C::PV;
+    const int gi = lane & 15;       // lane within its 16-lane transpose group
+    const int rr = gi >> 2;         // row within a run of 4 keys this lane loads
+    const int cc = gi & 3;          // 4-dim column piece this lane loads
+    const int mgrp = (lt >> 4) << 4;  // first MFMA row (dim) of the 16-lane group
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
+      int run0, run1;
+      if constexpr (T == 32) {
+        run0 = 16 * kk + 4 * hq;
+        run1 = 16 * kk + 8 + 4 * hq;
+      } else {
+        run0 = 4 * hq;
+        run1 = 16 + 4 * hq;
+      }
+      const int row0 = ks * 32 + run0 + rr;
+      const int row1 = ks * 32 + run1 + rr;
+#pragma unroll
+      for (int ot = 0; ot < C::OT; ++ot) {
+        const int dim = ot * T + mgrp + 4 * cc;
+        const bf16x4 lo = lds_read_tr16(vt, (uint32_t)(row0 * VP) * 16u + (uint32_t)dim * 2u);
+        const bf16x4 hi = lds_read_tr16(vt, (uint32_t)(row1 * VP) * 16u + (uint32_t)dim * 2u);
+        const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        M::mma_agpr(a, pb[kk], oacc[ot]);
+      }
+    }
+  };
+
+  __syncthreads();  // indices staged
+  if (ntiles > 0) gather(0, s_k0, s_v0);
+  __syncthreads();
+
+  for (int j = 0; j < ntiles; j += 2) {
+    if (j + 1 < ntiles) gather(j + 1, s_k1, s_v1);
+    compute(j, s_k0, C::VK ? s_k0 : s_v0);
+    __syncthreads();
+    if (j + 1 < ntiles) {
+      if (j + 2 < ntiles) gather(j + 2, s_k0, s_v0);
+      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1);
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < C::OT; ++i) M::drain(oacc[i]);
+
+  // ---- finish: row sums over the lane groups sharing a head -------------------
+  float l_sum = l_part;
+#pragma unroll
+  for (int o = T; o < 64; o <<= 1) l_sum += __shfl_xor(l_sum, o, 64);
+
+  float m_fin = m_used;
+  if constexpr (C::NSPLITW > 1) {
+    // merge the key sub-ranges of the waves sharing a head slice (through LDS;
+    // the last barrier of the tile loop ended every use of the tiles)
+    float* s_ml = reinterpret_cast<float*>(s_idx);  // [kWaves][2][T]
+    float* s_o = reinterpret_cast<float*>(s_k0);    // [kWaves][OT*CPL][64]
+    static_assert(2 * C::kWaves * T <= kIdxCap, "merge fits");
+    static_assert(C::kWaves * C::OT * C::CPL * 64 * 4 <= C::KBUF * 16, "merge fits");
+    if (lane < T) {
+      s_ml[(wave * 2 + 0) * T + lane] = m_used;
+      s_ml[(wave * 2 + 1) * T + lane] = l_sum;
+    }
+    __syncthreads();
+    float mm = kNegInf;
+#pragma unroll
+    for (int w = 0; w < C::NSPLITW; ++w) mm = fmaxf(mm, s_ml[((w * C::NSLICE + slice) * 2) * T + lt]);
+    float ltot = 0.f;
+#pragma unroll
+    for (int w = 0; w < C::NSPLITW; ++w) {
+      const float mw = s_ml[((w * C::NSLICE + slice) * 2) * T + lt];
+      const float lw = s_ml[((w * C::NSLICE + slice) * 2 + 1) * T + lt];
+      ltot += (mw == kNegInf) ? 0.f : lw * exp2f(mw - mm);
+    }
+    const float f = (m_used == kNegInf) ? 0.f : exp2f(m_used - mm);
+#pragma unroll
+    for (int i = 0; i < C::OT; ++i) {
+#pragma unroll
+      for (int e = 0; e < C::CPL; ++e) s_o[((wave * C::OT + i) * C::CPL + e) * 64 + lane] = oacc[i][e] * f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < C::OT; ++i) {
+#pragma unroll
+      for (int e = 0; e < C::CPL; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < C::NSPLITW; ++w) acc += s_o[(((w * C::NSLICE + slice) * C::OT + i) * C::CPL + e) * 64 + lane];
+        oacc[i][e] = acc;
+      }
+    }
+    m_fin = mm;
+    l_sum = ltot;
+    // every wave now holds the merged result of its slice; waves ks > 0 stop
+    if (ks != 0) return;
+  }
+
+  if (!hvalid) return;
+  const int h = g * p.G + hl;
+  const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
+  if (p.num_splits > 1) {
+    // normalised partial output and base-2 LSE of this split (no sink: the
+    // combine adds it once)
+    const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+    const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+    float* po = p.part_o + ((int64_t)split * nrows + row) * C::DV;
+#pragma unroll
+    for (int ot = 0; ot < C::OT; ++ot) {
+#pragma unroll
+      for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
+        const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
+        f32x4 v4 = {oacc[ot][4 * q4 + 0] * inv, oacc[ot][4 * q4 + 1] * inv, oacc[ot][4 * q4 + 2] * inv,
+                    oacc[ot][4 * q4 + 3] * inv};
+        *reinterpret_cast<f32x4*>(po + dim) = v4;
+      }
+    }
+    if (hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
+    return;
+  }
+  // final output with the optional sink in the denominator (SFA.py:469-478)
+  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  const float mm = fmaxf(m_fin, sink2);
+  const float fo = (m_fin == kNegInf) ? 0.f : exp2f(m_fin - mm);
+  float lt_ = l_sum * fo;
+  if (p.sink && mm != kNegInf) lt_ += exp2f(sink2 - mm);
+  const float scale_o = lt_ > 0.f ? fo / lt_ : 0.f;
+  bf16* orow = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh;
+#pragma unroll
+  for (int ot = 0; ot < C::OT; ++ot) {
+#pragma unroll
+    for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
+      const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
+      bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
+                   (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
+      *reinterpret_cast<bf16x4*>(orow + dim) = v4;
+    }
+  }
+  if (hq == 0) p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
+}
+
+// Variants: (T, DQK, DV, NSLICE, NSPLITW, V is a prefix of K)
+using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG>;  // DeepSeek MLA: G = 128, d_qk 576 / d_v 512
+using CfgD128G16 = FwdCfg<16, 128, 128, 1, 4, false, 4>;    // d = 128, G <= 16
+
+template <class C>
+hipError_t launch(const Params& p, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
+  hipLaunchKernelGGL(fwd_mfma_kernel<C>, dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+bool v_is_k_prefix(const Params& p) {
+  return p.v == p.k && p.v_sb == p.k_sb && p.v_ss == p.k_ss && p.v_sh == p.k_sh;
+}
+
+bool rows_fit_32bit(const Params& p) {
+  const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
+  const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
+  return kb < (int64_t)kOOB && vb < (int64_t)kOOB;
+}
+
+}  // namespace
+
+int fwd_mfma_tile_keys(const Params& p) {
+  if (p.Dqk == 576 && p.Dv == 512) return CfgMla::NKT;
+  return CfgD128G16::NKT;
+}
+
+bool fwd_mfma_supported(const Params& p) {
+  if (!rows_fit_32bit(p)) return false;
+  if (p.Dqk == 576 && p.Dv == 512 && p.G <= 128 && p.G > 64 && v_is_k_prefix(p)) return true;
+  if (p.Dqk == 128 && p.Dv == 128 && p.G <= 16 && p.G > 4) return true;
+  return false;
+}
+
+hipError_t launch_fwd_mfma(const Params& p, hipStream_t s) {
+  if (p.Dqk == 576 && p.Dv == 512) return launch<CfgMla>(p, s);
+  if (p.Dqk == 128 && p.Dv == 128) return launch<CfgD128G16>(p, s);
+  return hipErrorNotSupported;
+}
+
+}  // namespace sfa

@@ -1,0 +1,335 @@
+// Generic sparse flash attention kernels for any head dim / group size, in
+// float32 or bfloat16.  They are the float32 path (the tiny fp32 workload) and
+// the path for shapes the MFMA kernels do not cover.  One workgroup of 256
+// threads (4 waves) owns one (batch, query, head) row; a wave evaluates one
+// top-k slot at a time with a coalesced dot product over the feature dim.
+//
+// Math (reference SFA.py):  s = scale·<q, k[idx]>, masked to valid slots
+// (SFA.py:392-404, 436); lse = log Σ exp(s) (+ exp(sink), SFA.py:469-474);
+// out = Σ exp(s - lse)·v[idx] (SFA.py:441-480).  Backward: δ = Σ out·dout
+// (SFA.py:590-610); dS = P(dP - δ); dq = scale·Σ dS·k (SFA.py:649-716);
+// dk[idx] += scale·dS·q, dv[idx] += P·dout (SFA.py:757-853, fp32 atomics as
+// SFA.py:853); dsink = -Σ exp(sink - lse)·δ (SFA.py:964-970).
+
+#include "sfa_common.h"
+
+namespace sfa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ float block_reduce_max(float x, float* red) {
+  x = wave_max(x);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__device__ __forceinline__ float block_reduce_sum(float x, float* red) {
+  x = wave_sum(x);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r += red[i];
+  return r;
+}
+
+// Shared memory: q row [Dqk] | per-slot score / probability [topk] | reduce [kWaves]
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fwd_generic_kernel(Params p) {
+  extern __shared__ float smem[];
+  float* qs = smem;
+  float* sc = smem + p.Dqk;
+  float* red = sc + p.topk;
+
+  const int row = blockIdx.x;  // (b, t, h) flattened as ((b*Sq)+t)*Hq+h
+  const int h = row % p.Hq;
+  const int t = (row / p.Hq) % p.Sq;
+  const int b = row / (p.Hq * p.Sq);
+  const int g = h / p.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.q_sb + t * p.q_ss + h * p.q_sh;
+  for (int d = tid; d < p.Dqk; d += kThreads) qs[d] = to_f32(qrow[d]);
+  __syncthreads();
+
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
+  const T* kb = reinterpret_cast<const T*>(p.k) + b * p.k_sb + g * p.k_sh;
+  const T* vb = reinterpret_cast<const T*>(p.v) + b * p.v_sb + g * p.v_sh;
+
+  for (int j = wave; j < p.topk; j += kWaves) {
+    const int id = irow[j];
+    float s = kNegInf;
+    if (id >= 0 && id < bound) {
+      const T* kr = kb + (int64_t)id * p.k_ss;
+      float acc = 0.f;
+      for (int d = lane; d < p.Dqk; d += 64) acc += qs[d] * to_f32(kr[d]);
+      s = wave_sum(acc) * p.scale_log2;
+    }
+    if (lane == 0) sc[j] = s;
+  }
+  __syncthreads();
+
+  float m = kNegInf;
+  for (int j = tid; j < p.topk; j += kThreads) m = fmaxf(m, sc[j]);
+  m = block_reduce_max(m, red);
+  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  const float mm = fmaxf(m, sink2);
+
+  float l = 0.f;
+  for (int j = tid; j < p.topk; j += kThreads) {
+    const float s = sc[j];
+    const float e = (s == kNegInf) ? 0.f : exp2f(s - mm);
+    sc[j] = e;
+    l += e;
+  }
+  l = block_reduce_sum(l, red);  // contains the barrier that publishes sc[]
+  if (p.sink && mm != kNegInf) l += exp2f(sink2 - mm);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
+  for (int d = tid; d < p.Dv; d += kThreads) {
+    float acc = 0.f;
+    for (int j = 0; j < p.topk; ++j) {
+      const float e = sc[j];
+      if (e != 0.f) acc += e * to_f32(vb[(int64_t)irow[j] * p.v_ss + d]);
+    }
+    orow[d] = from_f32<T>(acc * inv);
+  }
+  if (tid == 0) {
+    p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
+  }
+}
+
+// δ = Σ_d out·dout per (b, t, h) row (SFA.py:590-610), minus dlse when a
+// gradient reaches the returned lse.  One wave per row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void delta_kernel(Params p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  if (row >= nrows) return;
+  const int h = row % p.Hq;
+  const int t = (row / p.Hq) % p.Sq;
+  const int b = row / ((int64_t)p.Hq * p.Sq);
+  const T* o = reinterpret_cast<const T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
+  const T* d = reinterpret_cast<const T*>(p.dout) + b * p.do_sb + t * p.do_ss + h * p.do_sh;
+  float acc = 0.f;
+  for (int i = lane; i < p.Dv; i += 64) acc += to_f32(o[i]) * to_f32(d[i]);
+  acc = wave_sum(acc);
+  // a gradient flowing into lse adds P·dlse to dS = P(dP - δ): fold it into δ
+  if (p.dlse) acc -= p.dlse[b * p.l_sb + t * p.l_ss + h * p.l_sh];
+  if (lane == 0) p.delta[row] = acc;
+}
+
+// Shared memory: q row [Dqk] | dout row [Dv] | per-wave dq partial [kWaves][Dqk]
+template <typename T>
+__global__ __launch_bounds__(kThreads) void bwd_generic_kernel(Params p) {
+  extern __shared__ float smem[];
+  float* qs = smem;
+  float* dos = qs + p.Dqk;
+  float* dqw = dos + p.Dv;
+
+  const int row = blockIdx.x;
+  const int h = row % p.Hq;
+  const int t = (row / p.Hq) % p.Sq;
+  const int b = row / (p.Hq * p.Sq);
+  const int g = h / p.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  const T* qrow = reinterpret_cast<const T*>(p.q) + b * p.q_sb + t * p.q_ss + h * p.q_sh;
+  const T* dorow = reinterpret_cast<const T*>(p.dout) + b * p.do_sb + t * p.do_ss + h * p.do_sh;
+  for (int d = tid; d < p.Dqk; d += kThreads) qs[d] = to_f32(qrow[d]);
+  for (int d = tid; d < p.Dv; d += kThreads) dos[d] = to_f32(dorow[d]);
+  for (int d = tid; d < kWaves * p.Dqk; d += kThreads) dqw[d] = 0.f;
+  __syncthreads();
+
+  const float lse = p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh];
+  const float delta = p.delta[row];
+  T* dqrow = reinterpret_cast<T*>(p.dq) + b * p.dq_sb + t * p.dq_ss + h * p.dq_sh;
+  if (lse == kNegInf) {  // no valid slot and no sink: every gradient of this row is 0
+    for (int d = tid; d < p.Dqk; d += kThreads) dqrow[d] = from_f32<T>(0.f);
+    return;
+  }
+  const float lse2 = lse * kLog2e;
+  if (p.sink && tid == 0) atomicAdd(&p.dsink[h], -exp2f(p.sink[h] * kLog2e - lse2) * delta);
+
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
+  const T* kb = reinterpret_cast<const T*>(p.k) + b * p.k_sb + g * p.k_sh;
+  const T* vb = reinterpret_cast<const T*>(p.v) + b * p.v_sb + g * p.v_sh;
+  const int64_t acc_row_k = (int64_t)p.Hkv * p.Dqk, acc_row_v = (int64_t)p.Hkv * p.Dv;
+  float* dkb = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * p.Dqk;
+  float* dvb = p.dv_acc + ((int64_t)b * p.Skv * p.Hkv + g) * p.Dv;
+  float* mydq = dqw + wave * p.Dqk;
+
+  for (int j = wave; j < p.topk; j += kWaves) {
+    const int id = irow[j];
+    if (id < 0 || id >= bound) continue;  // wave-uniform
+    const T* kr = kb + (int64_t)id * p.k_ss;
+    const T* vr = vb + (int64_t)id * p.v_ss;
+    float s = 0.f, dp = 0.f;
+    for (int d = lane; d < p.Dqk; d += 64) s += qs[d] * to_f32(kr[d]);
+    for (int d = lane; d < p.Dv; d += 64) dp += dos[d] * to_f32(vr[d]);
+    s = wave_sum(s);
+    dp = wave_sum(dp);
+    const float pr = exp2f(s * p.scale_log2 - lse2);
+    const float ds = pr * (dp - delta);
+    const float sds = p.scale * ds;
+    float* dkr = dkb + (int64_t)id * acc_row_k;
+    float* dvr = dvb + (int64_t)id * acc_row_v;
+    for (int d = lane; d < p.Dqk; d += 64) {
+      mydq[d] += sds * to_f32(kr[d]);
+      atomicAdd(&dkr[d], sds * qs[d]);
+    }
+    for (int d = lane; d < p.Dv; d += 64) atomicAdd(&dvr[d], pr * dos[d]);
+  }
+  __syncthreads();
+  for (int d = tid; d < p.Dqk; d += kThreads) {
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) acc += dqw[w * p.Dqk + d];
+    dqrow[d] = from_f32<T>(acc);
+  }
+}
+
+__global__ void zero_f32_kernel(float* ptr, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) ptr[i] = 0.f;
+}
+
+// fp32 accumulators [B, Skv, Hkv, D] -> output tensor with caller strides.
+template <typename T>
+__global__ void finish_kernel(const float* acc, int B, int Skv, int Hkv, int D, T* out, int64_t sb, int64_t ss,
+                              int64_t sh) {
+  const int64_t n = (int64_t)B * Skv * Hkv * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int d = i % D;
+    const int64_t r = i / D;
+    const int h = r % Hkv;
+    const int s = (r / Hkv) % Skv;
+    const int b = r / ((int64_t)Hkv * Skv);
+    out[b * sb + s * ss + h * sh + d] = from_f32<T>(acc[i]);
+  }
+}
+
+// Split-k combine: lse2 = log2 Σ_s 2^lse2_s, out = Σ_s 2^(lse2_s - lse2)·o_s,
+// then the optional sink joins the denominator.  One wave per (b, t, h) row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  if (row >= nrows) return;
+  const int h = row % p.Hq;
+  const int t = (row / p.Hq) % p.Sq;
+  const int b = row / ((int64_t)p.Hq * p.Sq);
+  float m = kNegInf;
+  for (int s = 0; s < p.num_splits; ++s) m = fmaxf(m, p.part_lse[s * nrows + row]);
+  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  const float mm = fmaxf(m, sink2);
+  float l = 0.f;
+  if (mm != kNegInf) {
+    for (int s = 0; s < p.num_splits; ++s) {
+      const float ls = p.part_lse[s * nrows + row];
+      l += (ls == kNegInf) ? 0.f : exp2f(ls - mm);
+    }
+    if (p.sink) l += exp2f(sink2 - mm);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
+  for (int d = lane; d < p.Dv; d += 64) {
+    float acc = 0.f;
+    for (int s = 0; s < p.num_splits; ++s) {
+      const float ls = p.part_lse[s * nrows + row];
+      if (ls != kNegInf) acc += exp2f(ls - mm) * p.part_o[(s * nrows + row) * p.Dv + d];
+    }
+    orow[d] = from_f32<T>(acc * inv);
+  }
+  if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
+}
+
+inline int grid_for(int64_t n, int threads) {
+  int64_t g = (n + threads - 1) / threads;
+  if (g > 65535 * 16) g = 65535 * 16;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+}  // namespace
+
+hipError_t launch_fwd_generic(const Params& p, int dtype, hipStream_t s) {
+  const size_t sh = sizeof(float) * ((size_t)p.Dqk + p.topk + kWaves);
+  const dim3 grid((unsigned)((int64_t)p.B * p.Sq * p.Hq));
+  if (dtype == SFA_DTYPE_F32)
+    hipLaunchKernelGGL(fwd_generic_kernel<float>, grid, dim3(kThreads), sh, s, p);
+  else
+    hipLaunchKernelGGL(fwd_generic_kernel<bf16>, grid, dim3(kThreads), sh, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s) {
+  const int64_t rows = (int64_t)p.B * p.Sq * p.Hq;
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (dtype == SFA_DTYPE_F32)
+    hipLaunchKernelGGL(delta_kernel<float>, grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(delta_kernel<bf16>, grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_generic(const Params& p, int dtype, hipStream_t s) {
+  const size_t sh = sizeof(float) * ((size_t)p.Dqk + p.Dv + (size_t)kWaves * p.Dqk);
+  const dim3 grid((unsigned)((int64_t)p.B * p.Sq * p.Hq));
+  if (dtype == SFA_DTYPE_F32)
+    hipLaunchKernelGGL(bwd_generic_kernel<float>, grid, dim3(kThreads), sh, s, p);
+  else
+    hipLaunchKernelGGL(bwd_generic_kernel<bf16>, grid, dim3(kThreads), sh, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_f32(float* ptr, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_for((int64_t)n, 256 * 4)), dim3(256), 0, s, ptr, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss, int64_t dk_sh,
+                             void* dv, int64_t dv_sb, int64_t dv_ss, int64_t dv_sh, hipStream_t s) {
+  const int64_t nk = (int64_t)p.B * p.Skv * p.Hkv * p.Dqk, nv = (int64_t)p.B * p.Skv * p.Hkv * p.Dv;
+  if (dtype == SFA_DTYPE_F32) {
+    hipLaunchKernelGGL(finish_kernel<float>, dim3(grid_for(nk, 256 * 4)), dim3(256), 0, s, p.dk_acc, p.B, p.Skv,
+                       p.Hkv, p.Dqk, (float*)dk, dk_sb, dk_ss, dk_sh);
+    hipLaunchKernelGGL(finish_kernel<float>, dim3(grid_for(nv, 256 * 4)), dim3(256), 0, s, p.dv_acc, p.B, p.Skv,
+                       p.Hkv, p.Dv, (float*)dv, dv_sb, dv_ss, dv_sh);
+  } else {
+    hipLaunchKernelGGL(finish_kernel<bf16>, dim3(grid_for(nk, 256 * 4)), dim3(256), 0, s, p.dk_acc, p.B, p.Skv,
+                       p.Hkv, p.Dqk, (bf16*)dk, dk_sb, dk_ss, dk_sh);
+    hipLaunchKernelGGL(finish_kernel<bf16>, dim3(grid_for(nv, 256 * 4)), dim3(256), 0, s, p.dv_acc, p.B, p.Skv,
+                       p.Hkv, p.Dv, (bf16*)dv, dv_sb, dv_ss, dv_sh);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const Params& p, int dtype, hipStream_t s) {
+  const int64_t rows = (int64_t)p.B * p.Sq * p.Hq;
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (dtype == SFA_DTYPE_F32)
+    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace sfa

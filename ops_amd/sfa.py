@@ -1,0 +1,215 @@
+"""Top-k sparse flash attention on MI355X: the drop-in host layer.
+
+Reference: ``SparseFlashAttentionTriton`` (lilac-me/ops SFA.py:69-306), an
+autograd Function whose forward launches ``_attn_fwd`` and whose backward
+launches ``_attn_bwd_dq_dsink`` and ``_attn_bwd_dk_dv``.  This module keeps
+that role and calls the HIP kernels of ``libsfa.so`` through its C ABI
+(``include/sfa.h``) on torch's current stream:
+
+``SparseFlashAttention.apply(q, k, v, topk_idxs, sm_scale, kv_lens, attn_sink)``
+    -> ``(out, lse)``; backward returns ``dq, dk, dv`` (and ``dsink``).
+
+Layout is BSHD: q ``[B, Sq, Hq, Dqk]``, k ``[B, Skv, Hkv, Dqk]``,
+v ``[B, Skv, Hkv, Dv]`` (``v`` may be a view of ``k``, e.g. MLA's
+``kv[..., :512]``), topk_idxs ``[B, Sq, Hkv, K]`` int32 with -1 padding,
+``lse`` float32 natural log ``[B, Sq, Hq]``.  Query head ``h`` reads KV head
+``h // (Hq // Hkv)``.  A slot is valid iff ``0 <= idx < kv_lens[b]`` (or
+``Skv``); invalid slots contribute nothing, at any slot position.
+
+Error behaviour follows the reference: an empty index tensor or a
+non-positive top-k raises ``ValueError`` (SFA.py:52-53, 63-64); this layer
+also raises ``ValueError`` for device/dtype/shape mismatches the reference
+leaves unchecked.  There is no host synchronisation (the reference's
+``_effective_topk`` ``.item()``, SFA.py:62-66, is replaced by device-side
+masking of every slot), so the op can be captured in a HIP graph.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward"]
+
+_DTYPES = {torch.float32: _lib.SFA_DTYPE_F32, torch.bfloat16: _lib.SFA_DTYPE_BF16}
+_DKV_MODES = {"auto": _lib.SFA_DKV_AUTO, "atomic": _lib.SFA_DKV_ATOMIC, "csr": _lib.SFA_DKV_CSR}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """The kernels need a unit stride on the feature dimension."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _validate(q, k, v, idx, kv_lens, sink):
+    if idx.numel() == 0:  # SFA.py:63-64
+        raise ValueError("topk_idxs tensor is empty. Cannot determine effective topk.")
+    for name, t in (("q", q), ("k", k), ("v", v), ("topk_idxs", idx)):
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4-D (BSHD), got shape {tuple(t.shape)}")
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
+    if not (q.device == k.device == v.device == idx.device):
+        raise ValueError("q, k, v, topk_idxs must be on the same device")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {q.dtype}; expected bfloat16 or float32")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share one dtype")
+    B, Sq, Hq, Dqk = q.shape
+    Bk, Skv, Hkv, Dk = k.shape
+    if Bk != B or Dk != Dqk:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if tuple(v.shape[:3]) != (B, Skv, Hkv):
+        raise ValueError(f"v shape {tuple(v.shape)} does not match k {tuple(k.shape)}")
+    if Hq % Hkv != 0:
+        raise ValueError(f"Hq ({Hq}) must be a multiple of Hkv ({Hkv})")
+    if tuple(idx.shape[:3]) != (B, Sq, Hkv):
+        raise ValueError(f"topk_idxs must be [B, Sq, Hkv, K] = [{B}, {Sq}, {Hkv}, K], got {tuple(idx.shape)}")
+    if idx.shape[3] <= 0:  # SFA.py:52-53
+        raise ValueError(f"Unsupported topk value: {idx.shape[3]}. Please make sure it is a positive integer.")
+    if kv_lens is not None and (kv_lens.numel() != B or kv_lens.device != q.device):
+        raise ValueError("kv_lens must be a [B] tensor on q's device")
+    if sink is not None and (sink.numel() != Hq or sink.device != q.device):
+        raise ValueError("attn_sink must be a [Hq] tensor on q's device")
+
+
+def _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits) -> _lib.FwdArgs:
+    B, Sq, Hq, Dqk = q.shape
+    _, Skv, Hkv, _ = k.shape
+    a = _lib.FwdArgs()
+    a.dtype = _DTYPES[q.dtype]
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv = B, Sq, Skv, Hq, Hkv
+    a.Dqk, a.Dv, a.topk = Dqk, v.shape[3], idx.shape[3]
+    a.scale = float(scale)
+    a.q, (a.q_sb, a.q_ss, a.q_sh) = q.data_ptr(), q.stride()[:3]
+    a.k, (a.k_sb, a.k_ss, a.k_sh) = k.data_ptr(), k.stride()[:3]
+    a.v, (a.v_sb, a.v_ss, a.v_sh) = v.data_ptr(), v.stride()[:3]
+    a.idx, (a.i_sb, a.i_ss, a.i_sh) = idx.data_ptr(), idx.stride()[:3]
+    a.kv_lens = kv_lens.data_ptr() if kv_lens is not None else None
+    a.sink = sink.data_ptr() if sink is not None else None
+    a.out, (a.o_sb, a.o_ss, a.o_sh) = out.data_ptr(), out.stride()[:3]
+    a.lse, (a.l_sb, a.l_ss, a.l_sh) = lse.data_ptr(), lse.stride()
+    a.num_splits = int(num_splits)
+    a.flags = 0
+    return a
+
+
+def _prep(q, k, v, topk_idxs, kv_lens, sink):
+    _validate(q, k, v, topk_idxs, kv_lens, sink)
+    q, k, v = _rows(q), _rows(k), _rows(v)
+    idx = topk_idxs
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+    if kv_lens is not None:
+        kv_lens = kv_lens.to(torch.int32).contiguous()
+    if sink is not None:
+        sink = sink.to(torch.float32).contiguous()
+    return q, k, v, idx, kv_lens, sink
+
+
+def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None, num_splits: int = 0,
+                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    """Forward only (no autograd): ``(out, lse)``.  ``out``/``lse`` may be
+    preallocated ([B, Sq, Hq, Dv] in q's dtype / [B, Sq, Hq] float32)."""
+    lib = _lib.load()
+    q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
+    B, Sq, Hq, Dqk = q.shape
+    Dv = v.shape[3]
+    scale = (1.0 / math.sqrt(Dqk)) if sm_scale is None else float(sm_scale)
+    if out is None:
+        out = torch.empty((B, Sq, Hq, Dv), dtype=q.dtype, device=q.device)
+    if lse is None:
+        lse = torch.empty((B, Sq, Hq), dtype=torch.float32, device=q.device)
+    a = _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits)
+    ws = lib.sfa_fwd_workspace_size(ctypes.byref(a))
+    wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.sfa_fwd(ctypes.byref(a), _ptr(wbuf), ws, ctypes.c_void_p(stream)))
+    return out, lse
+
+
+def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None, attn_sink=None,
+                 dlse: Optional[torch.Tensor] = None, dkv_mode: Optional[str] = None):
+    """Backward only (no autograd): ``(dq, dk, dv, dsink)``; ``dsink`` is None
+    without a sink."""
+    lib = _lib.load()
+    q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
+    B, Sq, Hq, Dqk = q.shape
+    _, Skv, Hkv, _ = k.shape
+    Dv = v.shape[3]
+    if tuple(dout.shape) != (B, Sq, Hq, Dv) or tuple(out.shape) != (B, Sq, Hq, Dv):
+        raise ValueError("out / grad_out must be [B, Sq, Hq, Dv]")
+    dout = _rows(dout.to(q.dtype))
+    out = _rows(out)
+    lse = lse.contiguous()
+    scale = (1.0 / math.sqrt(Dqk)) if sm_scale is None else float(sm_scale)
+    mode = dkv_mode or os.environ.get("SFA_DKV_MODE", "auto")
+    if mode not in _DKV_MODES:
+        raise ValueError(f"dkv_mode must be one of {sorted(_DKV_MODES)}")
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty((B, Skv, Hkv, Dqk), dtype=q.dtype, device=q.device)
+    dv = torch.empty((B, Skv, Hkv, Dv), dtype=q.dtype, device=q.device)
+    dsink = torch.empty((Hq,), dtype=torch.float32, device=q.device) if sink is not None else None
+    if dlse is not None:
+        dlse = dlse.to(torch.float32).contiguous()
+    a = _lib.BwdArgs()
+    a.fwd = _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, 0)
+    a.dout, (a.do_sb, a.do_ss, a.do_sh) = dout.data_ptr(), dout.stride()[:3]
+    a.dq, (a.dq_sb, a.dq_ss, a.dq_sh) = dq.data_ptr(), dq.stride()[:3]
+    a.dk, (a.dk_sb, a.dk_ss, a.dk_sh) = dk.data_ptr(), dk.stride()[:3]
+    a.dv, (a.dv_sb, a.dv_ss, a.dv_sh) = dv.data_ptr(), dv.stride()[:3]
+    a.dlse = dlse.data_ptr() if dlse is not None else None
+    a.dsink = dsink.data_ptr() if dsink is not None else None
+    a.dkv_mode = _DKV_MODES[mode]
+    a.flags = 0
+    ws = lib.sfa_bwd_workspace_size(ctypes.byref(a))
+    wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.sfa_bwd(ctypes.byref(a), _ptr(wbuf), ws, ctypes.c_void_p(stream)))
+    return dq, dk, dv, dsink
+
+
+class SparseFlashAttention(torch.autograd.Function):
+    """Autograd Function: ``apply(q, k, v, topk_idxs, sm_scale=None,
+    kv_lens=None, attn_sink=None) -> (out, lse)``.
+
+    Mirrors ``SparseFlashAttentionTriton`` (SFA.py:69-306) with the BSHD
+    q/k/v API; ``sm_scale=None`` means ``1/sqrt(Dqk)`` in both directions
+    (SFA.py:181-182).  The backward returns gradients for q, k, v and the
+    sink; gradients reaching ``lse`` are honoured.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None):
+        out, lse = sfa_forward(q, k, v, topk_idxs, sm_scale, kv_lens, attn_sink)
+        ctx.save_for_backward(q, k, v, topk_idxs, out, lse, kv_lens, attn_sink)
+        ctx.sm_scale = sm_scale
+        ctx.mark_non_differentiable()
+        ctx.set_materialize_grads(False)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_lse):
+        q, k, v, idx, out, lse, kv_lens, sink = ctx.saved_tensors
+        if grad_out is None:
+            grad_out = torch.zeros_like(out)
+        dq, dk, dv, dsink = sfa_backward(q, k, v, idx, out, lse, grad_out, ctx.sm_scale, kv_lens, sink,
+                                         dlse=grad_lse)
+        if dsink is not None and sink is not None:
+            dsink = dsink.to(sink.dtype)
+        return dq, dk, dv, None, None, None, dsink
+
+
+def sparse_flash_attention(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Functional form of :class:`SparseFlashAttention`."""
+    return SparseFlashAttention.apply(q, k, v, topk_idxs, sm_scale, kv_lens, attn_sink)

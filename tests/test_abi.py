@@ -1,0 +1,121 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol
+include/sfa.h declares, its argument structs match the header byte for byte,
+and invalid arguments come back as error codes (no HIP call is made before
+validation)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from ops_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sfa.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"SFA_API\s+[\w\s\*]+?\b(sfa_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_symbols():
+    assert _declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.lib_path())], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    for name in _declared_functions():
+        assert name in exported, name
+        assert hasattr(lib, name)
+    assert lib.sfa_abi_version() == _lib.SFA_ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    fields_f = [f for f, _ in _lib.FwdArgs._fields_]
+    fields_b = [f for f, _ in _lib.BwdArgs._fields_]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
+             'printf("%zu %zu\\n", sizeof(sfa_fwd_args), sizeof(sfa_bwd_args));']
+    lines += [f'printf("%zu\\n", offsetof(sfa_fwd_args, {f}));' for f in fields_f]
+    lines += [f'printf("%zu\\n", offsetof(sfa_bwd_args, {f}));' for f in fields_b]
+    lines += ["return 0; }"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    vals = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert int(vals[0]) == ctypes.sizeof(_lib.FwdArgs)
+    assert int(vals[1]) == ctypes.sizeof(_lib.BwdArgs)
+    offs = [int(x) for x in vals[2:]]
+    py = [getattr(_lib.FwdArgs, f).offset for f in fields_f] + [getattr(_lib.BwdArgs, f).offset for f in fields_b]
+    assert offs == py
+
+
+def _valid_args():
+    a = _lib.FwdArgs()
+    a.dtype = _lib.SFA_DTYPE_BF16
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = 1, 4, 8, 16, 1, 128, 128, 32
+    a.scale = 0.0
+    for name in ("q", "k", "v", "idx", "out", "lse"):
+        setattr(a, name, 0x10000)
+    return a
+
+
+@pytest.mark.parametrize("field,value", [
+    ("topk", 0), ("topk", -3), ("Hkv", 3), ("B", 0), ("Dqk", 0), ("Dqk", 5000), ("dtype", 7), ("num_splits", -1),
+    ("flags", 1), ("q", None),
+])
+def test_invalid_arguments_are_rejected(field, value):
+    lib = _lib.load()
+    a = _valid_args()
+    setattr(a, field, value)
+    rc = lib.sfa_fwd(ctypes.byref(a), None, 0, None)
+    assert rc == _lib.SFA_E_INVALID
+    assert lib.sfa_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 0
+
+
+def test_null_struct_is_rejected():
+    lib = _lib.load()
+    assert lib.sfa_fwd(None, None, 0, None) == _lib.SFA_E_INVALID
+    assert lib.sfa_bwd(None, None, 0, None) == _lib.SFA_E_INVALID
+
+
+def test_workspace_sizes_follow_the_plan():
+    lib = _lib.load()
+    a = _valid_args()
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 0  # generic / not split
+    # decode-shaped MLA: split-k partials (fp32 O + LSE per split)
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = 64, 1, 65536, 128, 1, 576, 512, 2048
+    a.k_ss = a.v_ss = 576
+    a.k_sh = a.v_sh = 576
+    a.k_sb = a.v_sb = 65536 * 576
+    a.q_sh, a.q_ss, a.q_sb = 576, 128 * 576, 128 * 576
+    a.o_sh, a.o_ss, a.o_sb = 512, 128 * 512, 128 * 512
+    a.v = a.k
+    ws = lib.sfa_fwd_workspace_size(ctypes.byref(a))
+    splits = ws // (64 * 128 * 512 * 4)
+    assert splits >= 2 and ws >= splits * 64 * 128 * (512 + 1) * 4
+    b = _lib.BwdArgs()
+    b.fwd = _valid_args()
+    need = lib.sfa_bwd_workspace_size(ctypes.byref(b))
+    assert need >= (8 * 128 * 2 + 4 * 16) * 4
+
+
+def test_bwd_rejects_missing_gradients_and_csr_mode():
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.fwd = _valid_args()
+    assert lib.sfa_bwd(ctypes.byref(b), None, 0, None) == _lib.SFA_E_INVALID  # null dq/dk/dv
+    for name in ("dout", "dq", "dk", "dv"):
+        setattr(b, name, 0x10000)
+    b.dkv_mode = 9
+    assert lib.sfa_bwd(ctypes.byref(b), None, 0, None) == _lib.SFA_E_INVALID
+    b.dkv_mode = _lib.SFA_DKV_ATOMIC
+    assert lib.sfa_bwd(ctypes.byref(b), None, 0, None) == _lib.SFA_E_WORKSPACE
