@@ -97,11 +97,17 @@ struct Mfma<32> {
   }
   // Accumulate into an AGPR-resident accumulator.  Written as inline asm so
   // the O^T accumulators (256 registers per lane) are pinned to the AGPR file
-  // while the S^T MFMAs keep theirs in VGPRs.  The leading s_nop provides the
-  // 2 wait states a VALU write of srcA/srcB needs before an MFMA reads it
-  // (the compiler does not model hazards inside inline asm).
+  // while the S^T MFMAs keep theirs in VGPRs.  The compiler does not model
+  // hazards inside inline asm, so the block carries its own wait states: 2
+  // before (a VALU write of srcA/srcB must precede the MFMA read by 2), and 12
+  // after, so no instruction the compiler places next can overwrite srcA/srcB
+  // while the 8-pass MFMA may still be reading them.  The "memory" clobber
+  // keeps the software-pipelined operand loads in program order around it.
   static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c) {
-    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 3"
+                 : "+a"(c)
+                 : "v"(a), "v"(b)
+                 : "memory");
   }
   // c *= s on an AGPR-resident accumulator without moving it to VGPRs.
   static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) {
@@ -343,33 +349,35 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       pb[i / 8][i % 8] = (bf16)e;
     }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
+    // of operand i + PD are issued before MFMA i (software pipeline).
     constexpr int VP = C::VK ? C::PK : C::PV;
-    const int gi = lane & 15;       // lane within its 16-lane transpose group
-    const int rr = gi >> 2;         // row within a run of 4 keys this lane loads
-    const int cc = gi & 3;          // 4-dim column piece this lane loads
+    const int gi = lane & 15;         // lane within its 16-lane transpose group
+    const int rr = gi >> 2;           // row within a run of 4 keys this lane loads
+    const int cc = gi & 3;            // 4-dim column piece this lane loads
     const int mgrp = (lt >> 4) << 4;  // first MFMA row (dim) of the 16-lane group
+    // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
+    const int run0 = (T == 32) ? 4 * hq : 4 * hq;
+    const int run1 = (T == 32) ? 8 + 4 * hq : 16 + 4 * hq;
+    const uint32_t base0 = (uint32_t)((ks * 32 + run0 + rr) * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
+    const uint32_t base1 = (uint32_t)((ks * 32 + run1 + rr) * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
+    auto load_a = [&](int i) -> bf16x8 {
+      const int kk = i / C::OT, ot = i % C::OT;
+      const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot * T) * 2u;  // T == 32 only has kk > 0
+      const bf16x4 lo = lds_read_tr16(vt, base0 + off);
+      const bf16x4 hi = lds_read_tr16(vt, base1 + off);
+      return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    constexpr int NI = KSTEPS * C::OT;
+    constexpr int PD = NI < 3 ? NI : 3;
+    bf16x8 abuf[PD];
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
-      int run0, run1;
-      if constexpr (T == 32) {
-        run0 = 16 * kk + 4 * hq;
-        run1 = 16 * kk + 8 + 4 * hq;
-      } else {
-        run0 = 4 * hq;
-        run1 = 16 + 4 * hq;
-      }
-      const int row0 = ks * 32 + run0 + rr;
-      const int row1 = ks * 32 + run1 + rr;
+    for (int i = 0; i < PD; ++i) abuf[i] = load_a(i);
 #pragma unroll
-      for (int ot = 0; ot < C::OT; ++ot) {
-        const int dim = ot * T + mgrp + 4 * cc;
-        const bf16x4 lo = lds_read_tr16(vt, (uint32_t)(row0 * VP) * 16u + (uint32_t)dim * 2u);
-        const bf16x4 hi = lds_read_tr16(vt, (uint32_t)(row1 * VP) * 16u + (uint32_t)dim * 2u);
-        const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        M::mma_agpr(a, pb[kk], oacc[ot]);
-      }
+    for (int i = 0; i < NI; ++i) {
+      const bf16x8 a = abuf[i % PD];
+      if (i + PD < NI) abuf[i % PD] = load_a(i + PD);
+      M::mma_agpr(a, pb[i / C::OT], oacc[i % C::OT]);
     }
   };
 

@@ -50,6 +50,19 @@ def _check_fwd(out, lse, o_ref, l_ref, rows=None):
     return err_o, err_l
 
 
+_CACHE = {}
+
+
+def _workload(name, **kw):
+    """make_workload on the GPU, cached across tests (the decode KV cache is 4.8 GB)."""
+    key = (name, tuple(sorted(kw.items())))
+    if key not in _CACHE:
+        if len(_CACHE) >= 3:
+            _CACHE.pop(next(iter(_CACHE)))
+        _CACHE[key] = make_workload(name, device=DEV, **kw)
+    return _CACHE[key]
+
+
 def _cpu(w):
     return (w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), None if w.kv_lens is None else w.kv_lens.cpu())
 
@@ -140,7 +153,7 @@ def _decode_compact(w):
 @pytest.mark.parametrize("splits", [0, 1, 2, 4, 8])
 def test_mla_decode_full(splits):
     _say(f"mla_decode bf16 B=64 Skv=65536 Hq=128 K=2048 num_splits={splits}")
-    w = make_workload("mla_decode", device=DEV)
+    w = _workload("mla_decode")
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens, num_splits=splits)
     kg, cidx = _decode_compact(w)
     o_ref, l_ref = ref_forward(w.q.cpu(), kg, kg[..., :512], cidx, w.scale)
@@ -184,8 +197,13 @@ def test_slot_permutation_and_duplicates():
     out0, lse0 = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     perm = torch.randperm(64, device=DEV)
     out1, lse1 = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx[..., perm].contiguous(), w.scale)
-    assert float((out0.float() - out1.float()).abs().max()) <= 1e-2
-    assert float((lse0 - lse1).abs().max()) <= 1e-4
+    # summation order differs, so compare each against the oracle (outputs
+    # are rounded to bf16: the two runs may differ by one bf16 ulp)
+    o_ref, l_ref = ref_forward(w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), w.scale)
+    _check_fwd(out0, lse0, o_ref, l_ref)
+    _check_fwd(out1, lse1, o_ref, l_ref)
+    lse_diff = float((lse0 - lse1).abs().max())
+    assert lse_diff <= 1e-4, lse_diff
     dup = w.idx.clone()
     dup[..., 1] = dup[..., 0]
     out2, lse2 = ops_amd.sfa_forward(w.q, w.k, w.v, dup, w.scale)
@@ -209,8 +227,10 @@ def test_mla_alias_equals_contiguous_copy():
     w = make_workload("mla_prefill", device=DEV, S=96, K=32, Hq=128)
     out0, lse0 = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     out1, lse1 = ops_amd.sfa_forward(w.q, w.k, w.v.contiguous(), w.idx, w.scale)
-    assert float((out0.float() - out1.float()).abs().max()) <= 1e-2
-    assert float((lse0 - lse1).abs().max()) <= 1e-4
+    o_diff = float((out0.float() - out1.float()).abs().max())
+    lse_diff = float((lse0 - lse1).abs().max())
+    assert o_diff <= O_TOL, o_diff
+    assert lse_diff <= 1e-4, lse_diff
 
 
 def test_autograd_function_and_dlse():
