@@ -95,19 +95,46 @@ struct Mfma<32> {
   static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // Accumulate into an AGPR-resident accumulator.  Written as inline asm so
-  // the O^T accumulators (256 registers per lane) are pinned to the AGPR file
-  // while the S^T MFMAs keep theirs in VGPRs.  The compiler does not model
-  // hazards inside inline asm, so the block carries its own wait states: 2
-  // before (a VALU write of srcA/srcB must precede the MFMA read by 2), and 12
-  // after, so no instruction the compiler places next can overwrite srcA/srcB
-  // while the 8-pass MFMA may still be reading them.  The "memory" clobber
-  // keeps the software-pipelined operand loads in program order around it.
-  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c) {
-    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 3"
-                 : "+a"(c)
-                 : "v"(a), "v"(b)
-                 : "memory");
+  // Inline-asm MFMAs.  The O^T accumulators (256 registers per lane) must stay
+  // in the AGPR file and the S^T accumulator in VGPRs; builtins leave that
+  // choice to the compiler, which mixes the files and spills.  The compiler
+  // does not model hazards inside inline asm, so the code provides them:
+  //  * RAW VALU -> srcA/srcB needs 2 wait states: callers pass nop = true
+  //    when an operand may have just been written by a VALU instruction;
+  //  * WAR srcA/srcB -> later write: every MFMA also takes the operands of
+  //    the previous MFMA (pa, pb) as inputs, so the compiler cannot reuse
+  //    those registers before the next MFMA has issued; the last MFMA of a
+  //    sequence is followed by tail(), which holds its operands for 8 more
+  //    wait states;
+  //  * RAW result -> VALU read needs up to 18 wait states: drain_*().
+  // The "memory" clobber keeps the software-pipelined operand loads in
+  // program order around the MFMAs.
+  template <bool NOP>
+  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
+    if constexpr (NOP)
+      asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+    else
+      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+  }
+  static __device__ __forceinline__ void mma_v(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                 : "+v"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+  }
+  static __device__ __forceinline__ void mma_v0(bf16x8 a, bf16x8 b, acc_t& c) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
+                 : "=&v"(c) : "v"(a), "v"(b) : "memory");
+  }
+  static __device__ __forceinline__ void tail(const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 7" : : "v"(a), "v"(b));
+  }
+  // wait states between the last asm MFMA writing an accumulator and VALU reads
+  static __device__ __forceinline__ void drain_v(acc_t& c, const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(c) : "v"(a), "v"(b));
+  }
+  static __device__ __forceinline__ void drain(acc_t& c) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(c));
   }
   // c *= s on an AGPR-resident accumulator without moving it to VGPRs.
   static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) {
@@ -124,11 +151,6 @@ struct Mfma<32> {
       c[e] = x;
     }
   }
-  // Wait states between the last asm MFMA writing `c` and any later read of it
-  // (an XDL result needs up to 18 before VALU reads; 3 x 8 + margin).
-  static __device__ __forceinline__ void drain(acc_t& c) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(c));
-  }
 };
 
 template <>
@@ -137,7 +159,16 @@ struct Mfma<16> {
   static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c) { c = mma(a, b, c); }
+  template <bool NOP>
+  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8&, const bf16x8&) {
+    c = mma(a, b, c);
+  }
+  static __device__ __forceinline__ void mma_v(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8&, const bf16x8&) {
+    c = mma(a, b, c);
+  }
+  static __device__ __forceinline__ void mma_v0(bf16x8 a, bf16x8 b, acc_t& c) { c = mma(a, b, acc_t{}); }
+  static __device__ __forceinline__ void tail(const bf16x8&, const bf16x8&) {}
+  static __device__ __forceinline__ void drain_v(acc_t&, const bf16x8&, const bf16x8&) {}
   static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) { c *= s; }
   static __device__ __forceinline__ void drain(acc_t&) {}
 };
@@ -145,6 +176,16 @@ struct Mfma<16> {
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
 // the compiler keeps per-array alias information and does not make the reads
 // of one tile buffer wait for the DMA still filling the other.
+// max / sum of x over lanes l and l ^ 32 (gfx950 v_permlane32_swap: no LDS trip)
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ bf16x8 lds_read_b128(const void* base, uint32_t byte_off) {
   return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
 }
@@ -292,41 +333,87 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 
     // S^T = K Q^T
     acc_t sacc[C::MT];
-#pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt) sacc[mt] = acc_t{};
     const uint32_t q_off = (uint32_t)(hl * C::QLP + hq) * 16u;
+    if constexpr (T == 32) {
+      // one 32-key M-tile: operands of step s + PDK are loaded before MFMA s
+      constexpr int PDK = 4;
+      const uint32_t k_off = (uint32_t)((ks * 32 + lt) * C::PK + hq) * 16u;
+      auto load_k = [&](int s) { return lds_read_b128(kt, k_off + (uint32_t)(s * C::LG) * 16u); };
+      auto load_q = [&](int s) { return lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u); };
+      bf16x8 kbuf[PDK], qbuf[PDK];
 #pragma unroll
-    for (int s = 0; s < C::QSTEPS; ++s) {
-      bf16x8 bq;
-      if (s < C::QREG)
-        bq = qb[s < C::QREG ? s : 0];
-      else
-        bq = lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u);
+      for (int i = 0; i < PDK; ++i) {
+        kbuf[i] = load_k(i);
+        if (i >= C::QREG) qbuf[i] = load_q(i);
+      }
+      bf16x8 pa = {}, pq = {};
 #pragma unroll
-      for (int mt = 0; mt < C::MT; ++mt) {
-        const int row = ks * 32 + mt * T + lt;
-        const int chunk = s * C::LG + hq;
-        const bf16x8 a = lds_read_b128(kt, (uint32_t)(row * C::PK + chunk) * 16u);
-        sacc[mt] = M::mma(a, bq, sacc[mt]);
+      for (int s = 0; s < C::QSTEPS; ++s) {
+        const bf16x8 a = kbuf[s % PDK];
+        const bf16x8 bq = (s < C::QREG) ? qb[s < C::QREG ? s : 0] : qbuf[s % PDK];
+        if (s + PDK < C::QSTEPS) {
+          kbuf[s % PDK] = load_k(s + PDK);
+          if (s + PDK >= C::QREG) qbuf[s % PDK] = load_q(s + PDK);
+        }
+        if (s == 0)
+          M::mma_v0(a, bq, sacc[0]);
+        else
+          M::mma_v(a, bq, sacc[0], pa, pq);
+        pa = a;
+        pq = bq;
+      }
+      M::drain_v(sacc[0], pa, pq);
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt) sacc[mt] = acc_t{};
+#pragma unroll
+      for (int s = 0; s < C::QSTEPS; ++s) {
+        bf16x8 bq;
+        if (s < C::QREG)
+          bq = qb[s < C::QREG ? s : 0];
+        else
+          bq = lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u);
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) {
+          const int row = ks * 32 + mt * T + lt;
+          const int chunk = s * C::LG + hq;
+          const bf16x8 a = lds_read_b128(kt, (uint32_t)(row * C::PK + chunk) * 16u);
+          sacc[mt] = M::mma(a, bq, sacc[mt]);
+        }
       }
     }
 
-    // masked scores in base-2 units
-    float sv[C::MT * C::CPL];
-    float tmax = kNegInf;
+    // Raw scores; invalid keys -> -inf.  A tile whose 32 keys are all valid
+    // (the common case) skips the per-element mask.  The softmax scale is
+    // applied inside the exponent (fma), and the max is taken on raw scores
+    // (scale > 0 preserves the order).
+    constexpr int NV = C::MT * C::CPL;
+    float sv[NV];
+    if (vmask == 0xffffffffu) {
 #pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt) {
+      for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
-      for (int e = 0; e < C::CPL; ++e) {
-        const int key = mt * T + 4 * C::LG * (e / 4) + 4 * hq + (e % 4);
-        const bool valid = (vmask >> key) & 1u;
-        const float x = valid ? sacc[mt][e] * p.scale_log2 : kNegInf;
-        sv[mt * C::CPL + e] = x;
-        tmax = fmaxf(tmax, x);
+        for (int e = 0; e < C::CPL; ++e) sv[mt * C::CPL + e] = sacc[mt][e];
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt) {
+#pragma unroll
+        for (int e = 0; e < C::CPL; ++e) {
+          const int key = mt * T + 4 * C::LG * (e / 4) + 4 * hq + (e % 4);
+          sv[mt * C::CPL + e] = ((vmask >> key) & 1u) ? sacc[mt][e] : kNegInf;
+        }
       }
     }
+    float tmax = sv[0];
 #pragma unroll
-    for (int o = T; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+    for (int i = 1; i < NV; ++i) tmax = fmaxf(tmax, sv[i]);
+    if constexpr (T == 32) {
+      tmax = xor32_max(tmax);
+    } else {
+#pragma unroll
+      for (int o = T; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+    }
+    tmax *= p.scale_log2;
 
     // lazy rescale
     const float m_new = fmaxf(m_used, tmax);
@@ -338,13 +425,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       m_used = m_new;
     }
 
-    // P^T (fp32 -> bf16) as the B operand of O^T = V^T P^T
-    constexpr int KSTEPS = (C::MT * C::CPL) / 8;  // O^T contraction steps per 32 keys
+    // P^T = 2^(scale_log2 * s - m) (fp32 -> bf16) as the B operand of
+    // O^T = V^T P^T; -inf scores give exactly 0.  While no valid key has been
+    // seen m_used is -inf and every score is -inf: use 0 as the offset.
+    constexpr int KSTEPS = NV / 8;  // O^T contraction steps per 32 keys
+    const float moff = (m_used == kNegInf) ? 0.f : -m_used;
     bf16x8 pb[KSTEPS];
 #pragma unroll
-    for (int i = 0; i < C::MT * C::CPL; ++i) {
-      const float x = sv[i];
-      const float e = (x == kNegInf) ? 0.f : exp2f(x - m_used);
+    for (int i = 0; i < NV; ++i) {
+      const float e = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
       l_part += e;
       pb[i / 8][i % 8] = (bf16)e;
     }
@@ -373,12 +462,19 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     bf16x8 abuf[PD];
 #pragma unroll
     for (int i = 0; i < PD; ++i) abuf[i] = load_a(i);
+    bf16x8 prev_a = {}, prev_b = {};
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const bf16x8 a = abuf[i % PD];
       if (i + PD < NI) abuf[i % PD] = load_a(i + PD);
-      M::mma_agpr(a, pb[i / C::OT], oacc[i % C::OT]);
+      if (i % C::OT == 0)  // first use of pb[kk], just written by VALU
+        M::template mma_agpr<true>(a, pb[i / C::OT], oacc[i % C::OT], prev_a, prev_b);
+      else
+        M::template mma_agpr<false>(a, pb[i / C::OT], oacc[i % C::OT], prev_a, prev_b);
+      prev_a = a;
+      prev_b = pb[i / C::OT];
     }
+    M::tail(prev_a, prev_b);
   };
 
   __syncthreads();  // indices staged
@@ -401,8 +497,12 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 
   // ---- finish: row sums over the lane groups sharing a head -------------------
   float l_sum = l_part;
+  if constexpr (T == 32) {
+    l_sum = xor32_sum(l_sum);
+  } else {
 #pragma unroll
-  for (int o = T; o < 64; o <<= 1) l_sum += __shfl_xor(l_sum, o, 64);
+    for (int o = T; o < 64; o <<= 1) l_sum += __shfl_xor(l_sum, o, 64);
+  }
 
   float m_fin = m_used;
   if constexpr (C::NSPLITW > 1) {
