@@ -83,6 +83,17 @@ bool mfma_layout_ok(const sfa_fwd_args* a) {
   return true;
 }
 
+// MFMA backward eligibility beyond the kernel-variant shape: 16-byte aligned
+// rows of q, k, v and dout, and 8-byte aligned dq rows.
+bool bwd_mfma_ok(const sfa_bwd_args* a) {
+  if (!mfma_layout_ok(&a->fwd)) return false;
+  if (!aligned16(a->dout) || ((uintptr_t)a->dq & 7u) != 0) return false;
+  const int64_t s[] = {a->do_sb, a->do_ss, a->do_sh, a->dq_sb, a->dq_ss, a->dq_sh};
+  for (int64_t x : s)
+    if (x % 8 != 0) return false;
+  return true;
+}
+
 struct FwdPlan {
   bool mfma;
   int num_splits;
@@ -209,10 +220,10 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   const size_t need = sfa_bwd_workspace_size(a);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(SFA_E_WORKSPACE, "sfa_bwd needs %zu workspace bytes (got %zu)", need, workspace_bytes);
-  if (f.topk > kGenericMaxTopk) return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d", f.topk, kGenericMaxTopk);
-
   hipStream_t s = (hipStream_t)stream;
   sfa::Params p = to_params(&f);
+  if (!(bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p)) && f.topk > kGenericMaxTopk)
+    return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d", f.topk, kGenericMaxTopk);
   p.dout = a->dout; p.do_sb = a->do_sb; p.do_ss = a->do_ss; p.do_sh = a->do_sh;
   p.dq = a->dq; p.dq_sb = a->dq_sb; p.dq_ss = a->dq_ss; p.dq_sh = a->dq_sh;
   const size_t nk = (size_t)f.B * f.Skv * f.Hkv * f.Dqk, nv = (size_t)f.B * f.Skv * f.Hkv * f.Dv;
@@ -226,7 +237,12 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   if (e == hipSuccess) e = sfa::launch_zero_f32(p.dv_acc, nv, s);
   if (e == hipSuccess && p.dsink) e = sfa::launch_zero_f32(p.dsink, (size_t)f.Hq, s);
   if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
-  if (e == hipSuccess) e = sfa::launch_bwd_generic(p, f.dtype, s);
+  if (e == hipSuccess) {
+    if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
+      e = sfa::launch_bwd_mfma(p, s);
+    else
+      e = sfa::launch_bwd_generic(p, f.dtype, s);
+  }
   if (e == hipSuccess)
     e = sfa::launch_bwd_finish(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, a->dv, a->dv_sb, a->dv_ss, a->dv_sh,
                                s);

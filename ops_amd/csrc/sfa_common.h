@@ -104,4 +104,6 @@ hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);
 bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
+hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
+bool bwd_mfma_supported(const Params& p);
 }  // namespace sfa

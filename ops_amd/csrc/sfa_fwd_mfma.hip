@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "sfa_common.h"
+#include "sfa_lds.h"
 
 namespace sfa {
 namespace {
@@ -82,9 +83,6 @@ struct FwdCfg {
   static_assert(!VK || DV <= DQK, "v must be a prefix of k");
   static_assert(CHK % 2 == 0 && CHV % 2 == 0, "rows need an even number of 16-byte chunks");
 };
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 template <int T>
 struct Mfma;
@@ -176,26 +174,6 @@ struct Mfma<16> {
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
 // the compiler keeps per-array alias information and does not make the reads
 // of one tile buffer wait for the DMA still filling the other.
-// max / sum of x over lanes l and l ^ 32 (gfx950 v_permlane32_swap: no LDS trip)
-__device__ __forceinline__ float xor32_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ bf16x8 lds_read_b128(const void* base, uint32_t byte_off) {
-  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
-}
-
-__device__ __forceinline__ bf16x4 lds_read_tr16(const void* base, uint32_t byte_off) {
-  typedef __attribute__((address_space(3))) const char lds_cchar;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (lds_bf16x4*)((lds_cchar*)(base) + byte_off));
-}
-
 template <class C>
 __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   constexpr int T = C::T;
@@ -270,50 +248,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
 
-  // Slot u of a tile holds 16-byte chunk (u % pitch) of row u / pitch; the pad
-  // slot of each row (chunk == CH) is loaded from an out-of-range offset (0).
-  // Thread tid owns slots tid, tid + kThreads, ...: its (row, chunk) walk is
-  // advanced incrementally from two registers made opaque per call, so the
-  // compiler cannot hoist one offset per instruction out of the tile loop.
-  auto gather_rows = [&](const int* ib, u32x4* dst, const __amdgpu_buffer_rsrc_t& rs, uint32_t row_bytes,
-                         auto pitch_c, auto ch_c) {
-    constexpr int PITCH = decltype(pitch_c)::value;
-    constexpr int CH = decltype(ch_c)::value;
-    constexpr int NSLOT = C::NKT * PITCH;
-    constexpr int NIT = (NSLOT + C::kThreads - 1) / C::kThreads;
-    constexpr int DR = C::kThreads / PITCH, DC = C::kThreads % PITCH;
-    int r = tid / PITCH, c = tid - (tid / PITCH) * PITCH;
-    asm volatile("" : "+v"(r), "+v"(c));
-    int ids[NIT], cs[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const bool live = (NSLOT % C::kThreads == 0) || (it * C::kThreads + tid < NSLOT);
-      ids[it] = live ? ib[r] : -1;
-      cs[it] = c;
-      c += DC;
-      r += DR;
-      if (c >= PITCH) {
-        c -= PITCH;
-        r += 1;
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      if ((NSLOT % C::kThreads == 0) || (it * C::kThreads + tid < NSLOT)) {
-        const uint32_t off = (ids[it] >= 0 && cs[it] < CH)
-                                 ? __umul24((uint32_t)ids[it], row_bytes) + (uint32_t)cs[it] * 16u
-                                 : kOOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + it * C::kThreads + wave * 64), 16, off, 0, 0,
-                                                 0);
-      }
-    }
-  };
   auto gather = [&](int tile, u32x4* kdst, u32x4* vdst) {
     const int* ib = s_idx + tile * C::NKT;
-    gather_rows(ib, kdst, rk, krow_bytes, std::integral_constant<int, C::PK>{}, std::integral_constant<int, C::CHK>{});
-    if constexpr (!C::VK)
-      gather_rows(ib, vdst, rv, vrow_bytes, std::integral_constant<int, C::PV>{},
-                  std::integral_constant<int, C::CHV>{});
+    gather_tile<C::NKT, C::CHK, C::kThreads>(ib, kdst, rk, krow_bytes, tid, wave);
+    if constexpr (!C::VK) gather_tile<C::NKT, C::CHV, C::kThreads>(ib, vdst, rv, vrow_bytes, tid, wave);
   };
 
   // ---- accumulators ----------------------------------------------------

@@ -95,7 +95,7 @@ def test_prefill_mqa_d128(S, K):
 
 def test_train_gqa_fwd_full():
     _say("train_gqa bf16 B=2 S=8192 Hq=32 Hkv=2 d=128 K=1024 forward")
-    w = make_workload("train_gqa", device=DEV, with_dout=False)
+    w = _workload("train_gqa")
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     q, k, v, idx, _ = _cpu(w)
     rows = torch.arange(0, 8192, 61)
@@ -116,6 +116,66 @@ def test_train_gqa_bwd_reduced():
     for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref[:3]):
         e = _rel_l2(a.cpu(), b)
         assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+
+
+def test_train_gqa_bwd_full():
+    """Full-size GQA backward (MFMA kernel); the oracle checks one (batch,
+    kv-head) slice, which is an independent problem of its own."""
+    _say("train_gqa bf16 B=2 S=8192 Hq=32 Hkv=2 d=128 K=1024 fwd+bwd (MFMA bwd)")
+    w = _workload("train_gqa")
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+    dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale)
+    torch.cuda.synchronize()
+    b, g, G = 1, 1, 16
+    hs = slice(g * G, (g + 1) * G)
+    q = w.q[b:b + 1, :, hs].cpu()
+    k = w.k[b:b + 1, :, g:g + 1].cpu()
+    v = w.v[b:b + 1, :, g:g + 1].cpu()
+    idx = w.idx[b:b + 1, :, g:g + 1].cpu()
+    o_s, l_s, do_s = out[b:b + 1, :, hs].cpu(), lse[b:b + 1, :, hs].cpu(), w.dout[b:b + 1, :, hs].cpu()
+    g_ref = ref_backward(q, k, v, idx, o_s, l_s, do_s, w.scale)
+    for name, a, ref in (("dq", dq[b:b + 1, :, hs], g_ref[0]), ("dk", dk[b:b + 1, :, g:g + 1], g_ref[1]),
+                         ("dv", dv[b:b + 1, :, g:g + 1], g_ref[2])):
+        e = _rel_l2(a.cpu(), ref)
+        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+
+
+def test_generic_bf16_bwd_large_group():
+    """G = 32 has no MFMA backward variant: the generic bf16 kernels run."""
+    _say("bf16 bwd G=32 d=64 (generic kernels)")
+    w = make_workload("train_gqa", device=DEV, S=256, K=64, Hq=64, Hkv=2, Dqk=64, Dv=64)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+    q, k, v, idx, _ = _cpu(w)
+    o_ref, l_ref = ref_forward(q, k, v, idx, w.scale)
+    _check_fwd(out, lse, o_ref, l_ref)
+    dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale)
+    g_ref = ref_backward(q, k, v, idx, out.cpu(), lse.cpu(), w.dout.cpu(), w.scale)
+    for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref[:3]):
+        e = _rel_l2(a.cpu(), b)
+        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+
+
+def test_bwd_mfma_masking_and_sink():
+    """MFMA backward with interior padding, kv_lens, a fully masked row, G < 16
+    and an attention sink."""
+    _say("MFMA bwd: padding / kv_lens / masked row / G=8 / sink")
+    w = make_workload("train_gqa", device=DEV, S=512, K=128, B=1, Hq=16, Hkv=2)
+    idx = w.idx.clone()
+    r = torch.rand(idx.shape, generator=torch.Generator(device=DEV).manual_seed(3), device=DEV)
+    idx = torch.where(r < 0.1, torch.full_like(idx, -1), idx)
+    idx[:, 7] = -1
+    kv_lens = torch.tensor([480], dtype=torch.int32, device=DEV)
+    sink = torch.linspace(-1, 2, 16, device=DEV)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, idx, w.scale, kv_lens=kv_lens, attn_sink=sink)
+    dq, dk, dv, ds = ops_amd.sfa_backward(w.q, w.k, w.v, idx, out, lse, w.dout, w.scale, kv_lens=kv_lens,
+                                          attn_sink=sink)
+    q, k, v, _, _ = _cpu(w)
+    g_ref = ref_backward(q, k, v, idx.cpu(), out.cpu(), lse.cpu(), w.dout.cpu(), w.scale, kv_lens=kv_lens.cpu(),
+                         sink=sink.cpu())
+    for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
+        e = _rel_l2(a.cpu(), b)
+        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+    assert torch.all(dq[:, 7] == 0)
 
 
 @pytest.mark.parametrize("S,K", [(300, 64), (1024, 256)])
