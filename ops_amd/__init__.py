@@ -8,6 +8,8 @@ Public API (BSHD, see ``ops_amd.sfa``)::
 The HIP kernels live in ``libsfa.so`` (``python -m ops_amd.build``), reached
 through the C ABI declared in ``include/sfa.h``.
 """
-from .sfa import SparseFlashAttention, sfa_backward, sfa_forward, sparse_flash_attention
+from .sfa import (SparseFlashAttention, SparseFlashAttentionSBHD, SparseFlashAttentionTriton, sfa_backward,
+                  sfa_forward, sparse_flash_attention)
 
-__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward"]
+__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward",
+           "SparseFlashAttentionSBHD", "SparseFlashAttentionTriton"]

@@ -19,8 +19,9 @@
 //      head-contractions (16x16x16 MFMA):
 //      dV  = P^T  dO          dK = scale · dS^T Q
 //    and dV/dK rows are scattered with fp32 atomics into per-key
-//    accumulators (the reference's scheme, SFA.py:849-853; see the backward
-//    design notes for why atomics over an index inversion).
+//    accumulators (the reference's scheme, SFA.py:849-853): its cost does
+//    not grow with the density of the index set and it needs no inverted
+//    index of the top-k rows.
 //  * dQ partials of the 4 waves are summed through LDS at the end and
 //    written once (no atomics on dQ).
 //  * δ = Σ O·dO (minus any gradient on lse) comes from a preceding kernel.

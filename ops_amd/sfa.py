@@ -34,7 +34,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward"]
+__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward",
+           "SparseFlashAttentionSBHD", "SparseFlashAttentionTriton"]
 
 _DTYPES = {torch.float32: _lib.SFA_DTYPE_F32, torch.bfloat16: _lib.SFA_DTYPE_BF16}
 _DKV_MODES = {"auto": _lib.SFA_DKV_AUTO, "atomic": _lib.SFA_DKV_ATOMIC, "csr": _lib.SFA_DKV_CSR}
@@ -213,3 +214,47 @@ class SparseFlashAttention(torch.autograd.Function):
 def sparse_flash_attention(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Functional form of :class:`SparseFlashAttention`."""
     return SparseFlashAttention.apply(q, k, v, topk_idxs, sm_scale, kv_lens, attn_sink)
+
+
+class SparseFlashAttentionSBHD(torch.autograd.Function):
+    """The reference's exact operator signature (SFA.py:69-164, 166-306):
+
+    ``apply(q [S, B, H, D], kv [S_kv, B, D], attn_sink [H], topk_idxs [S, B, K],
+    sm_scale) -> out [S, B, H, D]``; backward returns
+    ``(grad_q, grad_kv, grad_sink, None, None)``.
+
+    One KV head whose rows serve as both K and V (SFA.py:116); the index row of
+    query t is shared by all heads (SFA.py:538).  The SBHD tensors are passed
+    to the kernels as strided BSHD views, so nothing is copied; the gradient
+    of the shared ``kv`` is dK + dV (the reference sums them into one buffer,
+    SFA.py:849-853).
+    """
+
+    @staticmethod
+    def forward(ctx, q, kv, attn_sink, topk_idxs, sm_scale=None):
+        if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
+            raise ValueError("expected q [S, B, H, D], kv [S_kv, B, D], topk_idxs [S, B, K]")
+        qb = q.permute(1, 0, 2, 3)
+        kb = kv.permute(1, 0, 2).unsqueeze(2)
+        idx = topk_idxs.permute(1, 0, 2).unsqueeze(2)
+        out, lse = sfa_forward(qb, kb, kb, idx, sm_scale, attn_sink=attn_sink)
+        ctx.save_for_backward(q, kv, attn_sink, topk_idxs, out, lse)
+        ctx.sm_scale = sm_scale
+        return out.permute(1, 0, 2, 3)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, kv, sink, topk_idxs, out, lse = ctx.saved_tensors
+        qb = q.permute(1, 0, 2, 3)
+        kb = kv.permute(1, 0, 2).unsqueeze(2)
+        idx = topk_idxs.permute(1, 0, 2).unsqueeze(2)
+        dq, dk, dv, dsink = sfa_backward(qb, kb, kb, idx, out, lse, grad_out.permute(1, 0, 2, 3), ctx.sm_scale,
+                                         attn_sink=sink)
+        grad_kv = (dk.float() + dv.float()).to(kv.dtype).squeeze(2).permute(1, 0, 2)
+        if dsink is not None and sink is not None:
+            dsink = dsink.to(sink.dtype)
+        return dq.permute(1, 0, 2, 3), grad_kv, dsink, None, None
+
+
+# The reference's class name, for call sites that import it by name.
+SparseFlashAttentionTriton = SparseFlashAttentionSBHD

@@ -306,3 +306,31 @@ def test_autograd_function_and_dlse():
     ((o2 * w.dout.cpu().double()).sum() + (l2 * gl.cpu().double()).sum()).backward()
     for a, b in ((q, qc), (k, kc), (v, vc)):
         assert _rel_l2(a.grad.cpu(), b.grad) <= GRAD_RL2
+
+
+def test_reference_signature_shim():
+    """SparseFlashAttentionTriton.apply(q[S,B,H,D], kv[S_kv,B,D], sink[H],
+    idx[S,B,K], scale) -> out, with grads (q, kv, sink), against the oracle
+    (K = V = kv, one KV head)."""
+    _say("reference-signature SBHD shim, bf16 and fp32")
+    for dtype in (torch.float32, torch.bfloat16):
+        g = torch.Generator(device=DEV).manual_seed(11)
+        S, B, H, D, K = 96, 2, 16, 128, 48
+        q = torch.randn(S, B, H, D, device=DEV, generator=g).to(dtype).requires_grad_(True)
+        kv = torch.randn(S, B, D, device=DEV, generator=g).to(dtype).requires_grad_(True)
+        sink = torch.randn(H, device=DEV, generator=g).requires_grad_(True)
+        idx = torch.randint(-1, S, (S, B, K), device=DEV, generator=g, dtype=torch.int32)
+        dout = torch.randn(S, B, H, D, device=DEV, generator=g).to(dtype)
+        out = ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, 0.1)
+        out.backward(dout)
+        qb = q.detach().permute(1, 0, 2, 3).cpu()
+        kb = kv.detach().permute(1, 0, 2).unsqueeze(2).cpu()
+        ib = idx.permute(1, 0, 2).unsqueeze(2).cpu()
+        o_ref, l_ref = ref_forward(qb, kb, kb, ib, 0.1, sink=sink.detach().cpu())
+        err = float((out.detach().permute(1, 0, 2, 3).float().cpu() - o_ref).abs().max())
+        assert err <= O_TOL, (dtype, err)
+        dq, dk, dv, ds = ref_backward(qb, kb, kb, ib, o_ref, l_ref, dout.permute(1, 0, 2, 3).cpu(), 0.1,
+                                      sink=sink.detach().cpu())
+        assert _rel_l2(q.grad.permute(1, 0, 2, 3).cpu(), dq) <= GRAD_RL2
+        assert _rel_l2(kv.grad.permute(1, 0, 2).unsqueeze(2).cpu(), dk + dv) <= GRAD_RL2
+        assert _rel_l2(sink.grad.cpu(), ds) <= GRAD_RL2

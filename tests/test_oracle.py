@@ -259,3 +259,14 @@ def test_count_valid_pairs():
     idx = torch.tensor([[[[0, -1, 5, 9]], [[2, 3, -1, -1]]]], dtype=torch.int32)
     assert count_valid_pairs(idx, 6) == 4
     assert count_valid_pairs(idx, 6, torch.tensor([3], dtype=torch.int32)) == 2
+
+
+def test_autograd_restatement_forward_matches_brute_force():
+    q, k, v, idx, _ = _rand_case(B=2, S=6, Skv=9, seed=31)
+    kv_lens = torch.tensor([7, 9], dtype=torch.int32)
+    sink = torch.tensor([0.2, -0.4, 1.1, 0.0], dtype=torch.float64)
+    for s_ in (None, sink):
+        o, l = sfa_forward_autograd(q, k, v, idx, scale=0.45, kv_lens=kv_lens, sink=s_)
+        ob, lb = _brute_forward(q, k, v, idx, 0.45, kv_lens=kv_lens, sink=s_)
+        torch.testing.assert_close(o, ob, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(l, lb, rtol=1e-12, atol=1e-12)
