@@ -11,7 +11,7 @@ measured in the same run and reported under ``workloads``:
 * ``prefill``     MQA fwd, S=4096, Hq=16, d=128, top-k 512        (TFLOP/s)
 * ``train_gqa``   GQA fwd (+ bwd), B=2, S=8192, Hq=32, Hkv=2, top-k 1024
 * ``mla_decode``  B=64 x 1 query, KV [64, 65536, 1, 576], top-k 2048, split-k
-                  + combine, Infinity Cache flushed before every step (GB/s)
+                  + combine, caches flushed (by a 1 GiB read) before every step (GB/s)
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -181,11 +181,14 @@ def bench_mla_decode(args):
     B, _, Hq, Dqk = w.q.shape
     Dv = w.v.shape[3]
     nbytes = pairs * Dqk * 2 + w.q.numel() * 2 + B * Hq * Dv * 2 + B * Hq * 4 + w.idx.numel() * 4
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    # Before every step a 1 GiB buffer is READ, which evicts the KV rows from
+    # the 256 MB Infinity Cache and L2 without leaving dirty lines behind (a
+    # write-flush makes the next kernel pay for write-backs it did not cause).
+    flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     out = torch.empty((B, 1, Hq, Dv), dtype=w.q.dtype, device="cuda")
     lse = torch.empty((B, 1, Hq), dtype=torch.float32, device="cuda")
     fn = lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
-    times, _ = time_steps(fn, args.steps * 4, args.warmup, before=lambda: flush.fill_(1))
+    times, _ = time_steps(fn, args.steps * 4, args.warmup, before=lambda: flush.sum())
     us = sum(times) / len(times) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"metric": "decode GB/s (algorithmic bytes, cache flushed)", "value": gbs, "unit": "GB/s", "us": us,
@@ -203,6 +206,9 @@ def main():
     ap.add_argument("--bwd", action="store_true", help="also time the train_gqa backward")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB `steps` times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sparse attention path runs on a single MI355X "
@@ -211,6 +217,15 @@ def main():
     import torch
     assert torch.cuda.is_available(), "no GPU"
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": args.steps}), flush=True)
+        return
 
     w, head = bench_mla_prefill(args)
     extra = {}

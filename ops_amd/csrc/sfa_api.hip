@@ -104,11 +104,13 @@ struct FwdPlan {
 
 constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
 constexpr int kIdxCap = 2048;
+constexpr int kMaxSplits = 64;  // the combine kernel holds one split per lane of a wave
 
 FwdPlan plan_fwd(const sfa_fwd_args* a) {
   FwdPlan pl{};
   sfa::Params p = to_params(a);
-  pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p);
+  pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p) &&
+            (a->topk + kIdxCap - 1) / kIdxCap <= kMaxSplits;
   int splits = 1;
   if (pl.mfma) {
     const int nk = sfa::fwd_mfma_tile_keys(p);
@@ -124,6 +126,7 @@ FwdPlan plan_fwd(const sfa_fwd_args* a) {
     if (splits < min_splits) splits = min_splits;
     int max_splits = (a->topk + nk - 1) / nk;
     if (splits > max_splits) splits = max_splits;
+    if (splits > kMaxSplits) splits = kMaxSplits;
     if (splits < 1) splits = 1;
     int len = (a->topk + splits - 1) / splits;
     len = (len + nk - 1) / nk * nk;

@@ -225,7 +225,9 @@ __global__ void finish_kernel(const float* acc, int B, int Skv, int Hkv, int D, 
 }
 
 // Split-k combine: lse2 = log2 Σ_s 2^lse2_s, out = Σ_s 2^(lse2_s - lse2)·o_s,
-// then the optional sink joins the denominator.  One wave per (b, t, h) row.
+// then the optional sink joins the denominator.  One wave per (b, t, h) row:
+// the per-split weights are computed once per row (lane s), the partial rows
+// are read as float4.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -235,27 +237,35 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
   const int h = row % p.Hq;
   const int t = (row / p.Hq) % p.Sq;
   const int b = row / ((int64_t)p.Hq * p.Sq);
-  float m = kNegInf;
-  for (int s = 0; s < p.num_splits; ++s) m = fmaxf(m, p.part_lse[s * nrows + row]);
+  const float ls = lane < p.num_splits ? p.part_lse[lane * nrows + row] : kNegInf;
+  const float m = wave_max(ls);
   const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
   const float mm = fmaxf(m, sink2);
-  float l = 0.f;
-  if (mm != kNegInf) {
-    for (int s = 0; s < p.num_splits; ++s) {
-      const float ls = p.part_lse[s * nrows + row];
-      l += (ls == kNegInf) ? 0.f : exp2f(ls - mm);
-    }
-    if (p.sink) l += exp2f(sink2 - mm);
-  }
+  const float e = (ls == kNegInf || mm == kNegInf) ? 0.f : exp2f(ls - mm);
+  float l = wave_sum(e);
+  if (p.sink && mm != kNegInf) l += exp2f(sink2 - mm);
   const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float wl = e * inv;  // weight of split `lane`
   T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
-  for (int d = lane; d < p.Dv; d += 64) {
-    float acc = 0.f;
-    for (int s = 0; s < p.num_splits; ++s) {
-      const float ls = p.part_lse[s * nrows + row];
-      if (ls != kNegInf) acc += exp2f(ls - mm) * p.part_o[(s * nrows + row) * p.Dv + d];
+  if ((p.Dv & 3) == 0) {
+    for (int d = 4 * lane; d < p.Dv; d += 256) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < p.num_splits; ++s) {
+        const float w = __shfl(wl, s, 64);
+        if (w != 0.f) acc += w * *reinterpret_cast<const f32x4*>(p.part_o + (s * nrows + row) * p.Dv + d);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) orow[d + j] = from_f32<T>(acc[j]);
     }
-    orow[d] = from_f32<T>(acc * inv);
+  } else {
+    for (int d = lane; d < p.Dv; d += 64) {
+      float acc = 0.f;
+      for (int s = 0; s < p.num_splits; ++s) {
+        const float w = __shfl(wl, s, 64);
+        if (w != 0.f) acc += w * p.part_o[(s * nrows + row) * p.Dv + d];
+      }
+      orow[d] = from_f32<T>(acc);
+    }
   }
   if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
 }
