@@ -253,6 +253,30 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     gather_tile<C::NKT, C::CHK, C::kThreads>(ib, kdst, rk, krow_bytes, tid, wave);
     if constexpr (!C::VK) gather_tile<C::NKT, C::CHV, C::kThreads>(ib, vdst, rv, vrow_bytes, tid, wave);
   };
+  // Wide-row configs (v inside the k rows) issue the next tile's gather from
+  // inside the current tile's S^T MFMA stream instead of in one burst.
+  constexpr bool kSpread = C::VK && C::PK >= 64 && C::T == 32 && C::NKT % C::kWaves == 0;
+  typedef RowGather<(kSpread ? C::NKT : 32), (kSpread ? C::CHK : 72), (kSpread ? C::kWaves : 4)> RG;
+  // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
+  // tile's MFMA sequence (QSTEPS S^T MFMAs, then the O^T MFMAs)
+#ifndef SFA_DMA_STRIDE
+#define SFA_DMA_STRIDE 3
+#endif
+#ifndef SFA_DMA_FIRST
+#define SFA_DMA_FIRST 2
+#endif
+  constexpr int kDmaStride = SFA_DMA_STRIDE, kDmaFirst = SFA_DMA_FIRST;
+  constexpr int kOtMfmas = 32 / 16 * C::OT;
+  static_assert(!kSpread || kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kOtMfmas, "schedule fits");
+  // (on the last tile the offsets are all out of range: the instructions
+  // still issue, so the MFMA stream has no branches, and write zeros into the
+  // idle buffer)
+  auto dma_at = [&](int m, const RG& rg, u32x4* ndst) {
+    if constexpr (kSpread) {
+      if (m >= kDmaFirst && (m - kDmaFirst) % kDmaStride == 0 && (m - kDmaFirst) / kDmaStride < RG::NI)
+        rg.issue((m - kDmaFirst) / kDmaStride, rk, ndst, wave, lane);
+    }
+  };
 
   // ---- accumulators ----------------------------------------------------
   acc_t oacc[C::OT];
@@ -264,7 +288,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const int hq = lane / T;  // lane group: which k-slice of the MFMA operands
   const int lt = lane % T;
 
-  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt) {
+  // With kSpread, compute(tile) also issues the gather of the next tile into
+  // ndst (rg holds that tile's row offsets; the caller skips its own gather).
+  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, const RG& rg, u32x4* ndst) {
     // validity of this wave's 32 keys
     const int myid = s_idx[tile * C::NKT + ks * 32 + (lane & 31)];
     const uint32_t vmask = (uint32_t)__ballot(myid >= 0);
@@ -299,6 +325,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
           M::mma_v(a, bq, sacc[0], pa, pq);
         pa = a;
         pq = bq;
+        dma_at(s, rg, ndst);
       }
       M::drain_v(sacc[0], pa, pq);
     } else {
@@ -342,6 +369,20 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
         }
       }
     }
+    // P^T = 2^(scale_log2 * s - m) as the B operand of O^T = V^T P^T; -inf
+    // scores give exactly 0.  The exponentials are first taken against the
+    // running max m_used, independently of this tile's max, so the max
+    // reduction and the exponentials overlap; only when the tile's max
+    // exceeds m_used by more than kRescaleSlack (rare after the first valid
+    // tile) are O^T and l rescaled and the exponentials recomputed.  While no
+    // valid key has been seen m_used is -inf: the offset is then 0, and the
+    // first valid tile always takes the recompute path.
+    float ex[NV];
+    {
+      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+    }
     float tmax = sv[0];
 #pragma unroll
     for (int i = 1; i < NV; ++i) tmax = fmaxf(tmax, sv[i]);
@@ -352,8 +393,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       for (int o = T; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
     }
     tmax *= p.scale_log2;
-
-    // lazy rescale
     const float m_new = fmaxf(m_used, tmax);
     if (__any(m_new > m_used + kRescaleSlack)) {
       const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_used - m_new);
@@ -361,19 +400,21 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < C::OT; ++i) M::scale_agpr(oacc[i], alpha);
       m_used = m_new;
+      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
     }
-
-    // P^T = 2^(scale_log2 * s - m) (fp32 -> bf16) as the B operand of
-    // O^T = V^T P^T; -inf scores give exactly 0.  While no valid key has been
-    // seen m_used is -inf and every score is -inf: use 0 as the offset.
     constexpr int KSTEPS = NV / 8;  // O^T contraction steps per 32 keys
-    const float moff = (m_used == kNegInf) ? 0.f : -m_used;
     bf16x8 pb[KSTEPS];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const float e = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
-      l_part += e;
-      pb[i / 8][i % 8] = (bf16)e;
+    for (int i = 0; i < NV; ++i) pb[i / 8][i % 8] = (bf16)ex[i];
+    {
+      // pairwise sum (short dependency chain)
+#pragma unroll
+      for (int w = 1; w < NV; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < NV; i += 2 * w) ex[i] += ex[i + w];
+      l_part += ex[0];
     }
 
     // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
@@ -411,6 +452,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
         M::template mma_agpr<false>(a, pb[i / C::OT], oacc[i % C::OT], prev_a, prev_b);
       prev_a = a;
       prev_b = pb[i / C::OT];
+      dma_at(C::QSTEPS + i, rg, ndst);
     }
     M::tail(prev_a, prev_b);
   };
@@ -419,13 +461,25 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   if (ntiles > 0) gather(0, s_k0, s_v0);
   __syncthreads();
 
+  // row offsets of the next tile to gather (kSpread), read from s_idx ahead
+  // of the tile whose MFMA stream issues that gather, just before a barrier
+  RG rg;
+  auto next_ids = [&](int next) {
+    if constexpr (kSpread) {
+      const bool ok = next < ntiles;
+      rg.load_ids(s_idx + (ok ? next : 0) * C::NKT, ok, wave, krow_bytes);
+    }
+  };
+  next_ids(1);
   for (int j = 0; j < ntiles; j += 2) {
-    if (j + 1 < ntiles) gather(j + 1, s_k1, s_v1);
-    compute(j, s_k0, C::VK ? s_k0 : s_v0);
+    if (!kSpread && j + 1 < ntiles) gather(j + 1, s_k1, s_v1);
+    compute(j, s_k0, C::VK ? s_k0 : s_v0, rg, s_k1);
+    next_ids(j + 2);
     __syncthreads();
     if (j + 1 < ntiles) {
-      if (j + 2 < ntiles) gather(j + 2, s_k0, s_v0);
-      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1);
+      if (!kSpread && j + 2 < ntiles) gather(j + 2, s_k0, s_v0);
+      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1, rg, s_k0);
+      next_ids(j + 3);
       __syncthreads();
     }
   }

@@ -73,4 +73,66 @@ __device__ __forceinline__ void gather_tile(const int* ib, u32x4* dst, const __a
   }
 }
 
+// Row-wise gather for wide rows (PITCH = CH + 1 >= 64 slots, so one 64-lane
+// instruction spans at most two rows).  Wave w gathers tile rows
+// [w * RPW, (w + 1) * RPW), i.e. the contiguous slot range [w * SPW, (w+1) * SPW).
+// For instruction k every slot position is a compile-time constant, and the
+// two row byte offsets it needs are wave-uniform scalars, so issuing one
+// instruction costs two VALU operations and no per-lane index reads:
+//   voffset(lane) = 16 * lane + (lane < bnd ? S0 : S1)
+//   S0 = base[r0] + 16 * c0,  S1 = base[r0 + 1] + 16 * (c0 - PITCH)
+// with r0, c0 the row / chunk of the instruction's first slot and bnd the
+// lanes left in row r0.  base[r] is id * row_bytes, or kOOBRow for a padding
+// row, which keeps every offset of that row above 2^31 (out of range, the
+// hardware writes zeros).  The pad slot of a row reads the 16 bytes after the
+// row (the next row's first chunk, or zeros past the end of the range); pad
+// slots are never read.  Instructions can be issued one at a time (issue(k)),
+// so a caller can spread them over its MFMA stream.
+constexpr uint32_t kOOBRow = 0x80001000u;
+
+template <int NKT, int CH, int NWAVES>
+struct RowGather {
+  static constexpr int PITCH = CH + 1;
+  static constexpr int RPW = NKT / NWAVES;       // rows per wave
+  static constexpr int SPW = RPW * PITCH;        // slots per wave
+  static constexpr int NI = (SPW + 63) / 64;     // instructions per wave
+  static_assert(PITCH >= 64, "an instruction must span at most two rows");
+  static_assert(NKT % NWAVES == 0, "rows split evenly over the waves");
+
+  uint32_t base[RPW];
+
+  // ib: the tile's NKT staged row ids (-1 = padding row); wave-uniform reads.
+  // valid == false makes every row a padding row (the instructions then move
+  // no global data and write zeros); ib must still point into the array.
+  // (No pointer select: the compiler keeps ib's array identity, so the read
+  // does not wait for DMA into other LDS arrays.)
+  __device__ __forceinline__ void load_ids(const int* ib, bool valid, int wave, uint32_t row_bytes) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int id = __builtin_amdgcn_readfirstlane(ib[wave * RPW + r]);
+      base[r] = (valid && id >= 0) ? __umul24((uint32_t)id, row_bytes) : kOOBRow;
+    }
+  }
+
+  __device__ __forceinline__ void issue(int k, const __amdgpu_buffer_rsrc_t& rs, u32x4* dst, int wave,
+                                        int lane) const {
+    const int s0 = 64 * k;
+    const int r0 = s0 / PITCH, c0 = s0 % PITCH;
+    const int bnd = PITCH - c0;
+    const uint32_t S0 = base[r0] + 16u * (uint32_t)c0;
+    uint32_t off = S0;
+    if (bnd < 64 && r0 + 1 < RPW) {
+      const uint32_t S1 = base[r0 + 1] + 16u * (uint32_t)c0 - 16u * (uint32_t)PITCH;
+      off = lane < bnd ? S0 : S1;
+    }
+    off += 16u * (uint32_t)lane;
+    u32x4* d = dst + wave * SPW + s0;
+    if (s0 + 64 <= SPW) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)d, 16, off, 0, 0, 0);
+    } else if (lane < SPW - s0) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)d, 16, off, 0, 0, 0);
+    }
+  }
+};
+
 }  // namespace sfa
