@@ -542,10 +542,16 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     if (ks != 0) return;
   }
 
-  if (!hvalid) return;
-  const int h = g * p.G + hl;
+  // final output staged through LDS (every lane of the wave takes part in the
+  // row stores, so lanes of absent heads stay until then and only skip their
+  // own writes)
+  constexpr bool kStageOut = C::T == 32 && C::NSPLITW == 1 && C::DV == 512 && C::kWaves == 4 &&
+                             T * (C::DV + 8) * 2 <= C::KBUF * 16 && T * (C::DV + 8) * 2 <= C::QBUF * 8;
+  if (!kStageOut && !hvalid) return;
+  const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
   if (p.num_splits > 1) {
+    if (!hvalid) return;
     // normalised partial output and base-2 LSE of this split (no sink: the
     // combine adds it once)
     const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
@@ -571,18 +577,53 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   float lt_ = l_sum * fo;
   if (p.sink && mm != kNegInf) lt_ += exp2f(sink2 - mm);
   const float scale_o = lt_ > 0.f ? fo / lt_ : 0.f;
-  bf16* orow = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh;
+  if (hvalid && hq == 0)
+    p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
+  if constexpr (kStageOut) {
+    // The accumulator layout gives each lane 4-dim pieces of one head, i.e.
+    // stores that touch 32 rows per instruction.  Each wave instead writes
+    // its T x DV bf16 block into a private LDS area (row pitch DV + 8, so the
+    // 8-byte writes of the 32 heads fall in distinct banks), then streams it
+    // out row by row with 16-byte stores (one 1 KB row per instruction).  The
+    // tile buffers are idle here: the last barrier of the tile loop ended
+    // every read of them and every DMA into them.
+    constexpr int SP = C::DV + 8;
+    char* stg = wave == 0 ? reinterpret_cast<char*>(s_k0)
+              : wave == 1 ? reinterpret_cast<char*>(s_k1)
+                          : reinterpret_cast<char*>(s_q) + (wave - 2) * (C::QBUF * 8);
+    bf16* srow = reinterpret_cast<bf16*>(stg) + lt * SP;
 #pragma unroll
-  for (int ot = 0; ot < C::OT; ++ot) {
+    for (int ot = 0; ot < C::OT; ++ot) {
 #pragma unroll
-    for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
-      const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
-      bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
-                   (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
-      *reinterpret_cast<bf16x4*>(orow + dim) = v4;
+      for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
+        const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
+        bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
+                     (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
+        *reinterpret_cast<bf16x4*>(srow + dim) = v4;
+      }
+    }
+    const bf16* sbase = reinterpret_cast<const bf16*>(stg);
+    bf16* obase = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)(g * p.G + slice * T) * p.o_sh;
+#pragma unroll 4
+    for (int r = 0; r < T; ++r) {
+      if (slice * T + r >= p.G) break;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(sbase + r * SP + 8 * lane);
+      *reinterpret_cast<bf16x8*>(obase + (int64_t)r * p.o_sh + 8 * lane) = v;
+    }
+  } else {
+    if (!hvalid) return;
+    bf16* orow = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh;
+#pragma unroll
+    for (int ot = 0; ot < C::OT; ++ot) {
+#pragma unroll
+      for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
+        const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
+        bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
+                     (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
+        *reinterpret_cast<bf16x4*>(orow + dim) = v4;
+      }
     }
   }
-  if (hq == 0) p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
 }
 
 // Variants: (T, DQK, DV, NSLICE, NSPLITW, V is a prefix of K)

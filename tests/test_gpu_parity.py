@@ -187,6 +187,19 @@ def test_mla_prefill_reduced(S, K):
     _check_fwd(out, lse, o_ref, l_ref)
 
 
+@pytest.mark.parametrize("Hq", [80, 96, 112])
+def test_mla_prefill_partial_head_slices(Hq):
+    """G = Hq not a multiple of the 32-head slice: the last slices hold absent
+    heads, whose lanes still take part in the staged row stores; with a sink."""
+    _say(f"mla_prefill bf16 Hq={Hq} d_qk=576 d_v=512 S=200 K=64 with sink")
+    w = make_workload("mla_prefill", device=DEV, S=200, K=64, Hq=Hq)
+    sink = torch.randn(Hq, generator=torch.Generator().manual_seed(3)).to(DEV)
+    out = torch.full(w.q.shape[:3] + (512,), float("nan"), dtype=w.q.dtype, device=DEV)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, attn_sink=sink, out=out)
+    o_ref, l_ref = ref_forward(*_cpu(w)[:4], w.scale, sink=sink.cpu())
+    _check_fwd(out, lse, o_ref, l_ref)
+
+
 def test_mla_prefill_full_sampled():
     _say("mla_prefill bf16 full S=32768 K=2048 Hq=128 (sampled rows vs oracle)")
     w = make_workload("mla_prefill", device=DEV)
