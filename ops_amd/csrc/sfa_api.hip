@@ -139,7 +139,7 @@ FwdPlan plan_fwd(const sfa_fwd_args* a) {
   pl.num_splits = splits;
   if (splits > 1) {
     const size_t rows = (size_t)a->B * a->Sq * a->Hq;
-    pl.part_o_bytes = align_up((size_t)splits * rows * a->Dv * sizeof(float), 256);
+    pl.part_o_bytes = align_up((size_t)splits * rows * a->Dv * sizeof(__bf16), 256);
     pl.part_lse_bytes = align_up((size_t)splits * rows * sizeof(float), 256);
   }
   return pl;
@@ -181,7 +181,7 @@ int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void
       if (workspace == nullptr || workspace_bytes < pl.part_o_bytes + pl.part_lse_bytes)
         return fail(SFA_E_WORKSPACE, "sfa_fwd needs %zu workspace bytes (got %zu)", pl.part_o_bytes + pl.part_lse_bytes,
                     workspace_bytes);
-      p.part_o = (float*)workspace;
+      p.part_o = (__bf16*)workspace;
       p.part_lse = (float*)((char*)workspace + pl.part_o_bytes);
     }
     e = sfa::launch_fwd_mfma(p, s);

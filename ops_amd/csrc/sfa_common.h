@@ -35,7 +35,7 @@ struct Params {
   // split-k partial results (forward, num_splits > 1)
   int num_splits;
   int split_len;      // slots per split (multiple of the key tile)
-  float* part_o;      // [num_splits][B*Sq*Hq][Dv], normalised by the split's own sum
+  __bf16* part_o;     // [num_splits][B*Sq*Hq][Dv] bf16, normalised by the split's own sum
   float* part_lse;    // [num_splits][B*Sq*Hq], base-2 log-sum-exp of the split (-inf if empty)
   // backward
   const void* dout;

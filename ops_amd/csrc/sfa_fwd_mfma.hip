@@ -550,35 +550,33 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   if (!kStageOut && !hvalid) return;
   const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
-  if (p.num_splits > 1) {
-    if (!hvalid) return;
-    // normalised partial output and base-2 LSE of this split (no sink: the
-    // combine adds it once)
-    const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
-    const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-    float* po = p.part_o + ((int64_t)split * nrows + row) * C::DV;
-#pragma unroll
-    for (int ot = 0; ot < C::OT; ++ot) {
-#pragma unroll
-      for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
-        const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
-        f32x4 v4 = {oacc[ot][4 * q4 + 0] * inv, oacc[ot][4 * q4 + 1] * inv, oacc[ot][4 * q4 + 2] * inv,
-                    oacc[ot][4 * q4 + 3] * inv};
-        *reinterpret_cast<f32x4*>(po + dim) = v4;
-      }
-    }
-    if (hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
-    return;
+  // Split partials: normalised O of this split in bf16 plus its base-2 LSE
+  // (no sink: the combine adds it once).  Final output: the sink joins the
+  // denominator (SFA.py:469-478).
+  const bool partial = p.num_splits > 1;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  float scale_o;
+  if (partial) {
+    scale_o = l_sum > 0.f ? 1.f / l_sum : 0.f;
+    if (hvalid && hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
+  } else {
+    const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+    const float mm = fmaxf(m_fin, sink2);
+    const float fo = (m_fin == kNegInf) ? 0.f : exp2f(m_fin - mm);
+    float lt_ = l_sum * fo;
+    if (p.sink && mm != kNegInf) lt_ += exp2f(sink2 - mm);
+    scale_o = lt_ > 0.f ? fo / lt_ : 0.f;
+    if (hvalid && hq == 0)
+      p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
   }
-  // final output with the optional sink in the denominator (SFA.py:469-478)
-  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
-  const float mm = fmaxf(m_fin, sink2);
-  const float fo = (m_fin == kNegInf) ? 0.f : exp2f(m_fin - mm);
-  float lt_ = l_sum * fo;
-  if (p.sink && mm != kNegInf) lt_ += exp2f(sink2 - mm);
-  const float scale_o = lt_ > 0.f ? fo / lt_ : 0.f;
-  if (hvalid && hq == 0)
-    p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
+  // destination of the group's first head row, the same for every lane
+  // (lanes of absent heads included: they take part in the staged stores):
+  // output (strided) or partial buffer (dense); head hl's row is obase +
+  // hl * orstride
+  const int64_t row0 = ((int64_t)b * p.Sq + t) * p.Hq + (int64_t)g * p.G;
+  bf16* const obase = partial ? p.part_o + ((int64_t)split * nrows + row0) * C::DV
+                              : reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)(g * p.G) * p.o_sh;
+  const int64_t orstride = partial ? C::DV : p.o_sh;
   if constexpr (kStageOut) {
     // The accumulator layout gives each lane 4-dim pieces of one head, i.e.
     // stores that touch 32 rows per instruction.  Each wave instead writes
@@ -603,16 +601,16 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       }
     }
     const bf16* sbase = reinterpret_cast<const bf16*>(stg);
-    bf16* obase = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)(g * p.G + slice * T) * p.o_sh;
+    bf16* const wbase = obase + (int64_t)(slice * T) * orstride;
 #pragma unroll 4
     for (int r = 0; r < T; ++r) {
       if (slice * T + r >= p.G) break;
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(sbase + r * SP + 8 * lane);
-      *reinterpret_cast<bf16x8*>(obase + (int64_t)r * p.o_sh + 8 * lane) = v;
+      *reinterpret_cast<bf16x8*>(wbase + (int64_t)r * orstride + 8 * lane) = v;
     }
   } else {
     if (!hvalid) return;
-    bf16* orow = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh;
+    bf16* orow = obase + (int64_t)hl * orstride;
 #pragma unroll
     for (int ot = 0; ot < C::OT; ++ot) {
 #pragma unroll

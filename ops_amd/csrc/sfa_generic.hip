@@ -224,7 +224,8 @@ __global__ void finish_kernel(const float* acc, int B, int Skv, int Hkv, int D, 
   }
 }
 
-// Split-k combine: lse2 = log2 Σ_s 2^lse2_s, out = Σ_s 2^(lse2_s - lse2)·o_s,
+// Split-k combine: lse2 = log2 Σ_s 2^lse2_s, out = Σ_s 2^(lse2_s - lse2)·o_s
+// (o_s the bf16 normalised partial of split s, accumulated in fp32),
 // then the optional sink joins the denominator.  One wave per (b, t, h) row:
 // the per-split weights are computed once per row (lane s), the partial rows
 // are read as float4.
@@ -247,22 +248,26 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const float wl = e * inv;  // weight of split `lane`
   T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
-  if ((p.Dv & 3) == 0) {
-    for (int d = 4 * lane; d < p.Dv; d += 256) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if ((p.Dv & 7) == 0) {
+    for (int d = 8 * lane; d < p.Dv; d += 512) {
+      float acc[8] = {};
       for (int s = 0; s < p.num_splits; ++s) {
         const float w = __shfl(wl, s, 64);
-        if (w != 0.f) acc += w * *reinterpret_cast<const f32x4*>(p.part_o + (s * nrows + row) * p.Dv + d);
+        if (w != 0.f) {
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(p.part_o + (s * nrows + row) * p.Dv + d);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += w * (float)v[j];
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) orow[d + j] = from_f32<T>(acc[j]);
+      for (int j = 0; j < 8; ++j) orow[d + j] = from_f32<T>(acc[j]);
     }
   } else {
     for (int d = lane; d < p.Dv; d += 64) {
       float acc = 0.f;
       for (int s = 0; s < p.num_splits; ++s) {
         const float w = __shfl(wl, s, 64);
-        if (w != 0.f) acc += w * p.part_o[(s * nrows + row) * p.Dv + d];
+        if (w != 0.f) acc += w * (float)p.part_o[(s * nrows + row) * p.Dv + d];
       }
       orow[d] = from_f32<T>(acc);
     }
