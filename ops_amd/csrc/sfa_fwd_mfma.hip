@@ -221,7 +221,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const int hl = slice * T + (lane % T);  // head within the group
   const bool hvalid = hl < p.G;
   bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
-  {
+  // (issued after the first tile's gather, so the two latencies overlap)
+  auto load_q = [&]() {
     const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
                        (int64_t)(g * p.G + (hvalid ? hl : 0)) * p.q_sh + 8 * (lane / T);
 #pragma unroll
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       if (!hvalid) x = bf16x8{};
       *reinterpret_cast<bf16x8*>(&s_q[hl * C::QLP + (s - C::QREG) * C::LG + lane / T]) = x;
     }
-  }
+  };
 
   // ---- gather setup --------------------------------------------------------
   const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
@@ -459,7 +460,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 
   __syncthreads();  // indices staged
   if (ntiles > 0) gather(0, s_k0, s_v0);
-  __syncthreads();
+  load_q();
+  __syncthreads();  // first tile and the LDS part of Q in place
 
   // row offsets of the next tile to gather (kSpread), read from s_idx ahead
   // of the tile whose MFMA stream issues that gather, just before a barrier
