@@ -50,8 +50,9 @@ constexpr int kIdxCap = 2048;  // slots staged in LDS per work item
 #define MLA_QREG 18
 #endif
 
-template <int T_, int DQK_, int DV_, int NSLICE_, int NSPLITW_, bool VK_, int QREG_>
+template <int T_, int DQK_, int DV_, int NSLICE_, int NSPLITW_, bool VK_, int QREG_, bool SWZ_ = false>
 struct FwdCfg {
+  static constexpr bool SWZ = SWZ_;         // k tile: pitch CHK, chunks swizzled by row (tile_swz)
   static constexpr int T = T_;
   static constexpr int DQK = DQK_;
   static constexpr int DV = DV_;
@@ -73,7 +74,7 @@ struct FwdCfg {
   static constexpr int OT = DV / T;
   static constexpr int CHK = DQK / 8;       // 16-byte chunks per k row
   static constexpr int CHV = DV / 8;
-  static constexpr int PK = CHK + 1;        // LDS row pitch in 16-byte slots (odd)
+  static constexpr int PK = SWZ ? CHK : CHK + 1;  // LDS row pitch in 16-byte slots (odd unless swizzled)
   static constexpr int PV = CHV + 1;
   static constexpr int KBUF = NKT * PK;     // 16-byte slots per k tile
   static constexpr int VBUF = VK ? 0 : NKT * PV;
@@ -257,7 +258,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // Wide-row configs (v inside the k rows) issue the next tile's gather from
   // inside the current tile's S^T MFMA stream instead of in one burst.
   constexpr bool kSpread = C::VK && C::PK >= 64 && C::T == 32 && C::NKT % C::kWaves == 0;
-  typedef RowGather<(kSpread ? C::NKT : 32), (kSpread ? C::CHK : 72), (kSpread ? C::kWaves : 4)> RG;
+  typedef RowGather<(kSpread ? C::NKT : 32), (kSpread ? C::CHK : 72), (kSpread ? C::kWaves : 4), C::SWZ> RG;
+  static_assert(!C::SWZ || kSpread, "swizzled tiles are gathered by RowGather");
+  static_assert(!kSpread || RG::PITCH == C::PK, "gather and readers agree on the pitch");
   // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
   // tile's MFMA sequence (QSTEPS S^T MFMAs, then the O^T MFMAs)
 #ifndef SFA_DMA_STRIDE
@@ -302,8 +305,21 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     if constexpr (T == 32) {
       // one 32-key M-tile: operands of step s + PDK are loaded before MFMA s
       constexpr int PDK = 4;
-      const uint32_t k_off = (uint32_t)((ks * 32 + lt) * C::PK + hq) * 16u;
-      auto load_k = [&](int s) { return lds_read_b128(kt, k_off + (uint32_t)(s * C::LG) * 16u); };
+      // (swizzled tile: step s reads chunk 2s + hq = 8 (s >> 2) + v with
+      // v = 2 (s & 3) + hq at slot 8 (s >> 2) + (v ^ swz(row)): four bases)
+      uint32_t kb[C::SWZ ? 4 : 1];
+      if constexpr (C::SWZ) {
+        static_assert(C::LG == 2, "swizzled tiles are read with 32x32x16 operands");
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          kb[j] = (uint32_t)((ks * 32 + lt) * C::PK + ((2 * j + hq) ^ tile_swz(ks * 32 + lt))) * 16u;
+      } else {
+        kb[0] = (uint32_t)((ks * 32 + lt) * C::PK + hq) * 16u;
+      }
+      auto load_k = [&](int s) {
+        if constexpr (C::SWZ) return lds_read_b128(kt, kb[s & 3] + (uint32_t)(s >> 2) * 128u);
+        else return lds_read_b128(kt, kb[0] + (uint32_t)(s * C::LG) * 16u);
+      };
       auto load_q = [&](int s) { return lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u); };
       bf16x8 kbuf[PDK], qbuf[PDK];
 #pragma unroll
@@ -428,13 +444,40 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
     const int run0 = (T == 32) ? 4 * hq : 4 * hq;
     const int run1 = (T == 32) ? 8 + 4 * hq : 16 + 4 * hq;
-    const uint32_t base0 = (uint32_t)((ks * 32 + run0 + rr) * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
-    const uint32_t base1 = (uint32_t)((ks * 32 + run1 + rr) * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
+    // Unswizzled: operand (kk, ot) of a lane reads base + 16 kk rows + 32 ot
+    // dims.  Swizzled (T = 32): the lane's dims ot*32 + mgrp + 4cc .. +3 are
+    // in chunk 4 ot + cl, cl = mgrp / 8 + cc / 2, i.e. chunk 8 (ot >> 1) + v
+    // with v = 4 (ot & 1) + cl, at slot 8 (ot >> 1) + (v ^ swz(row)); rows
+    // r and r + 16 share swz, so each run needs one base per parity of ot.
+    uint32_t vb[2][C::SWZ ? 2 : 1];
+    {
+      const int rows[2] = {ks * 32 + run0 + rr, ks * 32 + run1 + rr};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (C::SWZ) {
+          const int cl = mgrp / 8 + cc / 2;
+#pragma unroll
+          for (int par = 0; par < 2; ++par)
+            vb[h][par] = (uint32_t)(rows[h] * VP + ((4 * par + cl) ^ tile_swz(rows[h]))) * 16u + (uint32_t)(cc & 1) * 8u;
+        } else {
+          vb[h][0] = (uint32_t)(rows[h] * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
+        }
+      }
+    }
     auto load_a = [&](int i) -> bf16x8 {
       const int kk = i / C::OT, ot = i % C::OT;
-      const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot * T) * 2u;  // T == 32 only has kk > 0
-      const bf16x4 lo = lds_read_tr16(vt, base0 + off);
-      const bf16x4 hi = lds_read_tr16(vt, base1 + off);
+      uint32_t o0, o1;
+      if constexpr (C::SWZ) {
+        const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot >> 1) * 128u;
+        o0 = vb[0][ot & 1] + off;
+        o1 = vb[1][ot & 1] + off;
+      } else {
+        const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot * T) * 2u;  // T == 32 only has kk > 0
+        o0 = vb[0][0] + off;
+        o1 = vb[1][0] + off;
+      }
+      const bf16x4 lo = lds_read_tr16(vt, o0);
+      const bf16x4 hi = lds_read_tr16(vt, o1);
       return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
     constexpr int NI = KSTEPS * C::OT;
@@ -459,7 +502,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   };
 
   __syncthreads();  // indices staged
-  if (ntiles > 0) gather(0, s_k0, s_v0);
+  if constexpr (kSpread) {
+    RG rg0;
+    rg0.load_ids(s_idx, ntiles > 0, wave, krow_bytes);
+#pragma unroll
+    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, rk, s_k0, wave, lane);
+  } else {
+    if (ntiles > 0) gather(0, s_k0, s_v0);
+  }
   load_q();
   __syncthreads();  // first tile and the LDS part of Q in place
 
@@ -627,7 +677,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 }
 
 // Variants: (T, DQK, DV, NSLICE, NSPLITW, V is a prefix of K)
-using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG>;  // DeepSeek MLA: G = 128, d_qk 576 / d_v 512
+using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;  // DeepSeek MLA: G = 128, d_qk 576 / d_v 512
 using CfgD128G16 = FwdCfg<16, 128, 128, 1, 4, false, 4>;    // d = 128, G <= 16
 
 template <class C>

@@ -73,31 +73,51 @@ __device__ __forceinline__ void gather_tile(const int* ib, u32x4* dst, const __a
   }
 }
 
-// Row-wise gather for wide rows (PITCH = CH + 1 >= 64 slots, so one 64-lane
+// Chunk swizzle of the MLA tile (row pitch 72 16-byte slots, no pad): row r
+// stores its chunk c at slot position c ^ swz(r), swz(r) < 8 built from bits
+// 1..3 of r.  With it both operand read patterns are bank-conflict free
+// (64 banks x 4 bytes; 256 bytes per pass):
+//  * S^T A operands (ds_read_b128): a 16-lane pass reads one chunk of 16
+//    consecutive rows;
+//  * O^T A operands (ds_read_b64_tr_b16): a 32-lane pass reads 4 consecutive
+//    rows x 4 consecutive chunks (an aligned group of 4);
+// the unswizzled pitch-73 layout makes the second pattern 2-way conflicted
+// and a pitch of 72 without swizzle makes the first 8-way conflicted.  The
+// swizzle never moves a chunk out of its aligned group of 8, so it commutes
+// with adding multiples of 8 to a chunk index.
+__device__ __forceinline__ int tile_swz(int r) {
+  return (((r >> 1) & 1) << 2) ^ ((r >> 2) & 1) ^ (((r >> 3) & 1) << 1);
+}
+
+// Row-wise gather for wide rows (PITCH >= 64 slots, so one 64-lane
 // instruction spans at most two rows).  Wave w gathers tile rows
 // [w * RPW, (w + 1) * RPW), i.e. the contiguous slot range [w * SPW, (w+1) * SPW).
 // For instruction k every slot position is a compile-time constant, and the
 // two row byte offsets it needs are wave-uniform scalars, so issuing one
-// instruction costs two VALU operations and no per-lane index reads:
-//   voffset(lane) = 16 * lane + (lane < bnd ? S0 : S1)
+// instruction costs a few VALU operations and no per-lane index reads:
+//   voffset(lane) = lane < bnd ? S0 + X0 : S1 + X1
 //   S0 = base[r0] + 16 * c0,  S1 = base[r0 + 1] + 16 * (c0 - PITCH)
-// with r0, c0 the row / chunk of the instruction's first slot and bnd the
-// lanes left in row r0.  base[r] is id * row_bytes, or kOOBRow for a padding
-// row, which keeps every offset of that row above 2^31 (out of range, the
-// hardware writes zeros).  The pad slot of a row reads the 16 bytes after the
-// row (the next row's first chunk, or zeros past the end of the range); pad
-// slots are never read.  Instructions can be issued one at a time (issue(k)),
-// so a caller can spread them over its MFMA stream.
+//   Xi = 16 * (lane ^ swz(row i))            (16 * lane without swizzle)
+// with r0, c0 the row / slot of the instruction's first slot and bnd the
+// lanes left in row r0 (with the swizzle c0 is a multiple of 8, so the lane at
+// slot c0 + lane loads chunk c0 + (lane ^ swz)).  base[r] is id * row_bytes,
+// or kOOBRow for a padding row, which keeps every offset of that row above
+// 2^31 (out of range, the hardware writes zeros).  Without the swizzle the
+// row has one pad slot (PITCH = CH + 1), which reads the 16 bytes after the
+// row (the next row's first chunk, or zeros past the end of the range) and is
+// never read.  Instructions can be issued one at a time (issue(k)), so a
+// caller can spread them over its MFMA stream.
 constexpr uint32_t kOOBRow = 0x80001000u;
 
-template <int NKT, int CH, int NWAVES>
+template <int NKT, int CH, int NWAVES, bool SWZ>
 struct RowGather {
-  static constexpr int PITCH = CH + 1;
+  static constexpr int PITCH = SWZ ? CH : CH + 1;
   static constexpr int RPW = NKT / NWAVES;       // rows per wave
   static constexpr int SPW = RPW * PITCH;        // slots per wave
   static constexpr int NI = (SPW + 63) / 64;     // instructions per wave
   static_assert(PITCH >= 64, "an instruction must span at most two rows");
   static_assert(NKT % NWAVES == 0, "rows split evenly over the waves");
+  static_assert(!SWZ || (PITCH % 8 == 0 && CH % 8 == 0), "swizzled rows are whole groups of 8 chunks");
 
   uint32_t base[RPW];
 
@@ -119,13 +139,14 @@ struct RowGather {
     const int s0 = 64 * k;
     const int r0 = s0 / PITCH, c0 = s0 % PITCH;
     const int bnd = PITCH - c0;
-    const uint32_t S0 = base[r0] + 16u * (uint32_t)c0;
-    uint32_t off = S0;
+    const uint32_t l16 = 16u * (uint32_t)lane;
+    const uint32_t x0 = SWZ ? l16 ^ (16u * (uint32_t)tile_swz(wave * RPW + r0)) : l16;
+    uint32_t off = base[r0] + 16u * (uint32_t)c0 + x0;
     if (bnd < 64 && r0 + 1 < RPW) {
-      const uint32_t S1 = base[r0 + 1] + 16u * (uint32_t)c0 - 16u * (uint32_t)PITCH;
-      off = lane < bnd ? S0 : S1;
+      const uint32_t x1 = SWZ ? l16 ^ (16u * (uint32_t)tile_swz(wave * RPW + r0 + 1)) : l16;
+      const uint32_t o1 = base[r0 + 1] + 16u * (uint32_t)c0 - 16u * (uint32_t)PITCH + x1;
+      off = lane < bnd ? off : o1;
     }
-    off += 16u * (uint32_t)lane;
     u32x4* d = dst + wave * SPW + s0;
     if (s0 + 64 <= SPW) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)d, 16, off, 0, 0, 0);
