@@ -199,13 +199,40 @@ int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void
   return SFA_OK;
 }
 
-size_t sfa_bwd_workspace_size(const sfa_bwd_args* a) {
-  if (a == nullptr || check_fwd(&a->fwd) != SFA_OK) return 0;
-  const sfa_fwd_args& f = a->fwd;
+}  // extern "C"
+
+namespace {
+
+// dK/dV scheme actually used: CSR (deterministic) when requested or, for
+// AUTO, whenever the shape has the key-major kernel; otherwise atomics.
+bool use_csr(const sfa_bwd_args* a, sfa::Params p) {
+  if (a->dkv_mode == SFA_DKV_ATOMIC) return false;
+  p.do_sb = a->do_sb;  // (the range checks also cover dout)
+  p.do_ss = a->do_ss;
+  p.do_sh = a->do_sh;
+  return bwd_mfma_ok(a) && sfa::bwd_csr_supported(p);
+}
+
+size_t bwd_base_bytes(const sfa_fwd_args& f) {
   const size_t dk = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dqk * sizeof(float), 256);
   const size_t dv = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dv * sizeof(float), 256);
   const size_t delta = align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
   return dk + dv + delta;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sfa_bwd_workspace_size(const sfa_bwd_args* a) {
+  if (a == nullptr || check_fwd(&a->fwd) != SFA_OK) return 0;
+  size_t n = bwd_base_bytes(a->fwd);
+  sfa::Params p = to_params(&a->fwd);
+  if (use_csr(a, p)) {
+    sfa::csr_geometry(p);
+    n += sfa::csr_workspace_bytes(p);
+  }
+  return n;
 }
 
 int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
@@ -219,12 +246,16 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
   if (a->dkv_mode != SFA_DKV_AUTO && a->dkv_mode != SFA_DKV_ATOMIC && a->dkv_mode != SFA_DKV_CSR)
     return fail(SFA_E_INVALID, "unknown dkv_mode %d", a->dkv_mode);
-  if (a->dkv_mode == SFA_DKV_CSR) return fail(SFA_E_UNSUPPORTED, "SFA_DKV_CSR is not available in this build");
   const size_t need = sfa_bwd_workspace_size(a);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(SFA_E_WORKSPACE, "sfa_bwd needs %zu workspace bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
   sfa::Params p = to_params(&f);
+  const bool csr = use_csr(a, p);
+  if (a->dkv_mode == SFA_DKV_CSR && !csr)
+    return fail(SFA_E_UNSUPPORTED,
+                "SFA_DKV_CSR needs bf16, d_qk = d_v = 128, G in {1, 2, 4, 8, 16}, top-k <= 2048 and "
+                "row offsets below 2^31 bytes");
   if (!(bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p)) && f.topk > kGenericMaxTopk)
     return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d", f.topk, kGenericMaxTopk);
   p.dout = a->dout; p.do_sb = a->do_sb; p.do_ss = a->do_ss; p.do_sh = a->do_sh;
@@ -235,17 +266,23 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   p.delta = (float*)((char*)p.dv_acc + align_up(nv * sizeof(float), 256));
   p.dsink = a->dsink;
   p.dlse = a->dlse;
+  if (csr) {
+    sfa::csr_geometry(p);
+    sfa::csr_bind_workspace(p, (char*)workspace + bwd_base_bytes(f));
+  }
 
   hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
   if (e == hipSuccess) e = sfa::launch_zero_f32(p.dv_acc, nv, s);
   if (e == hipSuccess && p.dsink) e = sfa::launch_zero_f32(p.dsink, (size_t)f.Hq, s);
   if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
+  if (e == hipSuccess && csr) e = sfa::launch_csr_index(p, s);  // before dQ: it reads the repeat flags
   if (e == hipSuccess) {
     if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
       e = sfa::launch_bwd_mfma(p, s);
     else
       e = sfa::launch_bwd_generic(p, f.dtype, s);
   }
+  if (e == hipSuccess && csr) e = sfa::launch_csr_dkv(p, s);
   if (e == hipSuccess)
     e = sfa::launch_bwd_finish(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, a->dv, a->dv_sb, a->dv_ss, a->dv_sh,
                                s);

@@ -1,0 +1,483 @@
+// Deterministic dK/dV for the gfx950 sparse flash attention backward
+// (SFA_DKV_CSR), d_qk = d_v = 128 and G = 1, 2, 4, 8 or 16 query heads per
+// KV head.
+//
+// Reference: `_attn_bwd_dk_dv` / `_inner_dkv` (SFA.py:1005-1145, 719-853)
+// gathers, per query tile, the selected K/V rows and scatters dK/dV with
+// atomics (SFA.py:849-853).  This path produces the same sums without
+// atomics and in a fixed order:
+//
+//  1. Index inversion.  A membership bitmap kmap[b][g][t] (bit k = key k is
+//     selected by query t) is built from the index rows; a slot whose key
+//     already has its bit (a repeated key in one row) is flagged in `dup`
+//     and its contribution is added by the query-major kernel with atomics
+//     instead (repeats are the only non-deterministic case; the workloads
+//     have none).  Then, for every key block of 128 keys, the ascending list
+//     of query blocks (128 query-head rows = 128 / G queries) that select at
+//     least one of its keys (`blist`, a per-key-block CSR at block
+//     granularity).
+//  2. Key-major recompute.  One workgroup owns a key block (each wave 32
+//     keys, K and V rows kept in registers) and a chunk of up to kChunk of
+//     its query blocks.  Per query block it recomputes, for every (row, key)
+//     pair of the block, S = Q K^T and dP = dO V^T (32x32x16 MFMA, rows as
+//     M, keys as N), P = 2^(S scale log2e - lse2) and dS = P (dP - δ) masked
+//     by the bitmap, and accumulates dV^T += dO^T P and dK^T += Q^T dS in
+//     AGPRs (the C layout of S is the B layout of these products; the A
+//     operands are transposing LDS reads of 4-row runs in the matching
+//     order).  Pairs that are not selected get P = 0, so a block costs the
+//     same whatever its density.
+//  3. Reduction.  The chunks of a key block write fp32 partials; a reduction
+//     kernel adds them in chunk order into the per-key accumulators.
+
+#include "sfa_common.h"
+#include "sfa_lds.h"
+#include "sfa_mfma.h"
+
+namespace sfa {
+namespace {
+
+constexpr int kKeyBlock = 128;          // keys per key block (4 waves x 32)
+constexpr int kRowBlock = 128;          // query-head rows per query block
+constexpr int kChunk = 128;             // query blocks per workgroup
+constexpr int kD = 128;                 // head dim (d_qk = d_v)
+constexpr int kCH = kD / 8;             // 16-byte chunks per row
+constexpr int kTB = kRowBlock * kCH;    // slots per Q or dO block buffer
+static_assert(kTB % 64 == 0 && kCH == 16, "block buffers: 4 rows per DMA instruction");
+
+// Q / dO block rows are stored unpadded (16 slots) with chunk c of row r at
+// slot c ^ blk_swz(r).  Both operand read patterns are then bank-conflict
+// free (64 banks x 4 bytes, 256 bytes per pass):
+//  * b128 reads of one chunk of 16 consecutive rows (S / dP A operands):
+//    blk_swz is a bijection on every 16 consecutive rows;
+//  * transposing reads of 4 consecutive rows x an aligned group of 4 chunks
+//    (dV / dK A operands): blk_swz(4m + i) = 4 i + (m & 3) sends the group of
+//    each of the 4 rows to a different group.
+__device__ __forceinline__ int blk_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// ---- 1a. membership bitmap and repeated-slot flags ------------------------
+__global__ __launch_bounds__(256) void csr_scatter_kernel(Params p) {
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.topk;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int s = (int)(i % p.topk);
+    int64_t r = i / p.topk;
+    const int g = (int)(r % p.Hkv);
+    r /= p.Hkv;
+    const int t = (int)(r % p.Sq);
+    const int b = (int)(r / p.Sq);
+    const int id = p.idx[b * p.i_sb + t * p.i_ss + g * p.i_sh + s];
+    uint8_t rep = 0;
+    if (id >= 0 && id < bound_of(p, b)) {
+      uint32_t* w = p.kmap + (((int64_t)b * p.Hkv + g) * p.Sq + t) * p.kmap_w + (id >> 5);
+      const uint32_t bit = 1u << (id & 31);
+      rep = (atomicOr(w, bit) & bit) ? 1 : 0;
+    }
+    p.dup[i] = rep;
+  }
+}
+
+// ---- 1b. per key block: ascending list of non-empty query blocks -----------
+__global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
+  __shared__ int s_cnt[4];
+  int wi = blockIdx.x;
+  const int kb = wi % p.nkb;
+  wi /= p.nkb;
+  const int g = wi % p.Hkv;
+  const int b = wi / p.Hkv;
+  const int nq = kRowBlock >> p.lg_g;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t* mrow = p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4;
+  const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
+  int* list = p.blist + bgk * p.nqb;
+  int total = 0;
+  for (int q0 = 0; q0 < p.nqb; q0 += 256) {
+    const int qb = q0 + tid;
+    bool any = false;
+    if (qb < p.nqb) {
+      const int t0 = qb * nq;
+      const int t1 = min(p.Sq, t0 + nq);
+      for (int t = t0; t < t1 && !any; ++t) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(mrow + (int64_t)t * p.kmap_w);
+        any = (w.x | w.y | w.z | w.w) != 0u;
+      }
+    }
+    const uint64_t m = __ballot(any);
+    if (lane == 0) s_cnt[wave] = __popcll(m);
+    __syncthreads();
+    int pos = total + __popcll(m & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) pos += s_cnt[w];
+    if (any) list[pos] = qb;
+    total += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+    __syncthreads();
+  }
+  if (tid == 0) p.bcount[bgk] = total;
+}
+
+// ---- 2. key-major dK / dV ---------------------------------------------------
+// LDS: Q and dO blocks double buffered (row r = query (r >> lg_g), head
+// (r & (G - 1)); swizzled, see blk_swz), each row's lse and δ, and per wave the
+// bitmap word of its 32 keys for each row.  Buffers are separate arrays so
+// reads of one are not made to wait for DMA into the other.
+__global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
+  typedef Mfma<32> M;
+  typedef M::acc_t acc_t;
+  __shared__ u32x4 s_q0[kTB];
+  __shared__ u32x4 s_q1[kTB];
+  __shared__ u32x4 s_d0[kTB];
+  __shared__ u32x4 s_d1[kTB];
+  __shared__ __attribute__((aligned(16))) float s_lse0[kRowBlock];
+  __shared__ __attribute__((aligned(16))) float s_lse1[kRowBlock];
+  __shared__ __attribute__((aligned(16))) float s_dlt0[kRowBlock];
+  __shared__ __attribute__((aligned(16))) float s_dlt1[kRowBlock];
+  __shared__ __attribute__((aligned(16))) uint32_t s_msk0[4][kRowBlock];
+  __shared__ __attribute__((aligned(16))) uint32_t s_msk1[4][kRowBlock];
+  __shared__ int s_list[kChunk];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int wi = blockIdx.x;
+  const int c = wi % p.max_chunks;
+  wi /= p.max_chunks;
+  const int kb = wi % p.nkb;
+  wi /= p.nkb;
+  const int g = wi % p.Hkv;
+  const int b = wi / p.Hkv;
+  const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
+  const int cnt = p.bcount[bgk];
+  const int e0 = c * kChunk;
+  if (e0 >= cnt) return;  // the whole workgroup: no query block in this chunk
+  const int nblk = min(kChunk, cnt - e0);
+  for (int i = tid; i < nblk; i += 256) s_list[i] = p.blist[bgk * p.nqb + e0 + i];
+
+  const int G = p.G, lg = p.lg_g;
+  const int nq = kRowBlock >> lg;
+  const int n = lane & 31, g2 = lane >> 5;
+  const int key = kb * kKeyBlock + wave * 32 + n;
+
+  // K and V rows of the lane's key as the B operands of S = Q K^T and
+  // dP = dO V^T: step s holds dims 16 s + 8 g2 .. +7 (keys past Skv: zeros)
+  bf16x8 kB[kD / 16], vB[kD / 16];
+  {
+    const bool ok = key < p.Skv;
+    const bf16* kr = reinterpret_cast<const bf16*>(p.k) + b * p.k_sb + (int64_t)(ok ? key : 0) * p.k_ss +
+                     g * p.k_sh + 8 * g2;
+    const bf16* vr = reinterpret_cast<const bf16*>(p.v) + b * p.v_sb + (int64_t)(ok ? key : 0) * p.v_ss +
+                     g * p.v_sh + 8 * g2;
+#pragma unroll
+    for (int s = 0; s < kD / 16; ++s) {
+      kB[s] = ok ? *reinterpret_cast<const bf16x8*>(kr + 16 * s) : bf16x8{};
+      vB[s] = ok ? *reinterpret_cast<const bf16x8*>(vr + 16 * s) : bf16x8{};
+    }
+  }
+
+  // buffer resources (ranges checked on the host to fit 31 bits)
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+      reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + (int64_t)(g * G) * p.q_sh,
+      (uint32_t)(2 * ((int64_t)(p.Sq - 1) * p.q_ss + (int64_t)(G - 1) * p.q_sh + kD)));
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(
+      reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + (int64_t)(g * G) * p.do_sh,
+      (uint32_t)(2 * ((int64_t)(p.Sq - 1) * p.do_ss + (int64_t)(G - 1) * p.do_sh + kD)));
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(
+      p.lse + b * p.l_sb + (int64_t)(g * G) * p.l_sh,
+      (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.l_ss + (int64_t)(G - 1) * p.l_sh + 1)));
+  const __amdgpu_buffer_rsrc_t rdl = make_rsrc(
+      p.delta + (int64_t)b * p.Sq * p.Hq + g * G, (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.Hq + G)));
+  const __amdgpu_buffer_rsrc_t rm = make_rsrc(
+      p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4,
+      (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.kmap_w + 4)));
+
+  // Query block qb into one set of buffers: Q / dO rows (32 instructions
+  // each, 4 rows per instruction, wave w issues instructions w, w + 4, ...),
+  // lse (wave 0), δ (wave 1), each wave its bitmap words.  Rows of queries
+  // >= Sq read out of range (zeros); such rows have an all-zero mask, so they
+  // contribute nothing.
+  // A block load in steps: step k < 8 issues Q and dO instruction 4 k + wave,
+  // steps 8 and 9 the lse / δ / mask rows 64 (k - 8) .. +63.  (Spreading the
+  // steps over the previous block's MFMA stream measured slower than the
+  // burst.)
+  constexpr int kLoadSteps = kTB / 64 / 4 + kRowBlock / 64;
+  auto load_step = [&](int step, int qb, u32x4* qd, u32x4* dd, float* ls, float* dl, uint32_t (*mk)[kRowBlock]) {
+    const int t0 = qb * nq;
+    if (step < kTB / 64 / 4) {
+      const int ki = 4 * step + wave;
+      const int r = 4 * ki + (lane >> 4);
+      const int cc = (lane & 15) ^ blk_swz(r);  // slot lane & 15 of row r holds chunk cc
+      const int t = t0 + (r >> lg), h = r & (G - 1);
+      const bool ok = t < p.Sq;
+      const uint32_t oq = ok ? (uint32_t)(2 * (t * p.q_ss + h * p.q_sh) + 16 * cc) : kOOB;
+      const uint32_t od = ok ? (uint32_t)(2 * (t * p.do_ss + h * p.do_sh) + 16 * cc) : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(qd + 64 * ki), 16, oq, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(dd + 64 * ki), 16, od, 0, 0, 0);
+    } else {
+      const int k2 = step - kTB / 64 / 4;
+      const int r = 64 * k2 + lane;
+      const int t = t0 + (r >> lg), h = r & (G - 1);
+      const bool ok = t < p.Sq;
+      if (wave == 0) {
+        const uint32_t o = ok ? (uint32_t)(4 * (t * p.l_ss + h * p.l_sh)) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void*)(ls + 64 * k2), 4, o, 0, 0, 0);
+      } else if (wave == 1) {
+        const uint32_t o = ok ? (uint32_t)(4 * (t * p.Hq + h)) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rdl, (lds_void*)(dl + 64 * k2), 4, o, 0, 0, 0);
+      }
+      const uint32_t om = ok ? (uint32_t)(4 * (t * p.kmap_w + wave)) : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)(&mk[wave][64 * k2]), 4, om, 0, 0, 0);
+    }
+  };
+  auto load_block = [&](int qb, u32x4* qd, u32x4* dd, float* ls, float* dl, uint32_t (*mk)[kRowBlock]) {
+#pragma unroll
+    for (int k = 0; k < kLoadSteps; ++k) load_step(k, qb, qd, dd, ls, dl, mk);
+  };
+
+  acc_t dkacc[kD / 32], dvacc[kD / 32];
+#pragma unroll
+  for (int d = 0; d < kD / 32; ++d) {
+    dkacc[d] = acc_t{};
+    dvacc[d] = acc_t{};
+  }
+
+  // Per-lane LDS byte offsets (tile row 0; rows of the tile add immediates).
+  // S / dP A operand of step s: row n, chunk 2 s + g2.
+  uint32_t aofs[kD / 16];
+#pragma unroll
+  for (int st = 0; st < kD / 16; ++st) aofs[st] = (uint32_t)(n * kCH + ((2 * st + g2) ^ blk_swz(n))) * 16u;
+  // dV / dK A operands (transposing reads): lane group gi of each 16 lanes
+  // loads row run + (gi >> 2), dims 32 d + mgrp + 4 (gi & 3) .. +3, i.e. chunk
+  // 4 d + cl with cl = mgrp / 8 + (gi & 3) / 2, bytes 8 (gi & 1) on; the runs
+  // are rows 4 g2 + rr and 4 g2 + rr + 8 (plus 32 mt + 16 kk, which leave
+  // blk_swz unchanged)
+  uint32_t vofs[2][kD / 32];
+  {
+    const int gi = lane & 15, rr = gi >> 2, cc4 = gi & 3, mgrp = (n >> 4) << 4;
+    const int cl = mgrp / 8 + cc4 / 2;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 4 * g2 + rr + 8 * hh;
+#pragma unroll
+      for (int d = 0; d < kD / 32; ++d)
+        vofs[hh][d] = (uint32_t)(row * kCH + ((4 * d + cl) ^ blk_swz(row))) * 16u + (uint32_t)(cc4 & 1) * 8u;
+    }
+  }
+  auto compute = [&](const u32x4* qt, const u32x4* dt, const float* ls, const float* dl,
+                     const uint32_t (*mk)[kRowBlock]) {
+    const uint32_t* msk = mk[wave];
+    bf16x8 prev_a = {}, prev_b = {};
+#pragma unroll 1
+    for (int mt = 0; mt < kRowBlock / 32; ++mt) {
+      const uint32_t mrow = (uint32_t)(32 * mt * kCH) * 16u;
+      // S, dP for rows 32 mt .. +31: two interleaved VGPR chains (inline-asm
+      // MFMAs, so the operand reads of step st + PDK stay ahead of the MFMAs
+      // of step st)
+      acc_t sacc, dpacc;
+      {
+        constexpr int NS = kD / 16, PDK = 4;
+        bf16x8 qa[PDK], da[PDK];
+#pragma unroll
+        for (int i = 0; i < PDK; ++i) {
+          qa[i] = lds_read_b128(qt, aofs[i] + mrow);
+          da[i] = lds_read_b128(dt, aofs[i] + mrow);
+        }
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+          const bf16x8 aq = qa[st % PDK], ad = da[st % PDK];
+          if (st + PDK < NS) {
+            qa[st % PDK] = lds_read_b128(qt, aofs[st + PDK] + mrow);
+            da[st % PDK] = lds_read_b128(dt, aofs[st + PDK] + mrow);
+          }
+          if (st == 0) {
+            M::mma_v0k(aq, kB[0], sacc, prev_a, prev_b);
+            M::mma_v0k(ad, vB[0], dpacc, aq, kB[0]);
+          } else {
+            M::mma_v(aq, kB[st], sacc, prev_a, prev_b);
+            M::mma_v(ad, vB[st], dpacc, aq, kB[st]);
+          }
+          prev_a = ad;
+          prev_b = vB[st];
+        }
+        M::drain_v2(sacc, dpacc, prev_a, prev_b);
+      }
+      // P and dS; C-layout element e is row 32 mt + 8 (e / 4) + 4 g2 + e % 4
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r0 = 32 * mt + 8 * q + 4 * g2;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + r0);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + r0);
+        const u32x4 m4 = *reinterpret_cast<const u32x4*>(msk + r0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e = 4 * q + j;
+          const bool mem = (m4[j] >> n) & 1u;
+          const float pr = mem ? __builtin_amdgcn_exp2f(fmaf(sacc[e], p.scale_log2, -l4[j] * kLog2e)) : 0.f;
+          const float ds = pr * (dpacc[e] - d4[j]);
+          pb[e / 8][e % 8] = (bf16)pr;
+          db[e / 8][e % 8] = (bf16)ds;
+        }
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS over the tile's rows in two 16-row
+      // steps kk; step kk's B operand (lane group g2) holds rows
+      // 32 mt + 16 kk + 4 g2 + {0..3} and the same + 8, which the A operand
+      // gets from two transposing reads of those 4-row runs.  Operand
+      // i = 8 kk + 2 d + w (w = 0: dO for dV, 1: Q for dK); the reads of
+      // operand i + PD are issued before MFMA i.
+      auto load_a = [&](int i) -> bf16x8 {
+        const int kk = i / 8, d = (i / 2) % 4, w = i % 2;
+        const uint32_t rb = mrow + (uint32_t)(16 * kk * kCH) * 16u;
+        const u32x4* src = w ? qt : dt;
+        const bf16x4 lo = lds_read_tr16(src, vofs[0][d] + rb);
+        const bf16x4 hi = lds_read_tr16(src, vofs[1][d] + rb);
+        return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      };
+      constexpr int NA = 16, PD = 4;
+      bf16x8 abuf[PD];
+#pragma unroll
+      for (int i = 0; i < PD; ++i) abuf[i] = load_a(i);
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int kk = i / 8, d = (i / 2) % 4, w = i % 2;
+        const bf16x8 a = abuf[i % PD];
+        if (i + PD < NA) abuf[i % PD] = load_a(i + PD);
+        const bf16x8 bop = w ? db[kk] : pb[kk];
+        acc_t& acc = w ? dkacc[d] : dvacc[d];
+        if (i % 8 < 2)  // first use of pb[kk] / db[kk], just written by VALU
+          M::template mma_agpr<true>(a, bop, acc, prev_a, prev_b);
+        else
+          M::template mma_agpr<false>(a, bop, acc, prev_a, prev_b);
+        prev_a = a;
+        prev_b = bop;
+      }
+    }
+    M::tail(prev_a, prev_b);
+  };
+
+  __syncthreads();  // list staged
+  load_block(s_list[0], s_q0, s_d0, s_lse0, s_dlt0, s_msk0);
+  __syncthreads();
+  for (int j = 0; j < nblk; j += 2) {
+    if (j + 1 < nblk) load_block(s_list[j + 1], s_q1, s_d1, s_lse1, s_dlt1, s_msk1);
+    compute(s_q0, s_d0, s_lse0, s_dlt0, s_msk0);
+    __syncthreads();
+    if (j + 1 < nblk) {
+      if (j + 2 < nblk) load_block(s_list[j + 2], s_q0, s_d0, s_lse0, s_dlt0, s_msk0);
+      compute(s_q1, s_d1, s_lse1, s_dlt1, s_msk1);
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int d = 0; d < kD / 32; ++d) {
+    M::drain(dkacc[d]);
+    M::drain(dvacc[d]);
+  }
+  // partial [key][dK 128 | dV 128] of this chunk; C layout: lane (key n,
+  // group g2), element e = dim 32 d + 8 (e / 4) + 4 g2 + e % 4
+  float* part = p.dkv_part + ((bgk * p.max_chunks + c) * kKeyBlock + wave * 32 + n) * (2 * kD);
+#pragma unroll
+  for (int d = 0; d < kD / 32; ++d) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int dim = 32 * d + 8 * q + 4 * g2;
+      const f32x4 k4 = {dkacc[d][4 * q] * p.scale, dkacc[d][4 * q + 1] * p.scale, dkacc[d][4 * q + 2] * p.scale,
+                        dkacc[d][4 * q + 3] * p.scale};
+      const f32x4 v4 = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2], dvacc[d][4 * q + 3]};
+      *reinterpret_cast<f32x4*>(part + dim) = k4;
+      *reinterpret_cast<f32x4*>(part + kD + dim) = v4;
+    }
+  }
+}
+
+// ---- 3. chunk partials -> per-key accumulators (chunk order) --------------
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(Params p) {
+  constexpr int Q4 = 2 * kD / 4;
+  const int64_t n4 = (int64_t)p.B * p.Skv * p.Hkv * Q4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const int q4 = (int)(i % Q4);
+    int64_t r = i / Q4;
+    const int g = (int)(r % p.Hkv);
+    r /= p.Hkv;
+    const int key = (int)(r % p.Skv);
+    const int b = (int)(r / p.Skv);
+    const int kb = key / kKeyBlock;
+    const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
+    const int nch = (p.bcount[bgk] + kChunk - 1) / kChunk;
+    const float* src = p.dkv_part + (bgk * p.max_chunks * kKeyBlock + (key % kKeyBlock)) * (2 * kD) + 4 * q4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int ch = 0; ch < nch; ++ch)
+      acc += *reinterpret_cast<const f32x4*>(src + (int64_t)ch * kKeyBlock * (2 * kD));
+    const int64_t row = (((int64_t)b * p.Skv + key) * p.Hkv + g) * kD;
+    float* dst = (4 * q4 < kD) ? p.dk_acc + row + 4 * q4 : p.dv_acc + row + 4 * q4 - kD;
+    *reinterpret_cast<f32x4*>(dst) += acc;
+  }
+}
+
+inline unsigned grid_stride_blocks(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return (unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192);
+}
+
+bool fits31(int64_t bytes) { return bytes > 0 && bytes < (int64_t)kOOB; }
+
+}  // namespace
+
+bool bwd_csr_supported(const Params& p) {
+  if (!bwd_mfma_supported(p)) return false;  // the query-major dQ kernel
+  if (p.Dqk != kD || p.Dv != kD) return false;
+  if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
+  const int nkb = (p.Skv + kKeyBlock - 1) / kKeyBlock;
+  const int64_t w = 4 * (int64_t)nkb;
+  return fits31(2 * ((int64_t)(p.Sq - 1) * p.q_ss + (int64_t)(p.G - 1) * p.q_sh + kD)) &&
+         fits31(2 * ((int64_t)(p.Sq - 1) * p.do_ss + (int64_t)(p.G - 1) * p.do_sh + kD)) &&
+         fits31(4 * ((int64_t)(p.Sq - 1) * p.l_ss + (int64_t)(p.G - 1) * p.l_sh + 1)) &&
+         fits31(4 * ((int64_t)(p.Sq - 1) * p.Hq + p.G)) && fits31(4 * ((int64_t)(p.Sq - 1) * w + 4));
+}
+
+void csr_geometry(Params& p) {
+  p.nkb = (p.Skv + kKeyBlock - 1) / kKeyBlock;
+  p.kmap_w = 4 * p.nkb;
+  p.lg_g = p.G <= 1 ? 0 : p.G <= 2 ? 1 : p.G <= 4 ? 2 : p.G <= 8 ? 3 : 4;
+  const int nq = kRowBlock >> p.lg_g;
+  p.nqb = (p.Sq + nq - 1) / nq;
+  p.max_chunks = (p.nqb + kChunk - 1) / kChunk;
+}
+
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t csr_workspace_bytes(const Params& p) {
+  const size_t bg = (size_t)p.B * p.Hkv;
+  return al256(bg * p.Sq * p.kmap_w * 4) + al256((size_t)p.B * p.Sq * p.Hkv * p.topk) +
+         al256(bg * p.nkb * p.nqb * 4) + al256(bg * p.nkb * 4) +
+         al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4);
+}
+
+void csr_bind_workspace(Params& p, void* ws) {
+  const size_t bg = (size_t)p.B * p.Hkv;
+  char* c = static_cast<char*>(ws);
+  p.kmap = reinterpret_cast<uint32_t*>(c);
+  c += al256(bg * p.Sq * p.kmap_w * 4);
+  p.dup = reinterpret_cast<uint8_t*>(c);
+  c += al256((size_t)p.B * p.Sq * p.Hkv * p.topk);
+  p.blist = reinterpret_cast<int*>(c);
+  c += al256(bg * p.nkb * p.nqb * 4);
+  p.bcount = reinterpret_cast<int*>(c);
+  c += al256(bg * p.nkb * 4);
+  p.dkv_part = reinterpret_cast<float*>(c);
+}
+
+hipError_t launch_csr_index(const Params& p, hipStream_t s) {
+  const size_t words = (size_t)p.B * p.Hkv * p.Sq * p.kmap_w;
+  hipError_t e = launch_zero_f32(reinterpret_cast<float*>(p.kmap), words, s);  // all-zero bits
+  if (e != hipSuccess) return e;
+  const int64_t slots = (int64_t)p.B * p.Sq * p.Hkv * p.topk;
+  hipLaunchKernelGGL(csr_scatter_kernel, dim3(grid_stride_blocks(slots)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(csr_blocklist_kernel, dim3((unsigned)((int64_t)p.B * p.Hkv * p.nkb)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_csr_dkv(const Params& p, hipStream_t s) {
+  const int64_t wgs = (int64_t)p.B * p.Hkv * p.nkb * p.max_chunks;
+  hipLaunchKernelGGL(dkv_keymajor_kernel, dim3((unsigned)wgs), dim3(256), 0, s, p);
+  const int64_t n4 = (int64_t)p.B * p.Skv * p.Hkv * (2 * kD / 4);
+  hipLaunchKernelGGL(dkv_reduce_kernel, dim3(grid_stride_blocks(n4)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace sfa

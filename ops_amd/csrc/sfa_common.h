@@ -47,6 +47,16 @@ struct Params {
   float* delta;       // [B*Sq*Hq] Σ O·dO − dlse
   const float* dlse;  // gradient w.r.t. lse (lse's strides) or nullptr
   float* dsink;       // [Hq] (accumulated; zeroed by the launcher)
+  // deterministic dK/dV (SFA_DKV_CSR): index inversion at block granularity
+  uint32_t* kmap;     // [B][Hkv][Sq][kmap_w] membership bitmap: bit k of row t = key k is selected
+  int kmap_w;         // 32-bit words per bitmap row (multiple of 4)
+  uint8_t* dup;       // [B][Sq][Hkv][topk] 1 = slot repeats an earlier slot's key (handled by atomics)
+  int* blist;         // [B][Hkv][nkb][nqb] non-empty query blocks of each key block, ascending
+  int* bcount;        // [B][Hkv][nkb] entries of blist
+  float* dkv_part;    // [B][Hkv][nkb][max_chunks][128][2 D] fp32 partial dK | dV per chunk
+  int nkb, nqb;       // key blocks (128 keys), query blocks (128 / G queries)
+  int lg_g;           // log2(G)
+  int max_chunks;     // chunks per key block (query blocks / chunk, rounded up)
 };
 
 typedef __bf16 bf16;
@@ -106,4 +116,11 @@ bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
+// deterministic dK/dV
+bool bwd_csr_supported(const Params& p);
+void csr_geometry(Params& p);                 // fills kmap_w, nkb, nqb, lg_g, max_chunks
+size_t csr_workspace_bytes(const Params& p);  // after csr_geometry
+void csr_bind_workspace(Params& p, void* ws); // carves kmap / dup / blist / bcount / dkv_part
+hipError_t launch_csr_index(const Params& p, hipStream_t s);  // bitmap, duplicate flags, block lists
+hipError_t launch_csr_dkv(const Params& p, hipStream_t s);    // key-major dK/dV partials + reduction
 }  // namespace sfa

@@ -40,6 +40,7 @@
 
 #include "sfa_common.h"
 #include "sfa_lds.h"
+#include "sfa_mfma.h"
 
 namespace sfa {
 namespace {
@@ -83,93 +84,6 @@ struct FwdCfg {
   static_assert(DQK % KD == 0 && DV % T == 0, "head dims must tile the MFMA");
   static_assert(!VK || DV <= DQK, "v must be a prefix of k");
   static_assert(CHK % 2 == 0 && CHV % 2 == 0, "rows need an even number of 16-byte chunks");
-};
-
-template <int T>
-struct Mfma;
-
-template <>
-struct Mfma<32> {
-  typedef f32x16 acc_t;
-  static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  // Inline-asm MFMAs.  The O^T accumulators (256 registers per lane) must stay
-  // in the AGPR file and the S^T accumulator in VGPRs; builtins leave that
-  // choice to the compiler, which mixes the files and spills.  The compiler
-  // does not model hazards inside inline asm, so the code provides them:
-  //  * RAW VALU -> srcA/srcB needs 2 wait states: callers pass nop = true
-  //    when an operand may have just been written by a VALU instruction;
-  //  * WAR srcA/srcB -> later write: every MFMA also takes the operands of
-  //    the previous MFMA (pa, pb) as inputs, so the compiler cannot reuse
-  //    those registers before the next MFMA has issued; the last MFMA of a
-  //    sequence is followed by tail(), which holds its operands for 8 more
-  //    wait states;
-  //  * RAW result -> VALU read needs up to 18 wait states: drain_*().
-  // The "memory" clobber keeps the software-pipelined operand loads in
-  // program order around the MFMAs.
-  template <bool NOP>
-  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
-    if constexpr (NOP)
-      asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
-    else
-      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
-  }
-  static __device__ __forceinline__ void mma_v(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
-    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-                 : "+v"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
-  }
-  static __device__ __forceinline__ void mma_v0(bf16x8 a, bf16x8 b, acc_t& c) {
-    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
-                 : "=&v"(c) : "v"(a), "v"(b) : "memory");
-  }
-  static __device__ __forceinline__ void tail(const bf16x8& a, const bf16x8& b) {
-    asm volatile("s_nop 7" : : "v"(a), "v"(b));
-  }
-  // wait states between the last asm MFMA writing an accumulator and VALU reads
-  static __device__ __forceinline__ void drain_v(acc_t& c, const bf16x8& a, const bf16x8& b) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(c) : "v"(a), "v"(b));
-  }
-  static __device__ __forceinline__ void drain(acc_t& c) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(c));
-  }
-  // c *= s on an AGPR-resident accumulator without moving it to VGPRs.
-  static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float x = c[e];
-      float tmp;
-      asm volatile(
-          "v_accvgpr_read_b32 %1, %0\n\t"
-          "v_mul_f32 %1, %1, %2\n\t"
-          "v_accvgpr_write_b32 %0, %1"
-          : "+a"(x), "=&v"(tmp)
-          : "v"(s));
-      c[e] = x;
-    }
-  }
-};
-
-template <>
-struct Mfma<16> {
-  typedef f32x4 acc_t;
-  static __device__ __forceinline__ acc_t mma(bf16x8 a, bf16x8 b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  template <bool NOP>
-  static __device__ __forceinline__ void mma_agpr(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8&, const bf16x8&) {
-    c = mma(a, b, c);
-  }
-  static __device__ __forceinline__ void mma_v(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8&, const bf16x8&) {
-    c = mma(a, b, c);
-  }
-  static __device__ __forceinline__ void mma_v0(bf16x8 a, bf16x8 b, acc_t& c) { c = mma(a, b, acc_t{}); }
-  static __device__ __forceinline__ void tail(const bf16x8&, const bf16x8&) {}
-  static __device__ __forceinline__ void drain_v(acc_t&, const bf16x8&, const bf16x8&) {}
-  static __device__ __forceinline__ void scale_agpr(acc_t& c, float s) { c *= s; }
-  static __device__ __forceinline__ void drain(acc_t&) {}
 };
 
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
