@@ -56,7 +56,7 @@ enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1 };
 /* How the backward produces dK/dV. */
 enum {
   SFA_DKV_AUTO = 0,    /* CSR where supported (bf16, d_qk = d_v = 128, G a power of two
-                          <= 16, top-k <= 2048), otherwise ATOMIC                       */
+                          <= 16, top-k <= 2048, Skv <= 262144), otherwise ATOMIC       */
   SFA_DKV_ATOMIC = 1,  /* fp32 atomic adds into a workspace accumulator (SFA.py:853)    */
   SFA_DKV_CSR = 2      /* deterministic: membership bitmap inverted into per-key-block
                           lists of referencing query blocks, key-major recompute, fixed-

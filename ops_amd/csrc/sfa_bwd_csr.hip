@@ -55,24 +55,33 @@ static_assert(kTB % 64 == 0 && kCH == 16, "block buffers: 4 rows per DMA instruc
 __device__ __forceinline__ int blk_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 
 // ---- 1a. membership bitmap and repeated-slot flags ------------------------
+// One workgroup per index row (b, t, g): the row's bitmap is built with LDS
+// atomics, then written out whole (no global atomics, no separate clearing).
+constexpr int kMaxMapWords = 8192;  // LDS words per bitmap row: Skv <= 262144
 __global__ __launch_bounds__(256) void csr_scatter_kernel(Params p) {
-  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.topk;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int s = (int)(i % p.topk);
-    int64_t r = i / p.topk;
-    const int g = (int)(r % p.Hkv);
-    r /= p.Hkv;
-    const int t = (int)(r % p.Sq);
-    const int b = (int)(r / p.Sq);
-    const int id = p.idx[b * p.i_sb + t * p.i_ss + g * p.i_sh + s];
+  __shared__ uint32_t s_map[kMaxMapWords];
+  int wi = blockIdx.x;
+  const int g = wi % p.Hkv;
+  wi /= p.Hkv;
+  const int t = wi % p.Sq;
+  const int b = wi / p.Sq;
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  uint32_t* mrow = p.kmap + (((int64_t)b * p.Hkv + g) * p.Sq + t) * p.kmap_w;
+  uint8_t* drow = p.dup + (((int64_t)b * p.Sq + t) * p.Hkv + g) * p.topk;
+  const int bound = bound_of(p, b);
+  for (int w = threadIdx.x; w < p.kmap_w; w += 256) s_map[w] = 0u;
+  __syncthreads();
+  for (int s = threadIdx.x; s < p.topk; s += 256) {
+    const int id = irow[s];
     uint8_t rep = 0;
-    if (id >= 0 && id < bound_of(p, b)) {
-      uint32_t* w = p.kmap + (((int64_t)b * p.Hkv + g) * p.Sq + t) * p.kmap_w + (id >> 5);
+    if (id >= 0 && id < bound) {
       const uint32_t bit = 1u << (id & 31);
-      rep = (atomicOr(w, bit) & bit) ? 1 : 0;
+      rep = (atomicOr(&s_map[id >> 5], bit) & bit) ? 1 : 0;
     }
-    p.dup[i] = rep;
+    drow[s] = rep;
   }
+  __syncthreads();
+  for (int w = threadIdx.x; w < p.kmap_w; w += 256) mrow[w] = s_map[w];
 }
 
 // ---- 1b. per key block: ascending list of non-empty query blocks -----------
@@ -424,6 +433,7 @@ bool bwd_csr_supported(const Params& p) {
   if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
   const int nkb = (p.Skv + kKeyBlock - 1) / kKeyBlock;
   const int64_t w = 4 * (int64_t)nkb;
+  if (w > kMaxMapWords) return false;
   return fits31(2 * ((int64_t)(p.Sq - 1) * p.q_ss + (int64_t)(p.G - 1) * p.q_sh + kD)) &&
          fits31(2 * ((int64_t)(p.Sq - 1) * p.do_ss + (int64_t)(p.G - 1) * p.do_sh + kD)) &&
          fits31(4 * ((int64_t)(p.Sq - 1) * p.l_ss + (int64_t)(p.G - 1) * p.l_sh + 1)) &&
@@ -463,11 +473,7 @@ void csr_bind_workspace(Params& p, void* ws) {
 }
 
 hipError_t launch_csr_index(const Params& p, hipStream_t s) {
-  const size_t words = (size_t)p.B * p.Hkv * p.Sq * p.kmap_w;
-  hipError_t e = launch_zero_f32(reinterpret_cast<float*>(p.kmap), words, s);  // all-zero bits
-  if (e != hipSuccess) return e;
-  const int64_t slots = (int64_t)p.B * p.Sq * p.Hkv * p.topk;
-  hipLaunchKernelGGL(csr_scatter_kernel, dim3(grid_stride_blocks(slots)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)((int64_t)p.B * p.Sq * p.Hkv)), dim3(256), 0, s, p);
   hipLaunchKernelGGL(csr_blocklist_kernel, dim3((unsigned)((int64_t)p.B * p.Hkv * p.nkb)), dim3(256), 0, s, p);
   return hipGetLastError();
 }
