@@ -9,7 +9,8 @@ top-k pairs (2·(d_qk+d_v) FLOP per head per pair).  The other workloads are
 measured in the same run and reported under ``workloads``:
 
 * ``prefill``     MQA fwd, S=4096, Hq=16, d=128, top-k 512        (TFLOP/s)
-* ``train_gqa``   GQA fwd (+ bwd), B=2, S=8192, Hq=32, Hkv=2, top-k 1024
+* ``train_gqa``   GQA fwd + bwd (deterministic and atomic dK/dV), B=2, S=8192,
+                  Hq=32, Hkv=2, top-k 1024
 * ``mla_decode``  B=64 x 1 query, KV [64, 65536, 1, 576], top-k 2048, split-k
                   + combine, caches flushed (by a 1 GiB read) before every step (GB/s)
 
@@ -161,14 +162,18 @@ def bench_train_gqa(args):
            "valid_pairs": pairs, "hot_share": w.meta.get("hot_share"),
            "config": {"B": 2, "S": 8192, "Hq": 32, "Hkv": 2, "d": 128, "topk": 1024}}
     res["frac_of_peak"] = res["value"] / PEAK_BF16_TFLOPS
-    if args.bwd:
+    if not args.no_bwd:
         out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
         bf = bwd_flops(w, pairs)
-        bt, _ = time_steps(lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale),
-                           max(1, args.steps // 2), 1)
-        bms = sum(bt) / len(bt)
-        res["bwd"] = {"value": bf / (bms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": bms,
-                      "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+        res["bwd"] = {}
+        for mode in ("csr", "atomic"):
+            bt, _ = time_steps(lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale,
+                                                            dkv_mode=mode), max(1, args.steps // 2), 1)
+            bms = sum(bt) / len(bt)
+            res["bwd"][mode] = {"value": bf / (bms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": bms,
+                                "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+        res["bwd"]["note"] = ("TFLOP/s over valid pairs (pairs * G * 2 (3 d_qk + 2 d_v)); 'csr' = deterministic "
+                              "dK/dV (the default), 'atomic' = fp32 atomics")
     return res
 
 
@@ -203,7 +208,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--extra", default="prefill,train_gqa,mla_decode",
                     help="comma list of additional workloads to measure ('' for none)")
-    ap.add_argument("--bwd", action="store_true", help="also time the train_gqa backward")
+    ap.add_argument("--no-bwd", action="store_true", help="skip the train_gqa backward timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
