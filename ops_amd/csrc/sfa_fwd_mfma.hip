@@ -109,9 +109,20 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const int ks = wave / C::NSLICE;
 
   // ---- work item -------------------------------------------------------
+  // Work item = (b, t, g) x split.  Workgroups are dispatched to the 8 XCDs
+  // round-robin (blockIdx % 8); with splits, the splits of one item are
+  // placed on the same XCD (so its L2 serves the item's Q rows to all of
+  // them) whenever the item count allows a bijective mapping.
   int wi = blockIdx.x;
-  const int split = wi % p.num_splits;
-  wi /= p.num_splits;
+  int split;
+  if (p.num_splits > 1 && (int64_t)p.B * p.Sq * p.Hkv % 8 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    split = r % p.num_splits;
+    wi = (r / p.num_splits) * 8 + x;
+  } else {
+    split = wi % p.num_splits;
+    wi /= p.num_splits;
+  }
   const int g = wi % p.Hkv;
   wi /= p.Hkv;
   const int t = wi % p.Sq;
