@@ -603,7 +603,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 
 // Variants: (T, DQK, DV, NSLICE, NSPLITW, V is a prefix of K)
 using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;  // DeepSeek MLA: G = 128, d_qk 576 / d_v 512
-using CfgD128G16 = FwdCfg<16, 128, 128, 1, 4, false, 4>;    // d = 128, G <= 16
+using CfgD128G16 = FwdCfg<16, 128, 128, 1, 2, false, 4>;    // d = 128, G <= 16 (2 waves: two workgroups per CU)
 
 template <class C>
 hipError_t launch(const Params& p, hipStream_t s) {
