@@ -97,6 +97,8 @@ __global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
   const uint32_t* mrow = p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4;
   const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
   int* list = p.blist + bgk * p.nqb;
+  int* start = p.bstart + bgk * (p.max_chunks + 1);
+  static_assert(2 * kChunk == 256, "one iteration covers two chunks");
   int total = 0;
   for (int q0 = 0; q0 < p.nqb; q0 += 256) {
     const int qb = q0 + tid;
@@ -115,10 +117,17 @@ __global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
     int pos = total + __popcll(m & ((1ull << lane) - 1ull));
     for (int w = 0; w < wave; ++w) pos += s_cnt[w];
     if (any) list[pos] = qb;
+    // chunk starts: query blocks [128 c, 128 (c + 1)) are this iteration's
+    // two halves (waves 0-1 and 2-3)
+    const int c0 = q0 / kChunk;
+    if (tid == 0) {
+      start[c0] = total;
+      if (c0 + 1 <= p.max_chunks) start[c0 + 1] = total + s_cnt[0] + s_cnt[1];
+    }
     total += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
     __syncthreads();
   }
-  if (tid == 0) p.bcount[bgk] = total;
+  if (tid == 0) start[p.max_chunks] = total;
 }
 
 // ---- 2. key-major dK / dV ---------------------------------------------------
@@ -143,18 +152,29 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int wi = blockIdx.x;
-  const int c = wi % p.max_chunks;
-  wi /= p.max_chunks;
-  const int kb = wi % p.nkb;
-  wi /= p.nkb;
-  const int g = wi % p.Hkv;
-  const int b = wi / p.Hkv;
+  // Workgroup = (b, g, key block kb, chunk c): the entries of kb's list that
+  // fall in query blocks [128 c, 128 (c + 1)).  Workgroups are dispatched to
+  // the 8 XCDs round-robin; when the key-block count allows, XCD x gets the
+  // key blocks kb = x (mod 8) in chunk-major order, so the workgroups that run
+  // together on one XCD share query blocks (its L2 serves them once loaded).
+  const int per_bg = p.nkb * p.max_chunks;
+  const int bg = blockIdx.x / per_bg, l = blockIdx.x % per_bg;
+  int kb, c;
+  if (p.nkb % 8 == 0) {
+    const int x = l % 8, r = l / 8;
+    kb = x + 8 * (r % (p.nkb / 8));
+    c = r / (p.nkb / 8);
+  } else {
+    kb = l / p.max_chunks;
+    c = l % p.max_chunks;
+  }
+  const int g = bg % p.Hkv;
+  const int b = bg / p.Hkv;
   const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
-  const int cnt = p.bcount[bgk];
-  const int e0 = c * kChunk;
-  if (e0 >= cnt) return;  // the whole workgroup: no query block in this chunk
-  const int nblk = min(kChunk, cnt - e0);
+  const int* start = p.bstart + bgk * (p.max_chunks + 1);
+  const int e0 = start[c];
+  const int nblk = start[c + 1] - e0;
+  if (nblk <= 0) return;  // the whole workgroup: no query block in this chunk
   for (int i = tid; i < nblk; i += 256) s_list[i] = p.blist[bgk * p.nqb + e0 + i];
 
   const int G = p.G, lg = p.lg_g;
@@ -407,11 +427,11 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(Params p) {
     const int b = (int)(r / p.Skv);
     const int kb = key / kKeyBlock;
     const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
-    const int nch = (p.bcount[bgk] + kChunk - 1) / kChunk;
+    const int* start = p.bstart + bgk * (p.max_chunks + 1);
     const float* src = p.dkv_part + (bgk * p.max_chunks * kKeyBlock + (key % kKeyBlock)) * (2 * kD) + 4 * q4;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ch = 0; ch < nch; ++ch)
-      acc += *reinterpret_cast<const f32x4*>(src + (int64_t)ch * kKeyBlock * (2 * kD));
+    for (int ch = 0; ch < p.max_chunks; ++ch)  // chunks with entries wrote a partial
+      if (start[ch + 1] > start[ch]) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)ch * kKeyBlock * (2 * kD));
     const int64_t row = (((int64_t)b * p.Skv + key) * p.Hkv + g) * kD;
     float* dst = (4 * q4 < kD) ? p.dk_acc + row + 4 * q4 : p.dv_acc + row + 4 * q4 - kD;
     *reinterpret_cast<f32x4*>(dst) += acc;
@@ -454,7 +474,7 @@ static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t csr_workspace_bytes(const Params& p) {
   const size_t bg = (size_t)p.B * p.Hkv;
   return al256(bg * p.Sq * p.kmap_w * 4) + al256((size_t)p.B * p.Sq * p.Hkv * p.topk) +
-         al256(bg * p.nkb * p.nqb * 4) + al256(bg * p.nkb * 4) +
+         al256(bg * p.nkb * p.nqb * 4) + al256(bg * p.nkb * (p.max_chunks + 1) * 4) +
          al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4);
 }
 
@@ -467,8 +487,8 @@ void csr_bind_workspace(Params& p, void* ws) {
   c += al256((size_t)p.B * p.Sq * p.Hkv * p.topk);
   p.blist = reinterpret_cast<int*>(c);
   c += al256(bg * p.nkb * p.nqb * 4);
-  p.bcount = reinterpret_cast<int*>(c);
-  c += al256(bg * p.nkb * 4);
+  p.bstart = reinterpret_cast<int*>(c);
+  c += al256(bg * p.nkb * (p.max_chunks + 1) * 4);
   p.dkv_part = reinterpret_cast<float*>(c);
 }
 

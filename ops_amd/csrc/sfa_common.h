@@ -52,7 +52,7 @@ struct Params {
   int kmap_w;         // 32-bit words per bitmap row (multiple of 4)
   uint8_t* dup;       // [B][Sq][Hkv][topk] 1 = slot repeats an earlier slot's key (handled by atomics)
   int* blist;         // [B][Hkv][nkb][nqb] non-empty query blocks of each key block, ascending
-  int* bcount;        // [B][Hkv][nkb] entries of blist
+  int* bstart;        // [B][Hkv][nkb][max_chunks + 1] blist index of each 128-query-block chunk's first entry
   float* dkv_part;    // [B][Hkv][nkb][max_chunks][128][2 D] fp32 partial dK | dV per chunk
   int nkb, nqb;       // key blocks (128 keys), query blocks (128 / G queries)
   int lg_g;           // log2(G)
