@@ -113,12 +113,21 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // round-robin (blockIdx % 8); with splits, the splits of one item are
   // placed on the same XCD (so its L2 serves the item's Q rows to all of
   // them) whenever the item count allows a bijective mapping.
+  // Without splits, XCD x gets runs of 32 consecutive items (queries), runs
+  // dealt round-robin over the XCDs: the workgroups running together on one
+  // XCD then share the keys their queries have in common (e.g. a recency
+  // window) in its L2.
   int wi = blockIdx.x;
   int split;
-  if (p.num_splits > 1 && (int64_t)p.B * p.Sq * p.Hkv % 8 == 0) {
+  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
+  if (p.num_splits > 1 && nitems % 8 == 0) {
     const int x = wi % 8, r = wi / 8;
     split = r % p.num_splits;
     wi = (r / p.num_splits) * 8 + x;
+  } else if (p.num_splits == 1 && nitems % 256 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    split = 0;
+    wi = ((r / 32) * 8 + x) * 32 + r % 32;
   } else {
     split = wi % p.num_splits;
     wi /= p.num_splits;
