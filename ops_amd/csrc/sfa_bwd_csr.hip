@@ -15,10 +15,13 @@
 //     have none).  Then, for every key block of 128 keys, the ascending list
 //     of query blocks (128 query-head rows = 128 / G queries) that select at
 //     least one of its keys (`blist`, a per-key-block CSR at block
-//     granularity).
+//     granularity), with `bstart` marking where each chunk of kChunk
+//     consecutive query blocks (an absolute query range) begins in it.
 //  2. Key-major recompute.  One workgroup owns a key block (each wave 32
-//     keys, K and V rows kept in registers) and a chunk of up to kChunk of
-//     its query blocks.  Per query block it recomputes, for every (row, key)
+//     keys, K and V rows kept in registers) and one chunk: the listed query
+//     blocks in one absolute range of kChunk query blocks, so the workgroups
+//     of neighbouring key blocks that run together read the same query
+//     blocks.  Per query block it recomputes, for every (row, key)
 //     pair of the block, S = Q K^T and dP = dO V^T (32x32x16 MFMA, rows as
 //     M, keys as N), P = 2^(S scale log2e - lse2) and dS = P (dP - δ) masked
 //     by the bitmap, and accumulates dV^T += dO^T P and dK^T += Q^T dS in
