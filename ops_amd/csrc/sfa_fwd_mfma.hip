@@ -227,11 +227,20 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const int lt = lane % T;
 
   // With kSpread, compute(tile) also issues the gather of the next tile into
-  // ndst (rg holds that tile's row offsets; the caller skips its own gather).
-  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, const RG& rg, u32x4* ndst) {
+  // ndst (rg holds that tile's row offsets; the caller skips its own gather),
+  // and, inside its O^T MFMA stream (all of that gather has been issued by
+  // then), reads the row ids of tile + 2 into rg and the validity mask of
+  // tile + 1 into vmask_io, so no LDS round trip sits between the end of one
+  // tile's MFMAs and the next tile's.  Without kSpread, vmask_io is unused.
+  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, RG& rg, u32x4* ndst, uint32_t& vmask_io) {
     // validity of this wave's 32 keys
-    const int myid = s_idx[tile * C::NKT + ks * 32 + (lane & 31)];
-    const uint32_t vmask = (uint32_t)__ballot(myid >= 0);
+    uint32_t vmask;
+    if constexpr (kSpread) {
+      vmask = vmask_io;
+    } else {
+      const int myid = s_idx[tile * C::NKT + ks * 32 + (lane & 31)];
+      vmask = (uint32_t)__ballot(myid >= 0);
+    }
 
     // S^T = K Q^T
     acc_t sacc[C::MT];
@@ -328,11 +337,20 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     // tile) are O^T and l rescaled and the exponentials recomputed.  While no
     // valid key has been seen m_used is -inf: the offset is then 0, and the
     // first valid tile always takes the recompute path.
+    // Only the NE0 values of the first O^T contraction step are needed before
+    // the first O^T MFMA; the rest are computed while the MFMAs of that step
+    // run (late_exps, after the max test, so never recomputed).
+    constexpr int NE0 = NV < 8 ? NV : 8;
     float ex[NV];
+    float moff = (m_used == kNegInf) ? 0.f : -m_used;
     {
-      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+      for (int i = 0; i < NE0; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+      // Materialise them here: the rescale path below overwrites them, so
+      // the compiler would otherwise sink this computation into the
+      // no-rescale branch, behind the max reduction.
+#pragma unroll
+      for (int i = 0; i < NE0; ++i) asm volatile("" : "+v"(ex[i]));
     }
     float tmax = sv[0];
 #pragma unroll
@@ -351,22 +369,37 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < C::OT; ++i) M::scale_agpr(oacc[i], alpha);
       m_used = m_new;
-      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
+      moff = (m_used == kNegInf) ? 0.f : -m_used;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+      for (int i = 0; i < NE0; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
     }
     constexpr int KSTEPS = NV / 8;  // O^T contraction steps per 32 keys
     bf16x8 pb[KSTEPS];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) pb[i / 8][i % 8] = (bf16)ex[i];
-    {
-      // pairwise sum (short dependency chain)
+    for (int i = 0; i < NE0; ++i) pb[i / 8][i % 8] = (bf16)ex[i];
+    // One wave per SIMD issues in order, so VALU work only overlaps an MFMA
+    // that is already running: the late exponentials and the row sum are
+    // spread over the O^T MFMA stream, one small piece after each MFMA (the
+    // pins keep the compiler from hoisting a piece in front of its MFMA).
+    constexpr int NLATE = NV - NE0;
+    auto late_exp = [&](int j) {  // value NE0 + j
+      const int i = NE0 + j;
+      asm volatile("" : "+v"(sv[i]));
+      ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+      if (j & 1) {
+        pb[i / 8][(i - 1) % 8] = (bf16)ex[i - 1];
+        pb[i / 8][i % 8] = (bf16)ex[i];
+      }
+    };
+    // pairwise sum of ex[lo, lo + n) (short dependency chain), into ex[lo]
+    auto sum_range = [&](int lo, int n) {
 #pragma unroll
-      for (int w = 1; w < NV; w *= 2)
+      for (int i = 0; i < n; ++i) asm volatile("" : "+v"(ex[lo + i]));
 #pragma unroll
-        for (int i = 0; i + w < NV; i += 2 * w) ex[i] += ex[i + w];
-      l_part += ex[0];
-    }
+      for (int w = 1; w < n; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < n; i += 2 * w) ex[lo + i] += ex[lo + i + w];
+    };
 
     // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
     // of operand i + PD are issued before MFMA i (software pipeline).
@@ -415,6 +448,17 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
     constexpr int NI = KSTEPS * C::OT;
+    // O^T MFMA after which the ids of tile + 2 are read, and the lag (in
+    // MFMAs) after which they are used
+    constexpr int kIdsAt = NLATE + 3, kIdsLag = 4;
+    static_assert(!kSpread || kIdsAt + kIdsLag + RG::RPW < NI, "id prefetch fits the O^T stream");
+    static_assert(!kSpread || kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kIdsAt,
+                  "the gather of tile + 1 is issued before rg is overwritten");
+    int ids_raw[RG::RPW];
+    bool ids_ok = false;
+    int vm_raw = 0;
+    static_assert(NI >= NLATE + 3 && NLATE <= C::OT && NE0 % 2 == 0 && NLATE % 2 == 0,
+                  "late softmax pieces must finish before the MFMAs that use them");
     constexpr int PD = NI < 3 ? NI : 3;
     bf16x8 abuf[PD];
 #pragma unroll
@@ -431,6 +475,31 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       prev_a = a;
       prev_b = pb[i / C::OT];
       dma_at(C::QSTEPS + i, rg, ndst);
+      if constexpr (kSpread) {
+        if (i == kIdsAt) {
+          ids_ok = tile + 2 < ntiles;
+          RG::fetch(s_idx + (ids_ok ? tile + 2 : 0) * C::NKT, wave, ids_raw);
+          vm_raw = s_idx[(tile + 1 < ntiles ? tile + 1 : 0) * C::NKT + ks * 32 + (lane & 31)];
+        }
+        // one row offset per MFMA from kIdsAt + kIdsLag on (each pinned at
+        // its MFMA, so the wait for the reads is not hoisted next to them and
+        // the scalar work does not bunch up between two MFMAs)
+        if (i >= kIdsAt + kIdsLag && i < kIdsAt + kIdsLag + RG::RPW) {
+          const int r = i - kIdsAt - kIdsLag;
+          asm volatile("" : "+v"(ids_raw[r]));
+          rg.set_row(r, ids_raw[r], ids_ok, krow_bytes);
+          asm volatile("" : "+s"(rg.base[r]));
+        }
+        if (i == kIdsAt + kIdsLag + RG::RPW) {
+          asm volatile("" : "+v"(vm_raw));
+          vmask_io = (uint32_t)__ballot(vm_raw >= 0);
+          asm volatile("" : "+s"(vmask_io));
+        }
+      }
+      if (i < NLATE) late_exp(i);
+      if (i == NLATE) sum_range(0, NE0);
+      if (NLATE > 0 && i == NLATE + 1) sum_range(NE0, NLATE);
+      if (i == NLATE + 2) l_part += (NLATE > 0) ? ex[0] + ex[NE0] : ex[0];
     }
     M::tail(prev_a, prev_b);
   };
@@ -447,25 +516,21 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   load_q();
   __syncthreads();  // first tile and the LDS part of Q in place
 
-  // row offsets of the next tile to gather (kSpread), read from s_idx ahead
-  // of the tile whose MFMA stream issues that gather, just before a barrier
+  // kSpread: row offsets of tile 1 (gathered during tile 0) and the validity
+  // mask of tile 0; compute() fetches those of the following tiles itself
   RG rg;
-  auto next_ids = [&](int next) {
-    if constexpr (kSpread) {
-      const bool ok = next < ntiles;
-      rg.load_ids(s_idx + (ok ? next : 0) * C::NKT, ok, wave, krow_bytes);
-    }
-  };
-  next_ids(1);
+  uint32_t vmask = 0;
+  if constexpr (kSpread) {
+    rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, krow_bytes);
+    vmask = (uint32_t)__ballot(s_idx[ks * 32 + (lane & 31)] >= 0);
+  }
   for (int j = 0; j < ntiles; j += 2) {
     if (!kSpread && j + 1 < ntiles) gather(j + 1, s_k1, s_v1);
-    compute(j, s_k0, C::VK ? s_k0 : s_v0, rg, s_k1);
-    next_ids(j + 2);
+    compute(j, s_k0, C::VK ? s_k0 : s_v0, rg, s_k1, vmask);
     __syncthreads();
     if (j + 1 < ntiles) {
       if (!kSpread && j + 2 < ntiles) gather(j + 2, s_k0, s_v0);
-      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1, rg, s_k0);
-      next_ids(j + 3);
+      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1, rg, s_k0, vmask);
       __syncthreads();
     }
   }

@@ -127,11 +127,23 @@ struct RowGather {
   // (No pointer select: the compiler keeps ib's array identity, so the read
   // does not wait for DMA into other LDS arrays.)
   __device__ __forceinline__ void load_ids(const int* ib, bool valid, int wave, uint32_t row_bytes) {
+    int raw[RPW];
+    fetch(ib, wave, raw);
+    set(raw, valid, row_bytes);
+  }
+  // load_ids in two halves, so a caller can issue the LDS reads early and
+  // turn them into offsets once they have landed.
+  __device__ __forceinline__ static void fetch(const int* ib, int wave, int (&raw)[RPW]) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      const int id = __builtin_amdgcn_readfirstlane(ib[wave * RPW + r]);
-      base[r] = (valid && id >= 0) ? __umul24((uint32_t)id, row_bytes) : kOOBRow;
-    }
+    for (int r = 0; r < RPW; ++r) raw[r] = ib[wave * RPW + r];
+  }
+  __device__ __forceinline__ void set_row(int r, int raw, bool valid, uint32_t row_bytes) {
+    const int id = __builtin_amdgcn_readfirstlane(raw);
+    base[r] = (valid && id >= 0) ? __umul24((uint32_t)id, row_bytes) : kOOBRow;
+  }
+  __device__ __forceinline__ void set(const int (&raw)[RPW], bool valid, uint32_t row_bytes) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) set_row(r, raw[r], valid, row_bytes);
   }
 
   __device__ __forceinline__ void issue(int k, const __amdgpu_buffer_rsrc_t& rs, u32x4* dst, int wave,
