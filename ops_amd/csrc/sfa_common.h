@@ -114,6 +114,10 @@ hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);
 bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
+// d = 128, G <= 16: register-direct gather (sfa_fwd_d128.hip)
+bool fwd_d128_supported(const Params& p);
+int fwd_d128_tile_keys();
+hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
 // deterministic dK/dV

@@ -1,0 +1,272 @@
+// gfx950 forward for d_qk = d_v = 128 with G <= 16 query heads per KV head
+// (the MQA prefill and GQA training shapes): register-direct gather.
+//
+// Reference: `_attn_fwd` / `_inner_fwd` (SFA.py:309-587); the math is the one
+// of the MLA kernel in sfa_fwd_mfma.hip (masked base-2 online softmax with a
+// lazy rescale, P V, sink, LSE, split-k partials).  The schedule follows from
+// the shape: one wave holds all G <= 16 heads of a work item, so a gathered K
+// or V row is used by exactly one wave and staging it in LDS buys no reuse.
+//  * K rows go straight from global memory into VGPRs as the A operands of
+//    S^T = K Q^T (16x16x32 MFMA: a lane needs 16 contiguous bytes of one row),
+//    double-buffered in registers one 32-key tile ahead;
+//  * V rows are loaded one tile ahead into VGPRs in the same lane layout and
+//    written to the wave's LDS area just before use, where the transposing
+//    reads (ds_read_b64_tr_b16) produce the V^T operands of O^T = V^T P^T;
+//  * one wave per workgroup, no barrier inside the tile loop and ~17 KB of
+//    LDS, so two waves share each SIMD and hide each other's load latency.
+// (Measured against the LDS-staged variant of sfa_fwd_mfma.hip: MQA prefill
+// 140 -> 122 us, GQA training forward 2.00 -> 1.75 ms.)
+
+#include "sfa_common.h"
+#include "sfa_lds.h"
+#include "sfa_mfma.h"
+
+namespace sfa {
+namespace {
+
+constexpr float kSlack = 8.0f;  // lazy-rescale slack (base-2 units), as in the MLA kernel
+constexpr int kIdxCapD = 2048;  // slots staged in LDS per work item
+constexpr int kT = 16;          // heads per wave (MFMA N)
+constexpr int kQSteps = 4;      // 128 / 32 contraction steps of S^T
+constexpr int kOT = 8;          // 128 / 16 O^T dim tiles
+constexpr int kPV = 17;         // V staging row pitch in 16-byte slots (odd: conflict-free reads)
+
+__global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
+  using M = Mfma<16>;
+  typedef M::acc_t acc_t;
+
+  __shared__ int s_idx[kIdxCapD];
+  __shared__ u32x4 s_v[32 * kPV];
+
+  const int lane = threadIdx.x;
+  const int lt = lane & 15;  // head (MFMA column) / key row within a 16-row M-tile
+  const int hq = lane >> 4;  // lane group: 8-element slice of the contraction
+
+  // ---- work item (same placement as the MLA kernel) ----------------------
+  int wi = blockIdx.x;
+  int split;
+  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
+  if (p.num_splits > 1 && nitems % 8 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    split = r % p.num_splits;
+    wi = (r / p.num_splits) * 8 + x;
+  } else if (p.num_splits == 1 && nitems % 256 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    split = 0;
+    wi = ((r / 32) * 8 + x) * 32 + r % 32;
+  } else {
+    split = wi % p.num_splits;
+    wi /= p.num_splits;
+  }
+  const int g = wi % p.Hkv;
+  wi /= p.Hkv;
+  const int t = wi % p.Sq;
+  const int b = wi / p.Sq;
+  const int slot0 = split * p.split_len;
+  int nslots = p.topk - slot0;
+  if (nslots > p.split_len) nslots = p.split_len;
+  if (nslots < 0) nslots = 0;
+  const int ntiles = (nslots + 31) / 32;
+
+  // ---- stage indices (invalid -> -1) --------------------------------------
+  {
+    const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
+    const int bound = bound_of(p, b);
+    for (int i = lane; i < ntiles * 32; i += 64) {
+      const int id = (i < nslots) ? irow[i] : -1;
+      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
+    }
+  }
+
+  // ---- Q^T B operands (16x16x32: lane holds head lt, dims 32 s + 8 hq ..) ---
+  const bool hvalid = lt < p.G;
+  bf16x8 qb[kQSteps];
+  {
+    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
+                       (int64_t)(g * p.G + (hvalid ? lt : 0)) * p.q_sh + 8 * hq;
+#pragma unroll
+    for (int s = 0; s < kQSteps; ++s) {
+      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+      if (!hvalid) x = bf16x8{};
+      qb[s] = x;
+    }
+  }
+
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
+  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
+  const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
+
+  __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
+
+  // Loads of tile j (keys 32 j .. 32 j + 31): operand i = 4 mt + s holds, for
+  // key row 16 mt + lt, the 16 bytes at dims 32 s + 8 hq (K: S^T A operand;
+  // V: 16-byte chunk 4 s + hq of the row, written to the staging area).
+  // Invalid keys read from an out-of-range offset and get zeros.
+  auto load_tile = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+    uint32_t ko[2], vo[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int id = s_idx[32 * j + 16 * mt + lt];
+      ko[mt] = id >= 0 ? __umul24((uint32_t)id, krow_bytes) : kOOB;
+      vo[mt] = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) : kOOB;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        kr[4 * mt + s] = __builtin_bit_cast(
+            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        vr[4 * mt + s] = __builtin_bit_cast(
+            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
+  };
+
+  // ---- accumulators ----------------------------------------------------
+  acc_t oacc[kOT];
+#pragma unroll
+  for (int i = 0; i < kOT; ++i) oacc[i] = acc_t{};
+  float m_used = kNegInf;  // running max (base 2) the exponentials are taken against
+  float l_part = 0.f;      // this lane's share of the row sum
+
+  // V^T operand reads (the transposing-read layout of 16-row M-tiles): lane
+  // group gi = lane % 16 reads 4-row runs at keys 4 hq .. and 16 + 4 hq ..
+  // (the P^T B-operand order), 4-dim piece cc of dim tile ot.
+  const int gi = lane & 15, rr = gi >> 2, cc = gi & 3;
+  const uint32_t vb0 = (uint32_t)((4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
+  const uint32_t vb1 = (uint32_t)((16 + 4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
+
+  auto step = [&](int j, const bf16x8 (&kc)[8], bf16x8 (&vr)[8], bf16x8 (&kn)[8]) {
+    // V of this tile into the staging area (the previous tile's reads of it
+    // are done: LDS operations of a wave complete in order), then the loads
+    // of the next tile into the freed registers
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        *reinterpret_cast<bf16x8*>(&s_v[(16 * mt + lt) * kPV + 4 * s + hq]) = vr[4 * mt + s];
+    const uint32_t vmask = (uint32_t)__ballot(s_idx[32 * j + (lane & 31)] >= 0);
+    if (j + 1 < ntiles) load_tile(j + 1, kn, vr);
+
+    // S^T = K Q^T: two 16-key M-tiles
+    acc_t sacc[2] = {acc_t{}, acc_t{}};
+#pragma unroll
+    for (int s = 0; s < kQSteps; ++s)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(kc[4 * mt + s], qb[s], sacc[mt]);
+
+    // softmax over this lane's 8 keys: key(mt, e) = 16 mt + 4 hq + e
+    float sv[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = 16 * mt + 4 * hq + e;
+        sv[4 * mt + e] = (vmask == 0xffffffffu || ((vmask >> key) & 1u)) ? sacc[mt][e] : kNegInf;
+      }
+    float ex[8];
+    {
+      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+    }
+    float tmax = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sv[i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax *= p.scale_log2;
+    const float m_new = fmaxf(m_used, tmax);
+    if (__any(m_new > m_used + kSlack)) {
+      const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_used - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < kOT; ++i) oacc[i] *= alpha;
+      m_used = m_new;
+      const float moff = (m_used == kNegInf) ? 0.f : -m_used;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
+    }
+    bf16x8 pb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pb[i] = (bf16)ex[i];
+    l_part += ((ex[0] + ex[1]) + (ex[2] + ex[3])) + ((ex[4] + ex[5]) + (ex[6] + ex[7]));
+
+    // O^T += V^T P^T (one 32-key contraction step per dim tile)
+#pragma unroll
+    for (int ot = 0; ot < kOT; ++ot) {
+      const bf16x4 lo = lds_read_tr16(s_v, vb0 + (uint32_t)(ot * kT) * 2u);
+      const bf16x4 hi = lds_read_tr16(s_v, vb1 + (uint32_t)(ot * kT) * 2u);
+      const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      oacc[ot] = M::mma(a, pb, oacc[ot]);
+    }
+  };
+
+  {
+    bf16x8 kA[8], kB[8], vr[8];
+    if (ntiles > 0) load_tile(0, kA, vr);
+    for (int j = 0; j < ntiles; j += 2) {
+      step(j, kA, vr, kB);
+      if (j + 1 < ntiles) step(j + 1, kB, vr, kA);
+    }
+  }
+
+  // ---- finish: row sums over the lane groups sharing a head ---------------
+  float l_sum = l_part;
+  l_sum += __shfl_xor(l_sum, 16, 64);
+  l_sum += __shfl_xor(l_sum, 32, 64);
+  const float m_fin = m_used;
+
+  if (!hvalid) return;
+  const int h = g * p.G + lt;
+  const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
+  // Split partials: normalised O of this split in bf16 plus its base-2 LSE
+  // (no sink: the merge adds it once).  Final output: the sink joins the
+  // denominator (SFA.py:469-478).
+  const bool partial = p.num_splits > 1;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  float scale_o;
+  bf16* orow;
+  if (partial) {
+    scale_o = l_sum > 0.f ? 1.f / l_sum : 0.f;
+    if (hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
+    orow = p.part_o + (split * nrows + row) * 128;
+  } else {
+    const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+    const float mm = fmaxf(m_fin, sink2);
+    const float fo = (m_fin == kNegInf) ? 0.f : exp2f(m_fin - mm);
+    float lt_ = l_sum * fo;
+    if (p.sink && mm != kNegInf) lt_ += exp2f(sink2 - mm);
+    scale_o = lt_ > 0.f ? fo / lt_ : 0.f;
+    if (hq == 0) p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] = lt_ > 0.f ? (mm + log2f(lt_)) * kLn2 : kNegInf;
+    orow = reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh;
+  }
+  // C layout: lane holds head lt, dims 16 ot + 4 hq + e
+#pragma unroll
+  for (int ot = 0; ot < kOT; ++ot) {
+    const bf16x4 v4 = {(bf16)(oacc[ot][0] * scale_o), (bf16)(oacc[ot][1] * scale_o), (bf16)(oacc[ot][2] * scale_o),
+                       (bf16)(oacc[ot][3] * scale_o)};
+    *reinterpret_cast<bf16x4*>(orow + 16 * ot + 4 * hq) = v4;
+  }
+}
+
+}  // namespace
+
+bool fwd_d128_supported(const Params& p) {
+  const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128);
+  const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128);
+  return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && kb < (int64_t)kOOB && vb < (int64_t)kOOB;
+}
+
+hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
+  hipLaunchKernelGGL(fwd_d128_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace sfa

@@ -1,15 +1,17 @@
-// gfx950 MFMA forward of top-k sparse flash attention (bf16 in, fp32 accumulate).
+// gfx950 MFMA forward of top-k sparse flash attention for DeepSeek MLA
+// (G = 128 query heads share one latent KV head, d_qk = 576, d_v = 512, V the
+// first 512 dims of the K rows); bf16 in, fp32 accumulate.  The d = 128,
+// G <= 16 shapes have their own kernel (sfa_fwd_d128.hip).
 //
 // Reference: `_attn_fwd` / `_inner_fwd` (lilac-me/ops SFA.py:309-587).  The
 // math is the same (gather the top-k rows, masked base-2 online softmax, P·V,
 // sink, LSE); the schedule is MI355X-native:
 //
 //  * One workgroup owns one (batch, query, kv-head[, split]) work item and
-//    all G = Hq/Hkv query heads of it, so every gathered KV row is used by all
-//    G heads (the reference re-gathers per 32-head tile, SFA.py:557).
-//  * Waves are arranged NSLICE (head slices of T heads) x NSPLITW (key
-//    sub-ranges).  A wave computes S^T = K·Q^T for its heads over 32 keys
-//    per tile: keys are MFMA rows, heads MFMA columns.  The fp32 S^T
+//    all G query heads of it, so every gathered KV row is used by all G heads
+//    (the reference re-gathers per 32-head tile, SFA.py:557).
+//  * 4 waves x 32 heads.  A wave computes S^T = K·Q^T for its heads over a
+//    32-key tile: keys are MFMA rows, heads MFMA columns.  The fp32 S^T
 //    accumulator layout then already is the B-operand layout of
 //    O^T = V^T·P^T (contraction over keys), so P never leaves registers, and
 //    every lane owns exactly one head: row max / sum and the rescale of the
@@ -17,26 +19,24 @@
 //  * V^T operands are read from the row-major LDS tile with
 //    ds_read_b64_tr_b16 (gfx950 transposing LDS read).
 //  * KV rows are gathered straight into LDS with buffer_load_dwordx4 ... lds
-//    (no VGPR staging), double-buffered one tile ahead.  Invalid slots use an
-//    out-of-range buffer offset, so the hardware writes zeros.  LDS rows are
-//    padded by one 16-byte slot (row pitch = odd number of slots), which
-//    makes the MFMA operand reads bank-conflict free and keeps every operand
-//    address a per-lane base plus an immediate offset.
+//    (no VGPR staging), double-buffered one tile ahead, the instructions
+//    spread over the previous tile's MFMA stream (RowGather).  Invalid slots
+//    use an out-of-range buffer offset, so the hardware writes zeros.  Tile
+//    rows have a pitch of 72 16-byte slots with the chunks XOR-swizzled by row
+//    (tile_swz), which makes both operand read patterns bank-conflict free.
 //  * Online softmax with a lazy rescale: the running max used for the
 //    exponentials is only raised when a tile's max exceeds it by more than
 //    kRescaleSlack (base-2 units).  Exponentials then stay <= 2^kRescaleSlack,
 //    and the final normalisation uses the same stale max, so the result is
 //    the exact softmax.
-//  * Split-k over the top-k slots (decode) writes normalised fp32 partial
+//  * Split-k over the top-k slots (decode) writes normalised bf16 partial
 //    outputs plus their base-2 LSE; sfa::launch_combine merges them.
 //
-// MFMA register layouts used (gfx950, bf16, 8 values per lane; T = 16 or 32):
+// MFMA register layouts used (gfx950 32x32x16 bf16, 8 values per lane, T = 32):
 //   A[m][k]: lane l holds m = l % T, k = 8*(l / T) + j        (j = 0..7)
 //   B[k][n]: lane l holds n = l % T, k = 8*(l / T) + j
 //   C[m][n]: lane l holds n = l % T, m = 4*LG*(e/4) + 4*(l/T) + e%4,
-//            e = 0..T*T/64-1, LG = 64/T.
-
-#include <type_traits>
+//            e = 0..15, LG = 64/T = 2.
 
 #include "sfa_common.h"
 #include "sfa_lds.h"
@@ -74,16 +74,12 @@ struct FwdCfg {
   static constexpr int QBUF = QL > 0 ? NSLICE * T * QLP : 1;
   static constexpr int OT = DV / T;
   static constexpr int CHK = DQK / 8;       // 16-byte chunks per k row
-  static constexpr int CHV = DV / 8;
   static constexpr int PK = SWZ ? CHK : CHK + 1;  // LDS row pitch in 16-byte slots (odd unless swizzled)
-  static constexpr int PV = CHV + 1;
   static constexpr int KBUF = NKT * PK;     // 16-byte slots per k tile
-  static constexpr int VBUF = VK ? 0 : NKT * PV;
-  static constexpr int GK = (KBUF + kThreads - 1) / kThreads;  // gather instructions per thread (k)
-  static constexpr int GV = (VBUF + kThreads - 1) / kThreads;  // gather instructions per thread (v)
   static_assert(DQK % KD == 0 && DV % T == 0, "head dims must tile the MFMA");
   static_assert(!VK || DV <= DQK, "v must be a prefix of k");
-  static_assert(CHK % 2 == 0 && CHV % 2 == 0, "rows need an even number of 16-byte chunks");
+  static_assert(CHK % 2 == 0, "rows need an even number of 16-byte chunks");
+  static_assert(T == 32 && NSPLITW == 1 && VK && SWZ, "the kernel is written for this configuration");
 };
 
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
@@ -98,8 +94,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   __shared__ int s_idx[kIdxCap];
   __shared__ u32x4 s_k0[C::KBUF];
   __shared__ u32x4 s_k1[C::KBUF];
-  __shared__ u32x4 s_v0[C::VK ? 1 : C::VBUF];
-  __shared__ u32x4 s_v1[C::VK ? 1 : C::VBUF];
   __shared__ u32x4 s_q[C::QBUF];
 
   const int tid = threadIdx.x;
@@ -184,17 +178,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
 
-  auto gather = [&](int tile, u32x4* kdst, u32x4* vdst) {
-    const int* ib = s_idx + tile * C::NKT;
-    gather_tile<C::NKT, C::CHK, C::kThreads>(ib, kdst, rk, krow_bytes, tid, wave);
-    if constexpr (!C::VK) gather_tile<C::NKT, C::CHV, C::kThreads>(ib, vdst, rv, vrow_bytes, tid, wave);
-  };
-  // Wide-row configs (v inside the k rows) issue the next tile's gather from
-  // inside the current tile's S^T MFMA stream instead of in one burst.
-  constexpr bool kSpread = C::VK && C::PK >= 64 && C::T == 32 && C::NKT % C::kWaves == 0;
-  typedef RowGather<(kSpread ? C::NKT : 32), (kSpread ? C::CHK : 72), (kSpread ? C::kWaves : 4), C::SWZ> RG;
-  static_assert(!C::SWZ || kSpread, "swizzled tiles are gathered by RowGather");
-  static_assert(!kSpread || RG::PITCH == C::PK, "gather and readers agree on the pitch");
+  // The next tile's gather is issued from inside the current tile's S^T MFMA
+  // stream instead of in one burst.
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ> RG;
+  static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
   // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
   // tile's MFMA sequence (QSTEPS S^T MFMAs, then the O^T MFMAs)
 #ifndef SFA_DMA_STRIDE
@@ -205,15 +192,13 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #endif
   constexpr int kDmaStride = SFA_DMA_STRIDE, kDmaFirst = SFA_DMA_FIRST;
   constexpr int kOtMfmas = 32 / 16 * C::OT;
-  static_assert(!kSpread || kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kOtMfmas, "schedule fits");
+  static_assert(kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kOtMfmas, "schedule fits");
   // (on the last tile the offsets are all out of range: the instructions
   // still issue, so the MFMA stream has no branches, and write zeros into the
   // idle buffer)
   auto dma_at = [&](int m, const RG& rg, u32x4* ndst) {
-    if constexpr (kSpread) {
-      if (m >= kDmaFirst && (m - kDmaFirst) % kDmaStride == 0 && (m - kDmaFirst) / kDmaStride < RG::NI)
-        rg.issue((m - kDmaFirst) / kDmaStride, rk, ndst, wave, lane);
-    }
+    if (m >= kDmaFirst && (m - kDmaFirst) % kDmaStride == 0 && (m - kDmaFirst) / kDmaStride < RG::NI)
+      rg.issue((m - kDmaFirst) / kDmaStride, rk, ndst, wave, lane);
   };
 
   // ---- accumulators ----------------------------------------------------
@@ -226,87 +211,52 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   const int hq = lane / T;  // lane group: which k-slice of the MFMA operands
   const int lt = lane % T;
 
-  // With kSpread, compute(tile) also issues the gather of the next tile into
-  // ndst (rg holds that tile's row offsets; the caller skips its own gather),
-  // and, inside its O^T MFMA stream (all of that gather has been issued by
-  // then), reads the row ids of tile + 2 into rg and the validity mask of
-  // tile + 1 into vmask_io, so no LDS round trip sits between the end of one
-  // tile's MFMAs and the next tile's.  Without kSpread, vmask_io is unused.
+  // compute(tile) also issues the gather of the next tile into ndst (rg
+  // holds that tile's row offsets), and, inside its O^T MFMA stream (all of
+  // that gather has been issued by then), reads the row ids of tile + 2 into
+  // rg and the validity mask of tile + 1 into vmask_io (on entry: this
+  // tile's), so no LDS round trip sits between the end of one tile's MFMAs
+  // and the next tile's.
   auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, RG& rg, u32x4* ndst, uint32_t& vmask_io) {
-    // validity of this wave's 32 keys
-    uint32_t vmask;
-    if constexpr (kSpread) {
-      vmask = vmask_io;
-    } else {
-      const int myid = s_idx[tile * C::NKT + ks * 32 + (lane & 31)];
-      vmask = (uint32_t)__ballot(myid >= 0);
-    }
+    const uint32_t vmask = vmask_io;  // validity of this wave's 32 keys
 
     // S^T = K Q^T
     acc_t sacc[C::MT];
     const uint32_t q_off = (uint32_t)(hl * C::QLP + hq) * 16u;
-    if constexpr (T == 32) {
-      // one 32-key M-tile: operands of step s + PDK are loaded before MFMA s
-      constexpr int PDK = 4;
-      // (swizzled tile: step s reads chunk 2s + hq = 8 (s >> 2) + v with
-      // v = 2 (s & 3) + hq at slot 8 (s >> 2) + (v ^ swz(row)): four bases)
-      uint32_t kb[C::SWZ ? 4 : 1];
-      if constexpr (C::SWZ) {
-        static_assert(C::LG == 2, "swizzled tiles are read with 32x32x16 operands");
+    // one 32-key M-tile: operands of step s + PDK are loaded before MFMA s
+    // (swizzled tile: step s reads chunk 2s + hq = 8 (s >> 2) + v with
+    // v = 2 (s & 3) + hq at slot 8 (s >> 2) + (v ^ swz(row)): four bases)
+    constexpr int PDK = 4;
+    uint32_t kb[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          kb[j] = (uint32_t)((ks * 32 + lt) * C::PK + ((2 * j + hq) ^ tile_swz(ks * 32 + lt))) * 16u;
-      } else {
-        kb[0] = (uint32_t)((ks * 32 + lt) * C::PK + hq) * 16u;
-      }
-      auto load_k = [&](int s) {
-        if constexpr (C::SWZ) return lds_read_b128(kt, kb[s & 3] + (uint32_t)(s >> 2) * 128u);
-        else return lds_read_b128(kt, kb[0] + (uint32_t)(s * C::LG) * 16u);
-      };
-      auto load_q = [&](int s) { return lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u); };
-      bf16x8 kbuf[PDK], qbuf[PDK];
+    for (int j = 0; j < 4; ++j)
+      kb[j] = (uint32_t)((ks * 32 + lt) * C::PK + ((2 * j + hq) ^ tile_swz(ks * 32 + lt))) * 16u;
+    auto load_k = [&](int s) { return lds_read_b128(kt, kb[s & 3] + (uint32_t)(s >> 2) * 128u); };
+    auto load_q = [&](int s) { return lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u); };
+    bf16x8 kbuf[PDK], qbuf[PDK];
 #pragma unroll
-      for (int i = 0; i < PDK; ++i) {
-        kbuf[i] = load_k(i);
-        if (i >= C::QREG) qbuf[i] = load_q(i);
-      }
-      bf16x8 pa = {}, pq = {};
-#pragma unroll
-      for (int s = 0; s < C::QSTEPS; ++s) {
-        const bf16x8 a = kbuf[s % PDK];
-        const bf16x8 bq = (s < C::QREG) ? qb[s < C::QREG ? s : 0] : qbuf[s % PDK];
-        if (s + PDK < C::QSTEPS) {
-          kbuf[s % PDK] = load_k(s + PDK);
-          if (s + PDK >= C::QREG) qbuf[s % PDK] = load_q(s + PDK);
-        }
-        if (s == 0)
-          M::mma_v0(a, bq, sacc[0]);
-        else
-          M::mma_v(a, bq, sacc[0], pa, pq);
-        pa = a;
-        pq = bq;
-        dma_at(s, rg, ndst);
-      }
-      M::drain_v(sacc[0], pa, pq);
-    } else {
-#pragma unroll
-      for (int mt = 0; mt < C::MT; ++mt) sacc[mt] = acc_t{};
-#pragma unroll
-      for (int s = 0; s < C::QSTEPS; ++s) {
-        bf16x8 bq;
-        if (s < C::QREG)
-          bq = qb[s < C::QREG ? s : 0];
-        else
-          bq = lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u);
-#pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) {
-          const int row = ks * 32 + mt * T + lt;
-          const int chunk = s * C::LG + hq;
-          const bf16x8 a = lds_read_b128(kt, (uint32_t)(row * C::PK + chunk) * 16u);
-          sacc[mt] = M::mma(a, bq, sacc[mt]);
-        }
-      }
+    for (int i = 0; i < PDK; ++i) {
+      kbuf[i] = load_k(i);
+      if (i >= C::QREG) qbuf[i] = load_q(i);
     }
+    bf16x8 pa = {}, pq = {};
+#pragma unroll
+    for (int s = 0; s < C::QSTEPS; ++s) {
+      const bf16x8 a = kbuf[s % PDK];
+      const bf16x8 bq = (s < C::QREG) ? qb[s < C::QREG ? s : 0] : qbuf[s % PDK];
+      if (s + PDK < C::QSTEPS) {
+        kbuf[s % PDK] = load_k(s + PDK);
+        if (s + PDK >= C::QREG) qbuf[s % PDK] = load_q(s + PDK);
+      }
+      if (s == 0)
+        M::mma_v0(a, bq, sacc[0]);
+      else
+        M::mma_v(a, bq, sacc[0], pa, pq);
+      pa = a;
+      pq = bq;
+      dma_at(s, rg, ndst);
+    }
+    M::drain_v(sacc[0], pa, pq);
 
     // Raw scores; invalid keys -> -inf.  A tile whose 32 keys are all valid
     // (the common case) skips the per-element mask.  The softmax scale is
@@ -355,12 +305,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     float tmax = sv[0];
 #pragma unroll
     for (int i = 1; i < NV; ++i) tmax = fmaxf(tmax, sv[i]);
-    if constexpr (T == 32) {
-      tmax = xor32_max(tmax);
-    } else {
-#pragma unroll
-      for (int o = T; o < 64; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
-    }
+    tmax = xor32_max(tmax);
     tmax *= p.scale_log2;
     const float m_new = fmaxf(m_used, tmax);
     if (__any(m_new > m_used + kRescaleSlack)) {
@@ -403,46 +348,34 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 
     // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
     // of operand i + PD are issued before MFMA i (software pipeline).
-    constexpr int VP = C::VK ? C::PK : C::PV;
+    constexpr int VP = C::PK;  // V rows are the K rows
     const int gi = lane & 15;         // lane within its 16-lane transpose group
     const int rr = gi >> 2;           // row within a run of 4 keys this lane loads
     const int cc = gi & 3;            // 4-dim column piece this lane loads
     const int mgrp = (lt >> 4) << 4;  // first MFMA row (dim) of the 16-lane group
     // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
-    const int run0 = (T == 32) ? 4 * hq : 4 * hq;
-    const int run1 = (T == 32) ? 8 + 4 * hq : 16 + 4 * hq;
-    // Unswizzled: operand (kk, ot) of a lane reads base + 16 kk rows + 32 ot
-    // dims.  Swizzled (T = 32): the lane's dims ot*32 + mgrp + 4cc .. +3 are
-    // in chunk 4 ot + cl, cl = mgrp / 8 + cc / 2, i.e. chunk 8 (ot >> 1) + v
-    // with v = 4 (ot & 1) + cl, at slot 8 (ot >> 1) + (v ^ swz(row)); rows
-    // r and r + 16 share swz, so each run needs one base per parity of ot.
-    uint32_t vb[2][C::SWZ ? 2 : 1];
+    const int run0 = 4 * hq;
+    const int run1 = 8 + 4 * hq;
+    // Operand (kk, ot) of a lane: its dims ot*32 + mgrp + 4cc .. +3 are in
+    // chunk 4 ot + cl, cl = mgrp / 8 + cc / 2, i.e. chunk 8 (ot >> 1) + v
+    // with v = 4 (ot & 1) + cl, at slot 8 (ot >> 1) + (v ^ swz(row)) of rows
+    // 16 kk + run + rr; rows r and r + 16 share swz, so each run needs one
+    // base per parity of ot.
+    uint32_t vb[2][2];
     {
       const int rows[2] = {ks * 32 + run0 + rr, ks * 32 + run1 + rr};
+      const int cl = mgrp / 8 + cc / 2;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (C::SWZ) {
-          const int cl = mgrp / 8 + cc / 2;
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int par = 0; par < 2; ++par)
-            vb[h][par] = (uint32_t)(rows[h] * VP + ((4 * par + cl) ^ tile_swz(rows[h]))) * 16u + (uint32_t)(cc & 1) * 8u;
-        } else {
-          vb[h][0] = (uint32_t)(rows[h] * VP) * 16u + (uint32_t)(mgrp + 4 * cc) * 2u;
-        }
-      }
+        for (int par = 0; par < 2; ++par)
+          vb[h][par] = (uint32_t)(rows[h] * VP + ((4 * par + cl) ^ tile_swz(rows[h]))) * 16u + (uint32_t)(cc & 1) * 8u;
     }
     auto load_a = [&](int i) -> bf16x8 {
       const int kk = i / C::OT, ot = i % C::OT;
-      uint32_t o0, o1;
-      if constexpr (C::SWZ) {
-        const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot >> 1) * 128u;
-        o0 = vb[0][ot & 1] + off;
-        o1 = vb[1][ot & 1] + off;
-      } else {
-        const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot * T) * 2u;  // T == 32 only has kk > 0
-        o0 = vb[0][0] + off;
-        o1 = vb[1][0] + off;
-      }
+      const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot >> 1) * 128u;
+      const uint32_t o0 = vb[0][ot & 1] + off;
+      const uint32_t o1 = vb[1][ot & 1] + off;
       const bf16x4 lo = lds_read_tr16(vt, o0);
       const bf16x4 hi = lds_read_tr16(vt, o1);
       return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -451,8 +384,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     // O^T MFMA after which the ids of tile + 2 are read, and the lag (in
     // MFMAs) after which they are used
     constexpr int kIdsAt = NLATE + 3, kIdsLag = 4;
-    static_assert(!kSpread || kIdsAt + kIdsLag + RG::RPW < NI, "id prefetch fits the O^T stream");
-    static_assert(!kSpread || kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kIdsAt,
+    static_assert(kIdsAt + kIdsLag + RG::RPW < NI, "id prefetch fits the O^T stream");
+    static_assert(kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kIdsAt,
                   "the gather of tile + 1 is issued before rg is overwritten");
     int ids_raw[RG::RPW];
     bool ids_ok = false;
@@ -475,26 +408,24 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       prev_a = a;
       prev_b = pb[i / C::OT];
       dma_at(C::QSTEPS + i, rg, ndst);
-      if constexpr (kSpread) {
-        if (i == kIdsAt) {
-          ids_ok = tile + 2 < ntiles;
-          RG::fetch(s_idx + (ids_ok ? tile + 2 : 0) * C::NKT, wave, ids_raw);
-          vm_raw = s_idx[(tile + 1 < ntiles ? tile + 1 : 0) * C::NKT + ks * 32 + (lane & 31)];
-        }
-        // one row offset per MFMA from kIdsAt + kIdsLag on (each pinned at
-        // its MFMA, so the wait for the reads is not hoisted next to them and
-        // the scalar work does not bunch up between two MFMAs)
-        if (i >= kIdsAt + kIdsLag && i < kIdsAt + kIdsLag + RG::RPW) {
-          const int r = i - kIdsAt - kIdsLag;
-          asm volatile("" : "+v"(ids_raw[r]));
-          rg.set_row(r, ids_raw[r], ids_ok, krow_bytes);
-          asm volatile("" : "+s"(rg.base[r]));
-        }
-        if (i == kIdsAt + kIdsLag + RG::RPW) {
-          asm volatile("" : "+v"(vm_raw));
-          vmask_io = (uint32_t)__ballot(vm_raw >= 0);
-          asm volatile("" : "+s"(vmask_io));
-        }
+      if (i == kIdsAt) {
+        ids_ok = tile + 2 < ntiles;
+        RG::fetch(s_idx + (ids_ok ? tile + 2 : 0) * C::NKT, wave, ids_raw);
+        vm_raw = s_idx[(tile + 1 < ntiles ? tile + 1 : 0) * C::NKT + ks * 32 + (lane & 31)];
+      }
+      // one row offset per MFMA from kIdsAt + kIdsLag on (each pinned at its
+      // MFMA, so the wait for the reads is not hoisted next to them and the
+      // scalar work does not bunch up between two MFMAs)
+      if (i >= kIdsAt + kIdsLag && i < kIdsAt + kIdsLag + RG::RPW) {
+        const int r = i - kIdsAt - kIdsLag;
+        asm volatile("" : "+v"(ids_raw[r]));
+        rg.set_row(r, ids_raw[r], ids_ok, krow_bytes);
+        asm volatile("" : "+s"(rg.base[r]));
+      }
+      if (i == kIdsAt + kIdsLag + RG::RPW) {
+        asm volatile("" : "+v"(vm_raw));
+        vmask_io = (uint32_t)__ballot(vm_raw >= 0);
+        asm volatile("" : "+s"(vmask_io));
       }
       if (i < NLATE) late_exp(i);
       if (i == NLATE) sum_range(0, NE0);
@@ -505,32 +436,25 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   };
 
   __syncthreads();  // indices staged
-  if constexpr (kSpread) {
+  {
     RG rg0;
     rg0.load_ids(s_idx, ntiles > 0, wave, krow_bytes);
 #pragma unroll
     for (int k = 0; k < RG::NI; ++k) rg0.issue(k, rk, s_k0, wave, lane);
-  } else {
-    if (ntiles > 0) gather(0, s_k0, s_v0);
   }
   load_q();
   __syncthreads();  // first tile and the LDS part of Q in place
 
-  // kSpread: row offsets of tile 1 (gathered during tile 0) and the validity
-  // mask of tile 0; compute() fetches those of the following tiles itself
+  // row offsets of tile 1 (gathered during tile 0) and the validity mask of
+  // tile 0; compute() fetches those of the following tiles itself
   RG rg;
-  uint32_t vmask = 0;
-  if constexpr (kSpread) {
-    rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, krow_bytes);
-    vmask = (uint32_t)__ballot(s_idx[ks * 32 + (lane & 31)] >= 0);
-  }
+  rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, krow_bytes);
+  uint32_t vmask = (uint32_t)__ballot(s_idx[ks * 32 + (lane & 31)] >= 0);
   for (int j = 0; j < ntiles; j += 2) {
-    if (!kSpread && j + 1 < ntiles) gather(j + 1, s_k1, s_v1);
-    compute(j, s_k0, C::VK ? s_k0 : s_v0, rg, s_k1, vmask);
+    compute(j, s_k0, s_k0, rg, s_k1, vmask);
     __syncthreads();
     if (j + 1 < ntiles) {
-      if (!kSpread && j + 2 < ntiles) gather(j + 2, s_k0, s_v0);
-      compute(j + 1, s_k1, C::VK ? s_k1 : s_v1, rg, s_k0, vmask);
+      compute(j + 1, s_k1, s_k1, rg, s_k0, vmask);
       __syncthreads();
     }
   }
@@ -539,66 +463,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   for (int i = 0; i < C::OT; ++i) M::drain(oacc[i]);
 
   // ---- finish: row sums over the lane groups sharing a head -------------------
-  float l_sum = l_part;
-  if constexpr (T == 32) {
-    l_sum = xor32_sum(l_sum);
-  } else {
-#pragma unroll
-    for (int o = T; o < 64; o <<= 1) l_sum += __shfl_xor(l_sum, o, 64);
-  }
-
-  float m_fin = m_used;
-  if constexpr (C::NSPLITW > 1) {
-    // merge the key sub-ranges of the waves sharing a head slice (through LDS;
-    // the last barrier of the tile loop ended every use of the tiles)
-    float* s_ml = reinterpret_cast<float*>(s_idx);  // [kWaves][2][T]
-    float* s_o = reinterpret_cast<float*>(s_k0);    // [kWaves][OT*CPL][64]
-    static_assert(2 * C::kWaves * T <= kIdxCap, "merge fits");
-    static_assert(C::kWaves * C::OT * C::CPL * 64 * 4 <= C::KBUF * 16, "merge fits");
-    if (lane < T) {
-      s_ml[(wave * 2 + 0) * T + lane] = m_used;
-      s_ml[(wave * 2 + 1) * T + lane] = l_sum;
-    }
-    __syncthreads();
-    float mm = kNegInf;
-#pragma unroll
-    for (int w = 0; w < C::NSPLITW; ++w) mm = fmaxf(mm, s_ml[((w * C::NSLICE + slice) * 2) * T + lt]);
-    float ltot = 0.f;
-#pragma unroll
-    for (int w = 0; w < C::NSPLITW; ++w) {
-      const float mw = s_ml[((w * C::NSLICE + slice) * 2) * T + lt];
-      const float lw = s_ml[((w * C::NSLICE + slice) * 2 + 1) * T + lt];
-      ltot += (mw == kNegInf) ? 0.f : lw * exp2f(mw - mm);
-    }
-    const float f = (m_used == kNegInf) ? 0.f : exp2f(m_used - mm);
-#pragma unroll
-    for (int i = 0; i < C::OT; ++i) {
-#pragma unroll
-      for (int e = 0; e < C::CPL; ++e) s_o[((wave * C::OT + i) * C::CPL + e) * 64 + lane] = oacc[i][e] * f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < C::OT; ++i) {
-#pragma unroll
-      for (int e = 0; e < C::CPL; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int w = 0; w < C::NSPLITW; ++w) acc += s_o[(((w * C::NSLICE + slice) * C::OT + i) * C::CPL + e) * 64 + lane];
-        oacc[i][e] = acc;
-      }
-    }
-    m_fin = mm;
-    l_sum = ltot;
-    // every wave now holds the merged result of its slice; waves ks > 0 stop
-    if (ks != 0) return;
-  }
+  const float l_sum = xor32_sum(l_part);
+  const float m_fin = m_used;
 
   // final output staged through LDS (every lane of the wave takes part in the
   // row stores, so lanes of absent heads stay until then and only skip their
   // own writes)
-  constexpr bool kStageOut = C::T == 32 && C::NSPLITW == 1 && C::DV == 512 && C::kWaves == 4 &&
-                             T * (C::DV + 8) * 2 <= C::KBUF * 16 && T * (C::DV + 8) * 2 <= C::QBUF * 8;
-  if (!kStageOut && !hvalid) return;
+  static_assert(T * (C::DV + 8) * 2 <= C::KBUF * 16 && T * (C::DV + 8) * 2 <= C::QBUF * 8,
+                "a wave's output block fits an idle tile buffer");
   const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
   // Split partials: normalised O of this split in bf16 plus its base-2 LSE
@@ -628,7 +500,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   bf16* const obase = partial ? p.part_o + ((int64_t)split * nrows + row0) * C::DV
                               : reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)(g * p.G) * p.o_sh;
   const int64_t orstride = partial ? C::DV : p.o_sh;
-  if constexpr (kStageOut) {
+  {
     // The accumulator layout gives each lane 4-dim pieces of one head, i.e.
     // stores that touch 32 rows per instruction.  Each wave instead writes
     // its T x DV bf16 block into a private LDS area (row pitch DV + 8, so the
@@ -659,25 +531,12 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(sbase + r * SP + 8 * lane);
       *reinterpret_cast<bf16x8*>(wbase + (int64_t)r * orstride + 8 * lane) = v;
     }
-  } else {
-    if (!hvalid) return;
-    bf16* orow = obase + (int64_t)hl * orstride;
-#pragma unroll
-    for (int ot = 0; ot < C::OT; ++ot) {
-#pragma unroll
-      for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
-        const int dim = ot * T + 4 * C::LG * q4 + 4 * hq;
-        bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
-                     (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
-        *reinterpret_cast<bf16x4*>(orow + dim) = v4;
-      }
-    }
   }
 }
 
-// Variants: (T, DQK, DV, NSLICE, NSPLITW, V is a prefix of K)
-using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;  // DeepSeek MLA: G = 128, d_qk 576 / d_v 512
-using CfgD128G16 = FwdCfg<16, 128, 128, 1, 2, false, 4>;    // d = 128, G <= 16 (2 waves: two workgroups per CU)
+// The one variant: DeepSeek MLA, G = 128 heads (65..128 accepted), d_qk 576 /
+// d_v 512 with V the first 512 dims of the K rows.
+using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;
 
 template <class C>
 hipError_t launch(const Params& p, hipStream_t s) {
@@ -696,23 +555,24 @@ bool rows_fit_32bit(const Params& p) {
   return kb < (int64_t)kOOB && vb < (int64_t)kOOB;
 }
 
+bool mla_supported(const Params& p) {
+  return p.Dqk == 576 && p.Dv == 512 && p.G <= 128 && p.G > 64 && v_is_k_prefix(p) && rows_fit_32bit(p);
+}
+
 }  // namespace
 
+// Dispatch over the MFMA forward kernels: the MLA kernel above and the
+// register-direct d = 128 kernel (sfa_fwd_d128.hip).
 int fwd_mfma_tile_keys(const Params& p) {
   if (p.Dqk == 576 && p.Dv == 512) return CfgMla::NKT;
-  return CfgD128G16::NKT;
+  return 32;  // d = 128 kernel: 32-key tiles
 }
 
-bool fwd_mfma_supported(const Params& p) {
-  if (!rows_fit_32bit(p)) return false;
-  if (p.Dqk == 576 && p.Dv == 512 && p.G <= 128 && p.G > 64 && v_is_k_prefix(p)) return true;
-  if (p.Dqk == 128 && p.Dv == 128 && p.G <= 16 && p.G > 4) return true;
-  return false;
-}
+bool fwd_mfma_supported(const Params& p) { return mla_supported(p) || fwd_d128_supported(p); }
 
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s) {
-  if (p.Dqk == 576 && p.Dv == 512) return launch<CfgMla>(p, s);
-  if (p.Dqk == 128 && p.Dv == 128) return launch<CfgD128G16>(p, s);
+  if (mla_supported(p)) return launch<CfgMla>(p, s);
+  if (fwd_d128_supported(p)) return launch_fwd_d128(p, s);
   return hipErrorNotSupported;
 }
 

@@ -86,11 +86,34 @@ def test_tiny_fp32_fwd_bwd():
 
 @pytest.mark.parametrize("S,K", [(256, 64), (1024, 256), (4096, 512)])
 def test_prefill_mqa_d128(S, K):
-    _say(f"prefill bf16 MQA G=16 d=128 S={S} K={K} (MFMA T=16 path)")
+    _say(f"prefill bf16 MQA G=16 d=128 S={S} K={K} (register-direct d=128 kernel)")
     w = make_workload("prefill", device=DEV, S=S, K=K)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     o_ref, l_ref = ref_forward(*_cpu(w)[:4], w.scale)
     _check_fwd(out, lse, o_ref, l_ref)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_d128_group_sizes_splits_kvlens_sink(G):
+    """The d=128 kernel for every group size it serves: 2 KV heads, 96 slots
+    (3 key tiles: an odd count), indices anywhere in [0, Skv) with -1 and
+    out-of-range entries, per-batch kv_lens, a sink, and forced split-k."""
+    _say(f"d=128 forward G={G} Hkv=2 B=2 S=40 Skv=300 K=96, splits 0/2/3")
+    g = torch.Generator(device="cpu").manual_seed(100 + G)
+    B, S, Skv, Hkv, K = 2, 40, 300, 2, 96
+    Hq = G * Hkv
+    q = torch.randn(B, S, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    idx = torch.randint(-40, Skv + 40, (B, S, Hkv, K), generator=g, dtype=torch.int32)
+    idx[0, 3] = -1  # a fully masked row
+    kv_lens = torch.tensor([300, 211], dtype=torch.int32)
+    sink = torch.linspace(-1.0, 2.0, Hq)
+    o_ref, l_ref = ref_forward(q, k, v, idx, 1.0 / math.sqrt(128), kv_lens=kv_lens, sink=sink)
+    for ns in (0, 2, 3):
+        out, lse = ops_amd.sfa_forward(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), None, kv_lens=kv_lens.to(DEV),
+                                       attn_sink=sink.to(DEV), num_splits=ns)
+        _check_fwd(out, lse, o_ref, l_ref)
 
 
 def test_train_gqa_fwd_full():
