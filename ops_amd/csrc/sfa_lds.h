@@ -18,17 +18,6 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// max / sum of x over lanes l and l ^ 16 (v_permlane16_swap exchanges the odd
-// 16-lane rows of one operand with the even rows of the other)
-__device__ __forceinline__ float xor16_max(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // LDS reads go through pointers derived from the __shared__ arrays themselves,
 // so the compiler keeps per-array alias information and does not make reads of
 // one tile buffer wait for the DMA still filling another.
