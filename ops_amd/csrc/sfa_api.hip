@@ -210,7 +210,9 @@ bool use_csr(const sfa_bwd_args* a, sfa::Params p) {
   p.do_sb = a->do_sb;  // (the range checks also cover dout)
   p.do_ss = a->do_ss;
   p.do_sh = a->do_sh;
-  return bwd_mfma_ok(a) && sfa::bwd_csr_supported(p);
+  // the deterministic scheme pairs the key-major dK/dV with the dQ kernel,
+  // which adds only the repeated-key slots' dK/dV
+  return bwd_mfma_ok(a) && sfa::bwd_csr_supported(p) && sfa::bwd_dq_supported(p);
 }
 
 size_t bwd_base_bytes(const sfa_fwd_args& f) {
@@ -277,7 +279,9 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
   if (e == hipSuccess && csr) e = sfa::launch_csr_index(p, s);  // before dQ: it reads the repeat flags
   if (e == hipSuccess) {
-    if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
+    if (csr)
+      e = sfa::launch_bwd_dq(p, s);
+    else if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
       e = sfa::launch_bwd_mfma(p, s);
     else
       e = sfa::launch_bwd_generic(p, f.dtype, s);

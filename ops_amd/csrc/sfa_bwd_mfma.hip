@@ -21,9 +21,8 @@
 //    and dV/dK rows are scattered with fp32 atomics into per-key
 //    accumulators (the reference's scheme, SFA.py:849-853): its cost does
 //    not grow with the density of the index set and it needs no inverted
-//    index of the top-k rows.  With the deterministic dK/dV path
-//    (sfa_bwd_csr.hip) only slots flagged as repeats of an earlier slot's
-//    key take this scatter (p.dup); a wave tile with no such slot skips it.
+//    index of the top-k rows.  This kernel serves the atomic dK/dV mode; the
+//    deterministic mode runs sfa_bwd_dq.hip (dQ) and sfa_bwd_csr.hip (dK/dV).
 //  * dQ partials of the 4 waves are summed through LDS at the end and
 //    written once (no atomics on dQ).
 //  * δ = Σ O·dO (minus any gradient on lse) comes from a preceding kernel.
@@ -69,7 +68,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
   __shared__ u32x4 s_v0[C::TBUF];
   __shared__ u32x4 s_v1[C::TBUF];
   __shared__ __attribute__((aligned(16))) bf16 s_patch[C::kWaves][2][16 * C::PSTRIDE];
-  __shared__ __attribute__((aligned(16))) uint8_t s_dup[kBwdIdxCap];  // slot takes the dK/dV scatter
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -88,13 +86,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
 
   {
     const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
-    const uint8_t* drow = p.dup ? p.dup + (((int64_t)b * p.Sq + t) * p.Hkv + g) * p.topk : nullptr;
     const int bound = bound_of(p, b);
     for (int i = tid; i < ntiles * C::NKT; i += C::kThreads) {
       const int id = (i < nslots) ? irow[i] : -1;
-      const bool valid = id >= 0 && id < bound;
-      s_idx[i] = valid ? id : -1;
-      s_dup[i] = valid && (drow == nullptr || drow[i] != 0);
+      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
     }
   }
 
@@ -217,8 +212,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
       }
     }
     // dV = P^T dO and dK = dS^T Q over the G heads; rows scattered atomically
-    const uint8_t* fb = s_dup + tile * C::NKT + ks * 32;
-    if (__ballot(fb[lane & 31] != 0) == 0u) return;  // wave-uniform: nothing to scatter
     const int rr = lt >> 2, cc = lt & 3;
 #pragma unroll
     for (int mk = 0; mk < 2; ++mk) {
@@ -226,8 +219,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
       const bf16x4 ap = lds_read_tr16(patch_p, poff);
       const bf16x4 as = lds_read_tr16(patch_s, poff);
       const int4 ids = *reinterpret_cast<const int4*>(ib + mk * 16 + 4 * hq);
-      const uchar4 fl = *reinterpret_cast<const uchar4*>(fb + mk * 16 + 4 * hq);
-      const int idv[4] = {fl.x ? ids.x : -1, fl.y ? ids.y : -1, fl.z ? ids.z : -1, fl.w ? ids.w : -1};
+      const int idv[4] = {ids.x, ids.y, ids.z, ids.w};
 #pragma unroll
       for (int nd = 0; nd < C::DT; ++nd) {
         const f32x4 dv = mma16x16(ap, doh[nd], f32x4{});

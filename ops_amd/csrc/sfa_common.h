@@ -120,6 +120,9 @@ int fwd_d128_tile_keys();
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
+// dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
+bool bwd_dq_supported(const Params& p);
+hipError_t launch_bwd_dq(const Params& p, hipStream_t s);
 // deterministic dK/dV
 bool bwd_csr_supported(const Params& p);
 void csr_geometry(Params& p);                 // fills kmap_w, nkb, nqb, lg_g, max_chunks
