@@ -136,10 +136,40 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   if (nslots < 0) nslots = 0;
   const int ntiles = (nslots + C::NKT - 1) / C::NKT;
 
-  // ---- stage indices (invalid -> -1) --------------------------------------
+  // ---- gather setup --------------------------------------------------------
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
+  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
+  const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
+
+  // The next tile's gather is issued from inside the current tile's S^T MFMA
+  // stream instead of in one burst.
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ> RG;
+  static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
+  // ---- first tile's gather, then stage indices (invalid -> -1) -----------
+  // Each wave reads the ids of its 8 rows of tile 0 straight from global
+  // memory (uniform addresses), so the first gather is in flight while the
+  // index row is staged and Q is loaded, instead of waiting for both.
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
+  const int bound = bound_of(p, b);
   {
-    const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
-    const int bound = bound_of(p, b);
+    RG rg0;
+    // (unconditional loads, all in flight together: slots past the split
+    // re-read its last slot, whose id is then discarded)
+    int raw[RG::RPW];
+#pragma unroll
+    for (int r = 0; r < RG::RPW; ++r) raw[r] = irow[min(wave * RG::RPW + r, max(nslots - 1, 0))];
+#pragma unroll
+    for (int r = 0; r < RG::RPW; ++r) {
+      const int id = raw[r];
+      rg0.set_row(r, (wave * RG::RPW + r < nslots && id >= 0 && id < bound) ? id : -1, true, krow_bytes);
+    }
+#pragma unroll
+    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, rk, s_k0, wave, lane);
+  }
+  {
     for (int i = tid; i < ntiles * C::NKT; i += C::kThreads) {
       const int id = (i < nslots) ? irow[i] : -1;
       s_idx[i] = (id >= 0 && id < bound) ? id : -1;
@@ -170,18 +200,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     }
   };
 
-  // ---- gather setup --------------------------------------------------------
-  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
-  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
-  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
-  const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
-
-  // The next tile's gather is issued from inside the current tile's S^T MFMA
-  // stream instead of in one burst.
-  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ> RG;
-  static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
   // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
   // tile's MFMA sequence (QSTEPS S^T MFMAs, then the O^T MFMAs)
 #ifndef SFA_DMA_STRIDE
@@ -435,15 +453,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     M::tail(prev_a, prev_b);
   };
 
-  __syncthreads();  // indices staged
-  {
-    RG rg0;
-    rg0.load_ids(s_idx, ntiles > 0, wave, krow_bytes);
-#pragma unroll
-    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, rk, s_k0, wave, lane);
-  }
   load_q();
-  __syncthreads();  // first tile and the LDS part of Q in place
+  __syncthreads();  // indices staged, first tile and the LDS part of Q in place
 
   // row offsets of tile 1 (gathered during tile 0) and the validity mask of
   // tile 0; compute() fetches those of the following tiles itself
