@@ -12,7 +12,9 @@ measured in the same run and reported under ``workloads``:
 * ``train_gqa``   GQA fwd + bwd (deterministic and atomic dK/dV), B=2, S=8192,
                   Hq=32, Hkv=2, top-k 1024
 * ``mla_decode``  B=64 x 1 query, KV [64, 65536, 1, 576], top-k 2048, split-k
-                  + combine, caches flushed (by a 1 GiB read) before every step (GB/s)
+                  + combine, caches flushed (by a 1 GiB read) before every step (GB/s);
+                  ``paged``: the same cache as a 64-row-page pool (4.8 GB, pages
+                  shuffled) read through a block table
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -196,9 +198,21 @@ def bench_mla_decode(args):
     times, _ = time_steps(fn, args.steps * 4, args.warmup, before=lambda: flush.sum())
     us = sum(times) / len(times) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"metric": "decode GB/s (algorithmic bytes, cache flushed)", "value": gbs, "unit": "GB/s", "us": us,
-            "bytes": nbytes, "frac_of_peak": gbs / PEAK_HBM_GBS, "tflops": fwd_flops(w, pairs) / (us * 1e-6) / 1e12,
-            "config": {"B": 64, "Skv": 65536, "Hq": 128, "d_qk": 576, "d_v": 512, "topk": 2048}}
+    res = {"metric": "decode GB/s (algorithmic bytes, cache flushed)", "value": gbs, "unit": "GB/s", "us": us,
+           "bytes": nbytes, "frac_of_peak": gbs / PEAK_HBM_GBS, "tflops": fwd_flops(w, pairs) / (us * 1e-6) / 1e12,
+           "config": {"B": 64, "Skv": 65536, "Hq": 128, "d_qk": 576, "d_v": 512, "topk": 2048}}
+    # the same step over a paged cache (block table of 64-row pages)
+    from ops_amd.workloads import page_kv
+    kp, vp, bt = page_kv(w.k, w.v, 64, seed=1)
+    pbytes = nbytes + pairs * 4  # one block-table entry per valid slot
+    fnp = lambda: ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
+    times, _ = time_steps(fnp, args.steps * 4, args.warmup, before=lambda: flush.sum())
+    pus = sum(times) / len(times) * 1e3
+    res["paged"] = {"value": pbytes / (pus * 1e-6) / 1e9, "unit": "GB/s", "us": pus, "bytes": pbytes,
+                    "frac_of_peak": pbytes / (pus * 1e-6) / 1e9 / PEAK_HBM_GBS, "page_size": 64,
+                    "pool_bytes": kp.numel() * kp.element_size()}
+    del kp, vp
+    return res
 
 
 def main():

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SFA_ABI_VERSION 1
+#define SFA_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define SFA_API __attribute__((visibility("default")))
@@ -101,6 +101,23 @@ typedef struct sfa_bwd_args {
   int32_t flags;                 /* reserved, must be 0                                 */
 } sfa_bwd_args;
 
+/* Paged KV cache (block table) for sfa_fwd_paged.  k and v then point to
+ * page pools [num_pages, page_size, Hkv, D]: k_sb / v_sb are the page strides,
+ * k_ss / v_ss the row strides within a page, k_sh / v_sh the head strides.
+ * Logical key position i of sequence b (what idx holds) is row
+ * i % page_size of page block_table[b * bt_sb + i / page_size].
+ * A slot is valid iff 0 <= idx < bound (bound = kv_lens[b] clamped to Skv,
+ * else Skv; Skv <= max_pages * page_size) and its page id lies in
+ * [0, num_pages); an unmapped page (e.g. -1) makes the slot invalid. */
+typedef struct sfa_kv_pages {
+  const int32_t* block_table;    /* [B, max_pages] int32 page ids                     */
+  int64_t bt_sb;                 /* block-table row stride (elements)                 */
+  int32_t max_pages;             /* block-table columns                               */
+  int32_t page_size;             /* rows per page, a power of two                     */
+  int32_t num_pages;             /* pages in each pool; num_pages * page_size < 2^31  */
+  int32_t flags;                 /* reserved, must be 0                               */
+} sfa_kv_pages;
+
 /* Library ABI version (SFA_ABI_VERSION of the build). */
 SFA_API int sfa_abi_version(void);
 
@@ -115,6 +132,16 @@ SFA_API size_t sfa_fwd_workspace_size(const sfa_fwd_args* a);
 /* Forward: out = softmax(scale * q k[idx]^T) v[idx], lse = log-sum-exp.
  * Replaces `_attn_fwd` (SFA.py:483-587 via SFA.py:122-159). */
 SFA_API int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace sfa_fwd_paged needs for `a` and `pages`. */
+SFA_API size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages);
+
+/* Forward over a paged KV cache: the same result as sfa_fwd on the contiguous
+ * cache the block table describes.  The reference has no paged variant (its
+ * `_attn_fwd`, SFA.py:483-587, reads one contiguous [S_kv, B, D] kv tensor);
+ * this is the serving-side layout of the decode step that precedes it. */
+SFA_API int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace sfa_bwd needs for `a` (fp32 dK/dV accumulators,
  * delta, and the CSR arrays in SFA_DKV_CSR mode).

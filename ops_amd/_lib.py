@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsfa.so"
 
-SFA_ABI_VERSION = 1
+SFA_ABI_VERSION = 2
 SFA_DTYPE_F32 = 0
 SFA_DTYPE_BF16 = 1
 SFA_DKV_AUTO = 0
@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "sfa_fwd",
     "sfa_bwd_workspace_size",
     "sfa_bwd",
+    "sfa_fwd_paged_workspace_size",
+    "sfa_fwd_paged",
 )
 
 _i32 = ctypes.c_int32
@@ -75,6 +77,14 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class KvPages(ctypes.Structure):
+    """Mirror of ``sfa_kv_pages``."""
+    _fields_ = [
+        ("block_table", _vp), ("bt_sb", _i64),
+        ("max_pages", _i32), ("page_size", _i32), ("num_pages", _i32), ("flags", _i32),
+    ]
+
+
 class SFAError(RuntimeError):
     """A failure reported by libsfa (HIP runtime or unsupported request)."""
 
@@ -109,6 +119,10 @@ def load() -> ctypes.CDLL:
         lib.sfa_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.sfa_bwd.restype = ctypes.c_int
         lib.sfa_bwd.argtypes = [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]
+        lib.sfa_fwd_paged_workspace_size.restype = ctypes.c_size_t
+        lib.sfa_fwd_paged_workspace_size.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(KvPages)]
+        lib.sfa_fwd_paged.restype = ctypes.c_int
+        lib.sfa_fwd_paged.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(KvPages), _vp, ctypes.c_size_t, _vp]
         ver = lib.sfa_abi_version()
         if ver != SFA_ABI_VERSION:
             raise SFAError(f"libsfa ABI version {ver} != expected {SFA_ABI_VERSION}; rebuild")

@@ -3,6 +3,7 @@
 // or synchronises; all work goes onto the caller's stream.
 
 #include <math.h>
+#include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -52,9 +53,32 @@ int check_fwd(const sfa_fwd_args* a) {
   return SFA_OK;
 }
 
-sfa::Params to_params(const sfa_fwd_args* a) {
+// Page-table checks of sfa_fwd_paged (after check_fwd).
+int check_pages(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
+  if (pg == nullptr || pg->block_table == nullptr) return fail(SFA_E_INVALID, "null page table");
+  if (pg->flags != 0) return fail(SFA_E_INVALID, "page table flags must be 0");
+  if (pg->page_size <= 0 || (pg->page_size & (pg->page_size - 1)) != 0)
+    return fail(SFA_E_INVALID, "page_size must be a power of two (got %d)", pg->page_size);
+  if (pg->max_pages <= 0 || pg->num_pages <= 0) return fail(SFA_E_INVALID, "max_pages and num_pages must be positive");
+  if ((int64_t)pg->num_pages * pg->page_size > INT32_MAX)
+    return fail(SFA_E_INVALID, "num_pages * page_size must stay below 2^31");
+  if (a->B > 1 && pg->bt_sb < pg->max_pages)
+    return fail(SFA_E_INVALID, "block-table row stride %lld is below max_pages %d", (long long)pg->bt_sb,
+                pg->max_pages);
+  if ((int64_t)a->Skv > (int64_t)pg->max_pages * pg->page_size)
+    return fail(SFA_E_INVALID, "Skv %d exceeds max_pages * page_size", a->Skv);
+  return SFA_OK;
+}
+
+sfa::Params to_params(const sfa_fwd_args* a, const sfa_kv_pages* pg = nullptr) {
   sfa::Params p;
   memset(&p, 0, sizeof(p));
+  if (pg != nullptr) {
+    p.block_table = pg->block_table;
+    p.bt_sb = pg->bt_sb;
+    p.page_shift = __builtin_ctz((unsigned)pg->page_size);
+    p.num_pages = pg->num_pages;
+  }
   p.q = a->q; p.k = a->k; p.v = a->v; p.idx = a->idx; p.kv_lens = a->kv_lens; p.sink = a->sink;
   p.out = a->out; p.lse = a->lse;
   p.q_sb = a->q_sb; p.q_ss = a->q_ss; p.q_sh = a->q_sh;
@@ -106,9 +130,9 @@ constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
 constexpr int kIdxCap = 2048;
 constexpr int kMaxSplits = 64;  // the combine kernel holds one split per lane of a wave
 
-FwdPlan plan_fwd(const sfa_fwd_args* a) {
+FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
   FwdPlan pl{};
-  sfa::Params p = to_params(a);
+  sfa::Params p = to_params(a, pg);
   pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p) &&
             (a->topk + kIdxCap - 1) / kIdxCap <= kMaxSplits;
   int splits = 1;
@@ -152,27 +176,12 @@ int check_generic_fwd(const sfa_fwd_args* a) {
   return SFA_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int sfa_abi_version(void) { return SFA_ABI_VERSION; }
-
-const char* sfa_last_error(void) { return g_err; }
-
-size_t sfa_fwd_workspace_size(const sfa_fwd_args* a) {
-  if (check_fwd(a) != SFA_OK) return 0;
-  const FwdPlan pl = plan_fwd(a);
-  return pl.part_o_bytes + pl.part_lse_bytes;
-}
-
-int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  g_err[0] = 0;
-  int rc = check_fwd(a);
-  if (rc != SFA_OK) return rc;
+// The forward of sfa_fwd (pg == nullptr) and sfa_fwd_paged, after validation.
+int run_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, void* workspace, size_t workspace_bytes, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  const FwdPlan pl = plan_fwd(a);
-  sfa::Params p = to_params(a);
+  const FwdPlan pl = plan_fwd(a, pg);
+  sfa::Params p = to_params(a, pg);
+  int rc;
   hipError_t e;
   if (pl.mfma) {
     p.num_splits = pl.num_splits;
@@ -197,6 +206,42 @@ int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void
   e = sfa::launch_fwd_generic(p, a->dtype, s);
   if (e != hipSuccess) return hip_fail(e, "sfa_fwd (generic)");
   return SFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sfa_abi_version(void) { return SFA_ABI_VERSION; }
+
+const char* sfa_last_error(void) { return g_err; }
+
+size_t sfa_fwd_workspace_size(const sfa_fwd_args* a) {
+  if (check_fwd(a) != SFA_OK) return 0;
+  const FwdPlan pl = plan_fwd(a, nullptr);
+  return pl.part_o_bytes + pl.part_lse_bytes;
+}
+
+int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  const int rc = check_fwd(a);
+  if (rc != SFA_OK) return rc;
+  return run_fwd(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages) {
+  if (check_fwd(a) != SFA_OK || check_pages(a, pages) != SFA_OK) return 0;
+  const FwdPlan pl = plan_fwd(a, pages);
+  return pl.part_o_bytes + pl.part_lse_bytes;
+}
+
+int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  g_err[0] = 0;
+  int rc = check_fwd(a);
+  if (rc == SFA_OK) rc = check_pages(a, pages);
+  if (rc != SFA_OK) return rc;
+  return run_fwd(a, pages, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

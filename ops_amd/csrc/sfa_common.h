@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/sfa.h"
 
 namespace sfa {
@@ -30,6 +32,13 @@ struct Params {
   int64_t o_sb, o_ss, o_sh;
   int64_t l_sb, l_ss, l_sh;
   int B, Sq, Skv, Hq, Hkv, Dqk, Dv, topk, G;
+  // paged KV (sfa_fwd_paged): k / v are pools [num_pages][page][Hkv][D] with
+  // k_sb / v_sb the page strides; logical key i of sequence b is row
+  // i & (page - 1) of page block_table[b * bt_sb + (i >> page_shift)]
+  const int32_t* block_table;  // nullptr: contiguous [B][Skv][Hkv][D] k / v
+  int64_t bt_sb;
+  int page_shift;
+  int num_pages;
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores in base-2 units
   // split-k partial results (forward, num_splits > 1)
@@ -80,6 +89,35 @@ __device__ __forceinline__ int bound_of(const Params& p, int b) {
   return n < p.Skv ? n : p.Skv;
 }
 
+// Pool row (page * page_size + offset) of logical key id of sequence b in
+// paged mode, or -1 when the slot is invalid (id outside [0, bound)) or its
+// page is unmapped (block-table entry outside [0, num_pages)).
+__device__ __forceinline__ int paged_row(const Params& p, int b, int id, int bound) {
+  if (id < 0 || id >= bound) return -1;
+  const int pg = p.block_table[b * p.bt_sb + (id >> p.page_shift)];
+  if (pg < 0 || pg >= p.num_pages) return -1;
+  return (pg << p.page_shift) | (id & ((1 << p.page_shift) - 1));
+}
+
+// The staged id of a slot: the key row itself (contiguous k / v) or its pool
+// row (paged), -1 for an invalid slot.
+template <bool PAGED>
+__device__ __forceinline__ int staged_id(const Params& p, int b, int id, int bound) {
+  if (PAGED) return paged_row(p, b, id, bound);
+  return (id >= 0 && id < bound) ? id : -1;
+}
+
+// Byte offset of pool row r from the pool base (paged mode): page r >> shift
+// at page_bytes, row r & mask at row_bytes (64-bit: pools may exceed 4 GiB).
+__device__ __forceinline__ uint64_t pool_row_offset(uint32_t r, int shift, uint64_t page_bytes, uint32_t row_bytes) {
+  return (uint64_t)(r >> shift) * page_bytes + (uint64_t)(r & ((1u << shift) - 1u)) * row_bytes;
+}
+
+// Zeros that padding rows of the 64-bit (paged) gathers read instead of an
+// out-of-range buffer offset: one row of up to 1280 bytes (one copy per
+// translation unit that uses it).
+static __device__ const u32x4 kZeroRow[80] = {};
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
@@ -111,7 +149,7 @@ hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb
                              void* dv, int64_t dv_sb, int64_t dv_ss, int64_t dv_sh, hipStream_t s);
 hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
 // MFMA paths: return hipErrorNotSupported when the shape has no variant.
-hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);
+hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);  // paged when p.block_table != nullptr
 bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
 // d = 128, G <= 16: register-direct gather (sfa_fwd_d128.hip)

@@ -14,6 +14,8 @@
 //    reads (ds_read_b64_tr_b16) produce the V^T operands of O^T = V^T P^T;
 //  * one wave per workgroup, no barrier inside the tile loop and ~17 KB of
 //    LDS, so two waves share each SIMD and hide each other's load latency.
+//  * paged KV (PAGED = true): indices are staged as pool rows (block table)
+//    and the rows loaded from 64-bit addresses; padding rows read kZeroRow.
 // (Measured against the LDS-staged variant of sfa_fwd_mfma.hip: MQA prefill
 // 140 -> 122 us, GQA training forward 2.00 -> 1.75 ms.)
 
@@ -31,6 +33,7 @@ constexpr int kQSteps = 4;      // 128 / 32 contraction steps of S^T
 constexpr int kOT = 8;          // 128 / 16 O^T dim tiles
 constexpr int kPV = 17;         // V staging row pitch in 16-byte slots (odd: conflict-free reads)
 
+template <bool PAGED>
 __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   using M = Mfma<16>;
   typedef M::acc_t acc_t;
@@ -72,10 +75,7 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   {
     const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
     const int bound = bound_of(p, b);
-    for (int i = lane; i < ntiles * 32; i += 64) {
-      const int id = (i < nslots) ? irow[i] : -1;
-      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
-    }
+    for (int i = lane; i < ntiles * 32; i += 64) s_idx[i] = (i < nslots) ? staged_id<PAGED>(p, b, irow[i], bound) : -1;
   }
 
   // ---- Q^T B operands (16x16x32: lane holds head lt, dims 32 s + 8 hq ..) ---
@@ -92,12 +92,14 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
     }
   }
 
-  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+  // contiguous: buffer resources over this (batch, kv head)'s rows; paged:
+  // the pools (the batch lives in the block table)
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * ((PAGED ? 0 : b * p.k_sb) + g * p.k_sh);
   const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
-  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
+  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * ((PAGED ? 0 : b * p.v_sb) + g * p.v_sh);
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
 
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
 
@@ -106,25 +108,46 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   // V: 16-byte chunk 4 s + hq of the row, written to the staging area).
   // Invalid keys read from an out-of-range offset and get zeros.
   auto load_tile = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
-    uint32_t ko[2], vo[2];
+    if constexpr (PAGED) {
+      const char* ka[2];
+      const char* va[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int id = s_idx[32 * j + 16 * mt + lt];
-      ko[mt] = id >= 0 ? __umul24((uint32_t)id, krow_bytes) : kOOB;
-      vo[mt] = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) : kOOB;
+      for (int mt = 0; mt < 2; ++mt) {
+        const int id = s_idx[32 * j + 16 * mt + lt];
+        ka[mt] = id >= 0 ? kbase + pool_row_offset((uint32_t)id, p.page_shift, (uint64_t)(2 * p.k_sb), krow_bytes)
+                         : reinterpret_cast<const char*>(kZeroRow);
+        va[mt] = id >= 0 ? vbase + pool_row_offset((uint32_t)id, p.page_shift, (uint64_t)(2 * p.v_sb), vrow_bytes)
+                         : reinterpret_cast<const char*>(kZeroRow);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kr[4 * mt + s] = *reinterpret_cast<const bf16x8*>(ka[mt] + 64 * s + 16 * hq);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) vr[4 * mt + s] = *reinterpret_cast<const bf16x8*>(va[mt] + 64 * s + 16 * hq);
+    } else {
+      uint32_t ko[2], vo[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int id = s_idx[32 * j + 16 * mt + lt];
+        ko[mt] = id >= 0 ? __umul24((uint32_t)id, krow_bytes) : kOOB;
+        vo[mt] = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) : kOOB;
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          kr[4 * mt + s] = __builtin_bit_cast(
+              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          vr[4 * mt + s] = __builtin_bit_cast(
+              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
     }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        kr[4 * mt + s] = __builtin_bit_cast(
-            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        vr[4 * mt + s] = __builtin_bit_cast(
-            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
   };
 
   // ---- accumulators ----------------------------------------------------
@@ -260,12 +283,17 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
 bool fwd_d128_supported(const Params& p) {
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128);
-  return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && kb < (int64_t)kOOB && vb < (int64_t)kOOB;
+  // contiguous rows use 32-bit buffer offsets, paged pools 64-bit addresses
+  const bool addressable = p.block_table != nullptr || (kb < (int64_t)kOOB && vb < (int64_t)kOOB);
+  return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && addressable;
 }
 
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
-  hipLaunchKernelGGL(fwd_d128_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
+  if (p.block_table)
+    hipLaunchKernelGGL(fwd_d128_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, p);
+  else
+    hipLaunchKernelGGL(fwd_d128_kernel<false>, dim3((unsigned)n), dim3(64), 0, s, p);
   return hipGetLastError();
 }
 

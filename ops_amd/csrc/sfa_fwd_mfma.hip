@@ -31,6 +31,10 @@
 //    the exact softmax.
 //  * Split-k over the top-k slots (decode) writes normalised bf16 partial
 //    outputs plus their base-2 LSE; sfa::launch_combine merges them.
+//  * Paged KV (PAGED = true, sfa_fwd_paged): the index staging turns each
+//    logical key into its pool row through the block table, and the gather
+//    uses 64-bit addresses (global_load_lds_dwordx4; a pool can exceed the
+//    4 GiB a buffer offset reaches), padding rows reading a zero row.
 //
 // MFMA register layouts used (gfx950 32x32x16 bf16, 8 values per lane, T = 32):
 //   A[m][k]: lane l holds m = l % T, k = 8*(l / T) + j        (j = 0..7)
@@ -85,7 +89,7 @@ struct FwdCfg {
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
 // the compiler keeps per-array alias information and does not make the reads
 // of one tile buffer wait for the DMA still filling the other.
-template <class C>
+template <class C, bool PAGED>
 __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   constexpr int T = C::T;
   using M = Mfma<T>;
@@ -136,17 +140,23 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   if (nslots < 0) nslots = 0;
   const int ntiles = (nslots + C::NKT - 1) / C::NKT;
 
-  // ---- gather setup --------------------------------------------------------
-  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
-  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
-  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
-  const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + C::DV)));
+  // ---- gather setup (V rows are the K rows: one gather) --------------------
+  typedef typename std::conditional<PAGED, PoolRows, BufRows>::type Src;
+  Src ksrc;
+  if constexpr (PAGED) {
+    ksrc.base = reinterpret_cast<const char*>(p.k) + 2 * g * p.k_sh;
+    ksrc.page_bytes = (uint64_t)(2 * p.k_sb);
+    ksrc.row_bytes = (uint32_t)(2 * p.k_ss);
+    ksrc.shift = p.page_shift;
+  } else {
+    const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+    ksrc.rs = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
+    ksrc.row_bytes = (uint32_t)(2 * p.k_ss);
+  }
 
   // The next tile's gather is issued from inside the current tile's S^T MFMA
   // stream instead of in one burst.
-  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ> RG;
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src> RG;
   static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
   // ---- first tile's gather, then stage indices (invalid -> -1) -----------
   // Each wave reads the ids of its 8 rows of tile 0 straight from global
@@ -162,18 +172,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
     for (int r = 0; r < RG::RPW; ++r) raw[r] = irow[min(wave * RG::RPW + r, max(nslots - 1, 0))];
 #pragma unroll
-    for (int r = 0; r < RG::RPW; ++r) {
-      const int id = raw[r];
-      rg0.set_row(r, (wave * RG::RPW + r < nslots && id >= 0 && id < bound) ? id : -1, true, krow_bytes);
-    }
+    for (int r = 0; r < RG::RPW; ++r)
+      rg0.set_row(r, (wave * RG::RPW + r < nslots) ? staged_id<PAGED>(p, b, raw[r], bound) : -1, true, ksrc);
 #pragma unroll
-    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, rk, s_k0, wave, lane);
+    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, ksrc, s_k0, wave, lane);
   }
   {
-    for (int i = tid; i < ntiles * C::NKT; i += C::kThreads) {
-      const int id = (i < nslots) ? irow[i] : -1;
-      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
-    }
+    for (int i = tid; i < ntiles * C::NKT; i += C::kThreads)
+      s_idx[i] = (i < nslots) ? staged_id<PAGED>(p, b, irow[i], bound) : -1;
   }
 
   // ---- Q^T B operands in registers ------------------------------------
@@ -216,7 +222,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // idle buffer)
   auto dma_at = [&](int m, const RG& rg, u32x4* ndst) {
     if (m >= kDmaFirst && (m - kDmaFirst) % kDmaStride == 0 && (m - kDmaFirst) / kDmaStride < RG::NI)
-      rg.issue((m - kDmaFirst) / kDmaStride, rk, ndst, wave, lane);
+      rg.issue((m - kDmaFirst) / kDmaStride, ksrc, ndst, wave, lane);
   };
 
   // ---- accumulators ----------------------------------------------------
@@ -437,7 +443,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       if (i >= kIdsAt + kIdsLag && i < kIdsAt + kIdsLag + RG::RPW) {
         const int r = i - kIdsAt - kIdsLag;
         asm volatile("" : "+v"(ids_raw[r]));
-        rg.set_row(r, ids_raw[r], ids_ok, krow_bytes);
+        rg.set_row(r, ids_raw[r], ids_ok, ksrc);
         asm volatile("" : "+s"(rg.base[r]));
       }
       if (i == kIdsAt + kIdsLag + RG::RPW) {
@@ -453,19 +459,27 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     M::tail(prev_a, prev_b);
   };
 
+  // vmcnt(0) before the barriers that publish a gathered tile, where the
+  // compiler does not see the DMA (PoolRows)
+  auto dma_done = [&]() {
+    if constexpr (Src::kUntrackedDma) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  };
   load_q();
+  dma_done();
   __syncthreads();  // indices staged, first tile and the LDS part of Q in place
 
   // row offsets of tile 1 (gathered during tile 0) and the validity mask of
   // tile 0; compute() fetches those of the following tiles itself
   RG rg;
-  rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, krow_bytes);
+  rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, ksrc);
   uint32_t vmask = (uint32_t)__ballot(s_idx[ks * 32 + (lane & 31)] >= 0);
   for (int j = 0; j < ntiles; j += 2) {
     compute(j, s_k0, s_k0, rg, s_k1, vmask);
+    dma_done();
     __syncthreads();
     if (j + 1 < ntiles) {
       compute(j + 1, s_k1, s_k1, rg, s_k0, vmask);
+      dma_done();
       __syncthreads();
     }
   }
@@ -552,7 +566,10 @@ using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;
 template <class C>
 hipError_t launch(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
-  hipLaunchKernelGGL(fwd_mfma_kernel<C>, dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
+  if (p.block_table)
+    hipLaunchKernelGGL((fwd_mfma_kernel<C, true>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((fwd_mfma_kernel<C, false>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
   return hipGetLastError();
 }
 
@@ -560,7 +577,10 @@ bool v_is_k_prefix(const Params& p) {
   return p.v == p.k && p.v_sb == p.k_sb && p.v_ss == p.k_ss && p.v_sh == p.k_sh;
 }
 
+// contiguous rows are addressed by 32-bit buffer offsets; paged pools by
+// 64-bit addresses (pool rows fit an int by the API's check)
 bool rows_fit_32bit(const Params& p) {
+  if (p.block_table) return true;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
   return kb < (int64_t)kOOB && vb < (int64_t)kOOB;

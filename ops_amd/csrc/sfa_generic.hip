@@ -64,14 +64,24 @@ __global__ __launch_bounds__(kThreads) void fwd_generic_kernel(Params p) {
 
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
   const int bound = bound_of(p, b);
-  const T* kb = reinterpret_cast<const T*>(p.k) + b * p.k_sb + g * p.k_sh;
-  const T* vb = reinterpret_cast<const T*>(p.v) + b * p.v_sb + g * p.v_sh;
+  // paged KV: k / v are pools and the slot's pool row comes from the block
+  // table (-1 for an invalid slot or an unmapped page)
+  const bool paged = p.block_table != nullptr;
+  const T* kb = reinterpret_cast<const T*>(p.k) + (paged ? 0 : b * p.k_sb) + g * p.k_sh;
+  const T* vb = reinterpret_cast<const T*>(p.v) + (paged ? 0 : b * p.v_sb) + g * p.v_sh;
+  const int pmask = (1 << p.page_shift) - 1;
+  auto key_row = [&](const T* base, int id, int64_t sb, int64_t ss) -> const T* {
+    if (paged) {
+      const int r = paged_row(p, b, id, bound);
+      return r < 0 ? nullptr : base + (int64_t)(r >> p.page_shift) * sb + (int64_t)(r & pmask) * ss;
+    }
+    return (id >= 0 && id < bound) ? base + (int64_t)id * ss : nullptr;
+  };
 
   for (int j = wave; j < p.topk; j += kWaves) {
-    const int id = irow[j];
+    const T* kr = key_row(kb, irow[j], p.k_sb, p.k_ss);
     float s = kNegInf;
-    if (id >= 0 && id < bound) {
-      const T* kr = kb + (int64_t)id * p.k_ss;
+    if (kr != nullptr) {
       float acc = 0.f;
       for (int d = lane; d < p.Dqk; d += 64) acc += qs[d] * to_f32(kr[d]);
       s = wave_sum(acc) * p.scale_log2;
@@ -102,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void fwd_generic_kernel(Params p) {
     float acc = 0.f;
     for (int j = 0; j < p.topk; ++j) {
       const float e = sc[j];
-      if (e != 0.f) acc += e * to_f32(vb[(int64_t)irow[j] * p.v_ss + d]);
+      if (e != 0.f) acc += e * to_f32(key_row(vb, irow[j], p.v_sb, p.v_ss)[d]);
     }
     orow[d] = from_f32<T>(acc * inv);
   }

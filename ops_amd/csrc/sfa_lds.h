@@ -109,7 +109,50 @@ __device__ __forceinline__ int tile_swz(int r) {
 // caller can spread them over its MFMA stream.
 constexpr uint32_t kOOBRow = 0x80001000u;
 
-template <int NKT, int CH, int NWAVES, bool SWZ>
+// Row sources of RowGather.  base_t is what a row's base is held in; a
+// padding row (id < 0 or !valid) gets a base whose every lane offset reads
+// zeros.
+// Contiguous rows of one (batch, kv head) slice: 32-bit offsets into a
+// buffer resource, padding rows out of range.
+struct BufRows {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t row_bytes;
+  typedef uint32_t base_t;
+  __device__ __forceinline__ base_t row_base(int id, bool valid) const {
+    return (valid && id >= 0) ? __umul24((uint32_t)id, row_bytes) : kOOBRow;
+  }
+  __device__ __forceinline__ void load_lds16(u32x4* dst, base_t off) const {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, off, 0, 0, 0);
+  }
+  static constexpr bool kUntrackedDma = false;  // the compiler tracks the DMA
+};
+// Rows of a paged pool (ids are pool rows): 64-bit addresses, since a pool
+// may exceed the 4 GiB a buffer offset reaches; padding rows read kZeroRow.
+// The DMA (global_load_lds_dwordx4: M0 = the wave's LDS destination, lane l
+// writes 16 bytes at M0 + 16 l) is issued as inline asm: the compiler counts
+// its builtin form against the LDS counter too, which turns every later
+// operand read's wait into lgkmcnt(0) and serialises the tile's LDS reads.
+// The hardware counts it on vmcnt only, and the compiler does not see it, so
+// the kernel waits for vmcnt(0) itself before the barrier that publishes a
+// tile (waits the compiler inserts for other loads only get stricter).
+struct PoolRows {
+  const char* base;      // pool base + the kv head's offset
+  uint64_t page_bytes;   // page stride
+  uint32_t row_bytes;    // row stride within a page
+  int shift;             // log2(rows per page)
+  typedef uint64_t base_t;
+  __device__ __forceinline__ base_t row_base(int id, bool valid) const {
+    return (valid && id >= 0) ? (uint64_t)(uintptr_t)base + pool_row_offset((uint32_t)id, shift, page_bytes, row_bytes)
+                              : (uint64_t)(uintptr_t)kZeroRow;
+  }
+  __device__ __forceinline__ void load_lds16(u32x4* dst, base_t addr) const {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(addr) : "memory", "m0");
+  }
+  static constexpr bool kUntrackedDma = true;  // the caller waits for vmcnt(0) before reading the tile
+};
+
+template <int NKT, int CH, int NWAVES, bool SWZ, class Src = BufRows>
 struct RowGather {
   static constexpr int PITCH = SWZ ? CH : CH + 1;
   static constexpr int RPW = NKT / NWAVES;       // rows per wave
@@ -119,17 +162,17 @@ struct RowGather {
   static_assert(NKT % NWAVES == 0, "rows split evenly over the waves");
   static_assert(!SWZ || (PITCH % 8 == 0 && CH % 8 == 0), "swizzled rows are whole groups of 8 chunks");
 
-  uint32_t base[RPW];
+  typename Src::base_t base[RPW];
 
   // ib: the tile's NKT staged row ids (-1 = padding row); wave-uniform reads.
   // valid == false makes every row a padding row (the instructions then move
   // no global data and write zeros); ib must still point into the array.
   // (No pointer select: the compiler keeps ib's array identity, so the read
   // does not wait for DMA into other LDS arrays.)
-  __device__ __forceinline__ void load_ids(const int* ib, bool valid, int wave, uint32_t row_bytes) {
+  __device__ __forceinline__ void load_ids(const int* ib, bool valid, int wave, const Src& src) {
     int raw[RPW];
     fetch(ib, wave, raw);
-    set(raw, valid, row_bytes);
+    set(raw, valid, src);
   }
   // load_ids in two halves, so a caller can issue the LDS reads early and
   // turn them into offsets once they have landed.
@@ -137,33 +180,35 @@ struct RowGather {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) raw[r] = ib[wave * RPW + r];
   }
-  __device__ __forceinline__ void set_row(int r, int raw, bool valid, uint32_t row_bytes) {
+  __device__ __forceinline__ void set_row(int r, int raw, bool valid, const Src& src) {
     const int id = __builtin_amdgcn_readfirstlane(raw);
-    base[r] = (valid && id >= 0) ? __umul24((uint32_t)id, row_bytes) : kOOBRow;
+    base[r] = src.row_base(id, valid);
   }
-  __device__ __forceinline__ void set(const int (&raw)[RPW], bool valid, uint32_t row_bytes) {
+  __device__ __forceinline__ void set(const int (&raw)[RPW], bool valid, const Src& src) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) set_row(r, raw[r], valid, row_bytes);
+    for (int r = 0; r < RPW; ++r) set_row(r, raw[r], valid, src);
   }
 
-  __device__ __forceinline__ void issue(int k, const __amdgpu_buffer_rsrc_t& rs, u32x4* dst, int wave,
-                                        int lane) const {
+  // (lanes past the first row's end read chunk c0 + lane' - PITCH of the
+  // next row, lane' = lane or lane ^ swz; lane' >= bnd, so that offset is
+  // non-negative)
+  __device__ __forceinline__ void issue(int k, const Src& src, u32x4* dst, int wave, int lane) const {
     const int s0 = 64 * k;
     const int r0 = s0 / PITCH, c0 = s0 % PITCH;
     const int bnd = PITCH - c0;
     const uint32_t l16 = 16u * (uint32_t)lane;
     const uint32_t x0 = SWZ ? l16 ^ (16u * (uint32_t)tile_swz(wave * RPW + r0)) : l16;
-    uint32_t off = base[r0] + 16u * (uint32_t)c0 + x0;
+    typename Src::base_t a = base[r0] + (16u * (uint32_t)c0 + x0);
     if (bnd < 64 && r0 + 1 < RPW) {
       const uint32_t x1 = SWZ ? l16 ^ (16u * (uint32_t)tile_swz(wave * RPW + r0 + 1)) : l16;
-      const uint32_t o1 = base[r0 + 1] + 16u * (uint32_t)c0 - 16u * (uint32_t)PITCH + x1;
-      off = lane < bnd ? off : o1;
+      const typename Src::base_t a1 = base[r0 + 1] + (16u * (uint32_t)c0 + x1 - 16u * (uint32_t)PITCH);
+      a = lane < bnd ? a : a1;
     }
     u32x4* d = dst + wave * SPW + s0;
     if (s0 + 64 <= SPW) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)d, 16, off, 0, 0, 0);
+      src.load_lds16(d, a);
     } else if (lane < SPW - s0) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)d, 16, off, 0, 0, 0);
+      src.load_lds16(d, a);
     }
   }
 };

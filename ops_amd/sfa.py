@@ -34,7 +34,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward",
+__all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward", "sfa_forward_paged",
            "SparseFlashAttentionSBHD", "SparseFlashAttentionTriton"]
 
 _DTYPES = {torch.float32: _lib.SFA_DTYPE_F32, torch.bfloat16: _lib.SFA_DTYPE_BF16}
@@ -103,8 +103,9 @@ def _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits) -> _lib.
     return a
 
 
-def _prep(q, k, v, topk_idxs, kv_lens, sink):
-    _validate(q, k, v, topk_idxs, kv_lens, sink)
+def _prep(q, k, v, topk_idxs, kv_lens, sink, validate=True):
+    if validate:
+        _validate(q, k, v, topk_idxs, kv_lens, sink)
     q, k, v = _rows(q), _rows(k), _rows(v)
     idx = topk_idxs
     if idx.dtype != torch.int32:
@@ -136,6 +137,69 @@ def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None,
     wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
     stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.sfa_fwd(ctypes.byref(a), _ptr(wbuf), ws, ctypes.c_void_p(stream)))
+    return out, lse
+
+
+def sfa_forward_paged(q, k_cache, v_cache, block_table, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None,
+                      num_splits: int = 0, out: Optional[torch.Tensor] = None,
+                      lse: Optional[torch.Tensor] = None):
+    """Forward over a paged KV cache (no autograd): ``(out, lse)``.
+
+    ``k_cache`` ``[num_pages, page_size, Hkv, Dqk]`` and ``v_cache``
+    ``[num_pages, page_size, Hkv, Dv]`` are page pools (``v_cache`` may be a
+    view of ``k_cache``, e.g. MLA's ``k_cache[..., :512]``); ``block_table``
+    ``[B, max_pages]`` int32 maps page ``i // page_size`` of sequence ``b`` to
+    a pool page; ``topk_idxs`` ``[B, Sq, Hkv, K]`` hold *logical* key
+    positions, valid iff ``0 <= idx < kv_lens[b]`` (or
+    ``max_pages * page_size``) and mapped to a page in ``[0, num_pages)``.
+    The result equals :func:`sfa_forward` on the contiguous cache the block
+    table describes.  ``page_size`` must be a power of two.
+    """
+    lib = _lib.load()
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("k_cache / v_cache must be [num_pages, page_size, Hkv, D]")
+    if block_table.dim() != 2 or block_table.shape[0] != q.shape[0]:
+        raise ValueError(f"block_table must be [B, max_pages] with B = {q.shape[0]}")
+    if block_table.device != q.device:
+        raise ValueError("block_table must be on q's device")
+    num_pages, page_size, Hkv, _ = k_cache.shape
+    if tuple(v_cache.shape[:3]) != (num_pages, page_size, Hkv):
+        raise ValueError(f"v_cache shape {tuple(v_cache.shape)} does not match k_cache {tuple(k_cache.shape)}")
+    if page_size <= 0 or page_size & (page_size - 1):
+        raise ValueError(f"page_size must be a power of two, got {page_size}")
+    max_pages = block_table.shape[1]
+    B = q.shape[0]
+    skv = max_pages * page_size
+    # stand-ins of the logical [B, Skv, Hkv, D] caches for the shared
+    # validation (zero-stride; the library gets the pools' strides)
+    kview = k_cache.new_empty(()).expand(B, skv, Hkv, k_cache.shape[3])
+    vview = v_cache.new_empty(()).expand(B, skv, Hkv, v_cache.shape[3])
+    _validate(q, kview, vview, topk_idxs, kv_lens, attn_sink)
+    q, k_cache, v_cache, idx, kv_lens, sink = _prep(q, k_cache.unsqueeze(0), v_cache.unsqueeze(0), topk_idxs,
+                                                    kv_lens, attn_sink, validate=False)
+    k_cache, v_cache = k_cache.squeeze(0), v_cache.squeeze(0)
+    bt = block_table.to(torch.int32)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    B, Sq, Hq, Dqk = q.shape
+    Dv = v_cache.shape[3]
+    scale = (1.0 / math.sqrt(Dqk)) if sm_scale is None else float(sm_scale)
+    if out is None:
+        out = torch.empty((B, Sq, Hq, Dv), dtype=q.dtype, device=q.device)
+    if lse is None:
+        lse = torch.empty((B, Sq, Hq), dtype=torch.float32, device=q.device)
+    a = _fwd_args(q, kview, vview, idx, out, lse, scale, kv_lens, sink, num_splits)
+    # pools: page, row and head strides
+    a.k, (a.k_sb, a.k_ss, a.k_sh) = k_cache.data_ptr(), k_cache.stride()[:3]
+    a.v, (a.v_sb, a.v_ss, a.v_sh) = v_cache.data_ptr(), v_cache.stride()[:3]
+    pg = _lib.KvPages()
+    pg.block_table = bt.data_ptr()
+    pg.bt_sb = bt.stride(0)
+    pg.max_pages, pg.page_size, pg.num_pages, pg.flags = max_pages, page_size, num_pages, 0
+    ws = lib.sfa_fwd_paged_workspace_size(ctypes.byref(a), ctypes.byref(pg))
+    wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.sfa_fwd_paged(ctypes.byref(a), ctypes.byref(pg), _ptr(wbuf), ws, ctypes.c_void_p(stream)))
     return out, lse
 
 

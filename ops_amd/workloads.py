@@ -329,3 +329,39 @@ def make_workload(name: str, device="cpu", seed: int = 0, with_dout: Optional[bo
     dout = _randn(tuple(q.shape[:3]) + (Dv,), dt, device, _gen(device, seed, 6)) if bwd else None
     return Workload(name=name, q=q, k=k, v=v, idx=idx.contiguous(), scale=scale, kv_lens=kv_lens,
                     dout=dout, meta=meta)
+
+
+def page_kv(k: torch.Tensor, v: torch.Tensor, page_size: int, seed: int = 0, spare_pages: int = 0):
+    """Paged copy of a contiguous cache for the paged-KV forward.
+
+    ``k`` ``[B, Skv, Hkv, Dqk]`` / ``v`` ``[B, Skv, Hkv, Dv]`` (``v`` may be a
+    prefix view of ``k``, as in MLA) are cut into pages of ``page_size`` rows
+    that are scattered over a pool in a seeded random order, with
+    ``spare_pages`` extra pages of noise.  Returns ``(k_pool, v_pool,
+    block_table)``: pools ``[num_pages, page_size, Hkv, D]`` (``v_pool`` a
+    prefix view of ``k_pool`` when ``v`` is one of ``k``) and the
+    ``[B, Skv / page_size]`` int32 block table that maps them back.
+    """
+    B, Skv, Hkv, Dqk = k.shape
+    if Skv % page_size:
+        raise ValueError("Skv must be a multiple of page_size")
+    npb = Skv // page_size
+    n = B * npb + spare_pages
+    g = _gen(k.device, seed, 7)
+    perm = torch.randperm(n, generator=g, device=k.device)       # pool slot -> logical page (>= B*npb: spare)
+    where = torch.empty_like(perm)
+    where[perm] = torch.arange(n, device=k.device)               # logical page -> pool slot
+    block_table = where[:B * npb].view(B, npb).to(torch.int32).contiguous()
+
+    def pool_of(x):
+        pages = x.reshape(B * npb, page_size, Hkv, x.shape[3])
+        if spare_pages:
+            noise = _randn((spare_pages, page_size, Hkv, x.shape[3]), x.dtype, x.device, _gen(x.device, seed, 8))
+            pages = torch.cat([pages, noise])
+        return pages[perm].contiguous()
+
+    shares_storage = v.data_ptr() == k.data_ptr() and v.stride() == k.stride()
+    k_pool = pool_of(k)
+    v_pool = k_pool[..., :v.shape[3]] if shares_storage else pool_of(v)
+    return k_pool, v_pool, block_table
+

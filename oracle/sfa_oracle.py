@@ -32,6 +32,13 @@ Generalisations relative to the reference (the drop-in boundary's API):
   in base 2, SFA.py:474; ``lse = lse2 · ln 2``).  A row with no valid slot gives
   ``O = 0`` and ``LSE = -inf`` (the reference's sentinel is ≈ −1e11, SFA.py:381).
 * The attention sink is optional (``sink=None`` ≡ sink = −∞).
+* Paged KV caches (``paged_to_contiguous``): not in the reference, whose
+  ``_attn_fwd`` reads one contiguous kv tensor (SFA.py:483-587).  The serving
+  layout is restated as a plain mapping back to the contiguous cache: logical
+  key ``i`` of sequence ``b`` is row ``i % page_size`` of pool page
+  ``block_table[b, i // page_size]``; a slot whose page id lies outside
+  ``[0, num_pages)`` is invalid.  The forward over a paged cache is then
+  ``sfa_forward`` of the mapped cache and indices.
 
 Duplicated indices are counted once per slot, as in the reference, which
 processes every slot independently (SFA.py:386-467).
@@ -63,6 +70,7 @@ __all__ = [
     "sfa_forward_autograd",
     "valid_mask",
     "count_valid_pairs",
+    "paged_to_contiguous",
 ]
 
 
@@ -257,3 +265,35 @@ def sfa_forward_autograd(q, k, v, idx, scale=None, kv_lens=None, sink=None):
         outs.append(torch.cat(ob, dim=1))
         lses.append(torch.cat(lb, dim=1))
     return torch.stack(outs), torch.stack(lses)
+
+
+def paged_to_contiguous(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
+                        idx: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Contiguous ``(k, v, idx)`` equivalent to a paged cache.
+
+    ``k_cache`` / ``v_cache``: ``[num_pages, page_size, Hkv, D]`` pools;
+    ``block_table``: ``[B, max_pages]`` pool page of each logical page;
+    ``idx``: ``[B, Sq, Hkv, K]`` logical key positions.  Returns
+    ``k``/``v`` ``[B, max_pages * page_size, Hkv, D]`` (rows of unmapped pages
+    are zero) and ``idx`` with every slot whose page is unmapped set to -1
+    (other slots unchanged, so the range / ``kv_lens`` rules still apply).
+    """
+    num_pages, page_size = k_cache.shape[:2]
+    B, max_pages = block_table.shape
+    bt = block_table.long()
+    mapped = (bt >= 0) & (bt < num_pages)                       # [B, max_pages]
+    safe = torch.where(mapped, bt, torch.zeros_like(bt))
+
+    def gather(cache):
+        rows = cache[safe.reshape(-1)]                           # [B*max_pages, page, Hkv, D]
+        rows = rows * mapped.reshape(-1, 1, 1, 1).to(rows.dtype)
+        return rows.reshape(B, max_pages * page_size, *cache.shape[2:])
+
+    il = idx.long()
+    page = torch.div(il, page_size, rounding_mode="floor")
+    in_table = (il >= 0) & (page < max_pages)
+    pmapped = torch.gather(mapped, 1, torch.where(in_table, page, torch.zeros_like(page)).reshape(B, -1))
+    pmapped = pmapped.reshape(idx.shape) & in_table
+    idx_out = torch.where(pmapped | (il < 0) | ~in_table, idx, torch.full_like(idx, -1))
+    return gather(k_cache), gather(v_cache), idx_out
+

@@ -39,10 +39,12 @@ def test_struct_layout_matches_header(tmp_path):
     src = tmp_path / "layout.c"
     fields_f = [f for f, _ in _lib.FwdArgs._fields_]
     fields_b = [f for f, _ in _lib.BwdArgs._fields_]
+    fields_p = [f for f, _ in _lib.KvPages._fields_]
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
-             'printf("%zu %zu\\n", sizeof(sfa_fwd_args), sizeof(sfa_bwd_args));']
+             'printf("%zu %zu %zu\\n", sizeof(sfa_fwd_args), sizeof(sfa_bwd_args), sizeof(sfa_kv_pages));']
     lines += [f'printf("%zu\\n", offsetof(sfa_fwd_args, {f}));' for f in fields_f]
     lines += [f'printf("%zu\\n", offsetof(sfa_bwd_args, {f}));' for f in fields_b]
+    lines += [f'printf("%zu\\n", offsetof(sfa_kv_pages, {f}));' for f in fields_p]
     lines += ["return 0; }"]
     src.write_text("\n".join(lines))
     exe = tmp_path / "layout"
@@ -50,8 +52,10 @@ def test_struct_layout_matches_header(tmp_path):
     vals = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
     assert int(vals[0]) == ctypes.sizeof(_lib.FwdArgs)
     assert int(vals[1]) == ctypes.sizeof(_lib.BwdArgs)
-    offs = [int(x) for x in vals[2:]]
-    py = [getattr(_lib.FwdArgs, f).offset for f in fields_f] + [getattr(_lib.BwdArgs, f).offset for f in fields_b]
+    assert int(vals[2]) == ctypes.sizeof(_lib.KvPages)
+    offs = [int(x) for x in vals[3:]]
+    py = ([getattr(_lib.FwdArgs, f).offset for f in fields_f] + [getattr(_lib.BwdArgs, f).offset for f in fields_b]
+          + [getattr(_lib.KvPages, f).offset for f in fields_p])
     assert offs == py
 
 
@@ -119,3 +123,44 @@ def test_bwd_rejects_missing_gradients_and_csr_mode():
     assert lib.sfa_bwd(ctypes.byref(b), None, 0, None) == _lib.SFA_E_INVALID
     b.dkv_mode = _lib.SFA_DKV_ATOMIC
     assert lib.sfa_bwd(ctypes.byref(b), None, 0, None) == _lib.SFA_E_WORKSPACE
+
+
+def _valid_pages():
+    pg = _lib.KvPages()
+    pg.block_table = 0x10000
+    pg.bt_sb, pg.max_pages, pg.page_size, pg.num_pages = 2, 2, 4, 4
+    return pg
+
+
+@pytest.mark.parametrize("field,value", [
+    ("block_table", None), ("page_size", 3), ("page_size", 0), ("max_pages", 0), ("num_pages", 0),
+    ("num_pages", 1 << 30), ("flags", 1), ("max_pages", 1),
+])
+def test_paged_arguments_are_rejected(field, value):
+    lib = _lib.load()
+    a = _valid_args()                  # Skv = 8 = max_pages * page_size
+    pg = _valid_pages()
+    setattr(pg, field, value)
+    rc = lib.sfa_fwd_paged(ctypes.byref(a), ctypes.byref(pg), None, 0, None)
+    assert rc == _lib.SFA_E_INVALID, field
+    assert lib.sfa_last_error()
+    assert lib.sfa_fwd_paged_workspace_size(ctypes.byref(a), ctypes.byref(pg)) == 0
+    assert lib.sfa_fwd_paged(ctypes.byref(a), None, None, 0, None) == _lib.SFA_E_INVALID
+
+
+def test_paged_workspace_matches_contiguous_plan():
+    lib = _lib.load()
+    a = _valid_args()
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = 64, 1, 65536, 128, 1, 576, 512, 2048
+    a.k_ss = a.v_ss = a.k_sh = a.v_sh = 576
+    a.k_sb = a.v_sb = 64 * 576          # page stride of a 64-row page pool
+    a.q_sh, a.q_ss, a.q_sb = 576, 128 * 576, 128 * 576
+    a.o_sh, a.o_ss, a.o_sb = 512, 128 * 512, 128 * 512
+    a.v = a.k
+    pg = _valid_pages()
+    pg.max_pages, pg.page_size, pg.num_pages, pg.bt_sb = 1024, 64, 65536, 1024
+    ws = lib.sfa_fwd_paged_workspace_size(ctypes.byref(a), ctypes.byref(pg))
+    assert ws > 0
+    a.k_sb = a.v_sb = 65536 * 576
+    assert ws == lib.sfa_fwd_workspace_size(ctypes.byref(a))
+
