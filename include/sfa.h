@@ -118,6 +118,30 @@ typedef struct sfa_kv_pages {
   int32_t flags;                 /* reserved, must be 0                               */
 } sfa_kv_pages;
 
+/* Top-k index producer (sfa_indexer_topk): creates the index rows sfa_fwd
+ * consumes.  The reference takes them as an input (`topk_idxs`, "Sparse
+ * indices mapping queries to KV blocks", SFA.py:88-90); the scores are those
+ * of DeepSeek-V3.2's lightning indexer:
+ *   I[b,t,s] = sum_h w[b,t,h] * max(0, <q[b,t,h,:], k[b,s,:]>)
+ * Query t of sequence b may see keys s <= t + L_b - Sq (L_b = kv_lens[b]
+ * clamped to Skv, else Skv): causal prefill when Sq = L_b, the whole context
+ * for a single decode query.  Row idx[b,t,:] receives the min(topk, allowed)
+ * allowed keys with the largest scores (equal scores: the lower key first),
+ * in ascending key order, then -1 padding.
+ * Supported: bf16 q / k, D = 128, H in {32, 64, 128}, Skv <= 65536. */
+typedef struct sfa_indexer_args {
+  int32_t B, Sq, Skv, H, D, topk;
+  const void* q;   int64_t q_sb, q_ss, q_sh;      /* [B, Sq, H, D] bf16, unit feature stride  */
+  const void* k;   int64_t k_sb, k_ss;            /* [B, Skv, D] bf16, unit feature stride    */
+  const float* w;  int64_t w_sb, w_ss;            /* [B, Sq, H] float32, unit head stride     */
+  const int32_t* kv_lens;                         /* [B] or NULL                              */
+  int32_t* idx;    int64_t i_sb, i_ss;            /* [B, Sq, topk] int32 out, unit slot stride */
+  float* logits;   int64_t g_sb, g_ss;            /* optional [B, Sq, Skv] float32 out (scores
+                                                     of allowed keys; other entries unspecified;
+                                                     16-byte aligned rows, g_ss % 4 == 0), or NULL */
+  int32_t flags;                                  /* reserved, must be 0                       */
+} sfa_indexer_args;
+
 /* Library ABI version (SFA_ABI_VERSION of the build). */
 SFA_API int sfa_abi_version(void);
 
@@ -142,6 +166,14 @@ SFA_API size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_
  * this is the serving-side layout of the decode step that precedes it. */
 SFA_API int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace sfa_indexer_topk needs (the scores of a chunk of
+ * queries; 0 when `logits` is given). */
+SFA_API size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a);
+
+/* Scores and top-k selection (no counterpart kernel in the reference, which
+ * consumes the result: SFA.py:88-90). */
+SFA_API int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace sfa_bwd needs for `a` (fp32 dK/dV accumulators,
  * delta, and the CSR arrays in SFA_DKV_CSR mode).

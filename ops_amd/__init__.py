@@ -8,11 +8,15 @@ Public API (BSHD, see ``ops_amd.sfa``)::
 Paged KV cache (serving): ``ops_amd.sfa_forward_paged(q, k_cache, v_cache,
 block_table, topk_idxs, ...)``.
 
+Top-k index producer (scores + selection that create ``topk_idxs``):
+``ops_amd.indexer_topk(q_idx, k_idx, weights, topk, kv_lens=None)``.
+
 The HIP kernels live in ``libsfa.so`` (``python -m ops_amd.build``), reached
 through the C ABI declared in ``include/sfa.h``.
 """
+from .indexer import indexer_topk
 from .sfa import (SparseFlashAttention, SparseFlashAttentionSBHD, SparseFlashAttentionTriton, sfa_backward,
                   sfa_forward, sfa_forward_paged, sparse_flash_attention)
 
 __all__ = ["SparseFlashAttention", "sparse_flash_attention", "sfa_forward", "sfa_backward", "sfa_forward_paged",
-           "SparseFlashAttentionSBHD", "SparseFlashAttentionTriton"]
+           "SparseFlashAttentionSBHD", "SparseFlashAttentionTriton", "indexer_topk"]

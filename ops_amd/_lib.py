@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "sfa_bwd",
     "sfa_fwd_paged_workspace_size",
     "sfa_fwd_paged",
+    "sfa_indexer_topk_workspace_size",
+    "sfa_indexer_topk",
 )
 
 _i32 = ctypes.c_int32
@@ -85,6 +87,20 @@ class KvPages(ctypes.Structure):
     ]
 
 
+class IndexerArgs(ctypes.Structure):
+    """Mirror of ``sfa_indexer_args``."""
+    _fields_ = [
+        ("B", _i32), ("Sq", _i32), ("Skv", _i32), ("H", _i32), ("D", _i32), ("topk", _i32),
+        ("q", _vp), ("q_sb", _i64), ("q_ss", _i64), ("q_sh", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_ss", _i64),
+        ("w", _vp), ("w_sb", _i64), ("w_ss", _i64),
+        ("kv_lens", _vp),
+        ("idx", _vp), ("i_sb", _i64), ("i_ss", _i64),
+        ("logits", _vp), ("g_sb", _i64), ("g_ss", _i64),
+        ("flags", _i32),
+    ]
+
+
 class SFAError(RuntimeError):
     """A failure reported by libsfa (HIP runtime or unsupported request)."""
 
@@ -123,6 +139,10 @@ def load() -> ctypes.CDLL:
         lib.sfa_fwd_paged_workspace_size.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(KvPages)]
         lib.sfa_fwd_paged.restype = ctypes.c_int
         lib.sfa_fwd_paged.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(KvPages), _vp, ctypes.c_size_t, _vp]
+        lib.sfa_indexer_topk_workspace_size.restype = ctypes.c_size_t
+        lib.sfa_indexer_topk_workspace_size.argtypes = [ctypes.POINTER(IndexerArgs)]
+        lib.sfa_indexer_topk.restype = ctypes.c_int
+        lib.sfa_indexer_topk.argtypes = [ctypes.POINTER(IndexerArgs), _vp, ctypes.c_size_t, _vp]
         ver = lib.sfa_abi_version()
         if ver != SFA_ABI_VERSION:
             raise SFAError(f"libsfa ABI version {ver} != expected {SFA_ABI_VERSION}; rebuild")

@@ -340,3 +340,102 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
 }
 
 }  // extern "C"
+
+namespace {
+
+// Scores are produced and consumed a chunk of queries at a time, so the
+// workspace stays bounded (about 512 MiB) whatever Sq and Skv are.
+constexpr size_t kIndexerChunkBytes = size_t(512) << 20;
+constexpr int kIndexerMaxSkv = 65536;
+
+int check_indexer(const sfa_indexer_args* a) {
+  if (a == nullptr) return fail(SFA_E_INVALID, "null argument struct");
+  if (a->B <= 0 || a->Sq <= 0 || a->Skv <= 0 || a->H <= 0 || a->D <= 0)
+    return fail(SFA_E_INVALID, "B, Sq, Skv, H, D must be positive");
+  if (a->topk <= 0) return fail(SFA_E_INVALID, "topk must be positive (got %d)", a->topk);
+  if (!a->q || !a->k || !a->w || !a->idx) return fail(SFA_E_INVALID, "null tensor pointer");
+  if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if (a->D != 128 || (a->H != 32 && a->H != 64 && a->H != 128))
+    return fail(SFA_E_UNSUPPORTED, "the indexer supports D = 128 and H in {32, 64, 128} (got D = %d, H = %d)", a->D,
+                a->H);
+  if (a->Skv > kIndexerMaxSkv) return fail(SFA_E_UNSUPPORTED, "the indexer supports Skv <= %d", kIndexerMaxSkv);
+  if (!aligned16(a->q) || !aligned16(a->k)) return fail(SFA_E_INVALID, "q and k rows must be 16-byte aligned");
+  const int64_t st[] = {a->q_sb, a->q_ss, a->q_sh, a->k_sb, a->k_ss};
+  for (int64_t x : st)
+    if (x % 8 != 0) return fail(SFA_E_INVALID, "q / k strides must be multiples of 8 elements");
+  if (2 * ((int64_t)(a->Skv - 1) * a->k_ss + a->D) >= (int64_t)0x80000000LL)
+    return fail(SFA_E_UNSUPPORTED, "k rows of one sequence must lie within 2 GiB");
+  if (a->logits) {
+    if (!aligned16(a->logits) || a->g_ss % 4 != 0 || a->g_sb % 4 != 0 || a->g_ss < a->Skv)
+      return fail(SFA_E_INVALID, "logits rows must be 16-byte aligned with a row stride >= Skv, multiple of 4");
+  }
+  return SFA_OK;
+}
+
+sfa::IndexerParams to_iparams(const sfa_indexer_args* a) {
+  sfa::IndexerParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.k = a->k; p.w = a->w; p.kv_lens = a->kv_lens; p.idx = a->idx; p.logits = a->logits;
+  p.q_sb = a->q_sb; p.q_ss = a->q_ss; p.q_sh = a->q_sh;
+  p.k_sb = a->k_sb; p.k_ss = a->k_ss;
+  p.w_sb = a->w_sb; p.w_ss = a->w_ss;
+  p.i_sb = a->i_sb; p.i_ss = a->i_ss;
+  p.g_sb = a->g_sb; p.g_ss = a->g_ss;
+  p.B = a->B; p.Sq = a->Sq; p.Skv = a->Skv; p.H = a->H; p.D = a->D; p.topk = a->topk;
+  return p;
+}
+
+// Queries per chunk (a multiple of the logits kernel's query block) and the
+// score row stride of the workspace.
+void indexer_chunk(const sfa_indexer_args* a, int* rows, int64_t* ld) {
+  const sfa::IndexerParams p = to_iparams(a);
+  const int qb = sfa::indexer_query_block(p);
+  *ld = (int64_t)(a->Skv + 31) / 32 * 32;
+  int64_t r = (int64_t)(kIndexerChunkBytes / ((size_t)a->B * (size_t)*ld * sizeof(float)));
+  r = r / qb * qb;
+  if (r < qb) r = qb;
+  const int64_t all = (int64_t)(a->Sq + qb - 1) / qb * qb;
+  *rows = (int)(r < all ? r : all);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a) {
+  if (check_indexer(a) != SFA_OK || a->logits) return 0;
+  int rows;
+  int64_t ld;
+  indexer_chunk(a, &rows, &ld);
+  return align_up((size_t)a->B * (size_t)rows * (size_t)ld * sizeof(float), 256);
+}
+
+int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  const int rc = check_indexer(a);
+  if (rc != SFA_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  sfa::IndexerParams p = to_iparams(a);
+  int rows = a->Sq;
+  if (a->logits == nullptr) {
+    const size_t need = sfa_indexer_topk_workspace_size(a);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(SFA_E_WORKSPACE, "sfa_indexer_topk needs %zu workspace bytes (got %zu)", need, workspace_bytes);
+    int64_t ld;
+    indexer_chunk(a, &rows, &ld);
+    p.logits = (float*)workspace;
+    p.g_ss = ld;
+    p.g_sb = (int64_t)rows * ld;
+  }
+  for (int t0 = 0; t0 < a->Sq; t0 += rows) {
+    const int t1 = t0 + rows < a->Sq ? t0 + rows : a->Sq;
+    p.g_t0 = a->logits ? 0 : t0;
+    hipError_t e = sfa::launch_indexer_logits(p, t0, t1, s);
+    if (e == hipSuccess) e = sfa::launch_topk_select(p, t0, t1, s);
+    if (e != hipSuccess) return hip_fail(e, "sfa_indexer_topk");
+  }
+  return SFA_OK;
+}
+
+}  // extern "C"
+

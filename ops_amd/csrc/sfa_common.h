@@ -137,6 +137,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads 0
 
+// Top-k index producer (sfa_indexer.hip): indexer scores + top-k selection.
+struct IndexerParams {
+  const void* q;          // [B, Sq, H, D] bf16
+  const void* k;          // [B, Skv, D] bf16
+  const float* w;         // [B, Sq, H] float32, head stride 1
+  const int32_t* kv_lens; // [B] or nullptr
+  int32_t* idx;           // [B, Sq, topk] int32 out, slot stride 1
+  float* logits;          // rows [g_t0, ...) of the scores: [B, rows, Skv], row stride g_ss
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss;
+  int64_t w_sb, w_ss;
+  int64_t i_sb, i_ss;
+  int64_t g_sb, g_ss;
+  int g_t0;               // query of logits row 0 (the workspace holds a chunk of queries)
+  int B, Sq, Skv, H, D, topk;
+};
+
 }  // namespace sfa
 
 // Launchers implemented in the .hip translation units; return a HIP error.
@@ -168,4 +185,8 @@ size_t csr_workspace_bytes(const Params& p);  // after csr_geometry
 void csr_bind_workspace(Params& p, void* ws); // carves kmap / dup / blist / bcount / dkv_part
 hipError_t launch_csr_index(const Params& p, hipStream_t s);  // bitmap, duplicate flags, block lists
 hipError_t launch_csr_dkv(const Params& p, hipStream_t s);    // key-major dK/dV partials + reduction
+// top-k index producer: queries [t_begin, t_end) of every sequence
+int indexer_query_block(const IndexerParams& p);
+hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s);
+hipError_t launch_topk_select(const IndexerParams& p, int t_begin, int t_end, hipStream_t s);
 }  // namespace sfa

@@ -1,0 +1,360 @@
+// gfx950 top-k index producer: the step that creates the index rows the
+// sparse attention consumes (`topk_idxs`, "Sparse indices mapping queries to
+// KV blocks", SFA.py:88-90).  The reference takes them as an input; the
+// scores follow DeepSeek-V3.2's lightning indexer:
+//
+//   I[b,t,s] = sum_h w[b,t,h] * max(0, <q[b,t,h,:], k[b,s,:]>)
+//
+// over the keys s a query may see (s <= t + L_b - Sq, L_b = kv_lens[b] or
+// Skv), then the top-k keys of every query row.
+//
+// Two kernels:
+//  * indexer_logits_kernel<H>: bf16 MFMA (32x32x16), heads as MFMA rows and
+//    keys as columns.  A wave keeps 4 M-tiles of q in VGPRs (128 / H queries
+//    x H heads, d = 128), the workgroup's 4 waves share each 32-key tile of k,
+//    DMA'd into a double-buffered LDS tile (row pitch 17 slots: the b128
+//    operand reads are bank-conflict free); the head weights sit in LDS, so
+//    two workgroups fit a CU and one's MFMAs cover the other's epilogue and
+//    tile wait.  The epilogue applies the weights
+//    and the ReLU to the fp32 accumulators and sums over the heads in
+//    registers (16 rows per lane, then the lane pair l, l ^ 32), so one
+//    coalesced 128-byte store per query writes 32 scores.
+//  * topk_select_kernel: one 1024-thread workgroup per query row, the row's
+//    scores spread over the threads in contiguous runs of 4, 8, 16, 32 or 64
+//    (the smallest that holds the row; one instantiation each) in VGPRs as
+//    order-preserving u32 keys.  The k-th largest key
+//    is found exactly by bisection over its 32 bits (per step: one compare per
+//    score and one block sum; no histogram atomics), then the selected keys are
+//    written in ascending key order: all keys above the threshold, and the
+//    lowest-index keys equal to it until k are chosen (two block scans).
+
+#include "sfa_common.h"
+#include "sfa_lds.h"
+#include "sfa_mfma.h"
+
+namespace sfa {
+
+namespace {
+
+constexpr int kD = 128;          // index head dim
+constexpr int kKT = 32;          // keys per tile
+constexpr int kPitch = 17;       // LDS row pitch of a key tile in 16-byte slots (16 + 1 pad)
+constexpr int kTileSlots = kKT * kPitch;
+constexpr int kLogitThreads = 256;
+constexpr int kSelThreads = 1024;
+constexpr int kSelEpt = 64;      // scores per thread in the selection kernel
+constexpr int kSelCap = kSelThreads * kSelEpt;  // longest score row (the API admits Skv <= 65536)
+static_assert(kSelCap == 65536, "selection capacity");
+
+// Keys query t of sequence b may see: [0, end).
+__device__ __forceinline__ int key_end(const IndexerParams& p, int b, int t) {
+  int L = p.Skv;
+  if (p.kv_lens) L = min(p.kv_lens[b], p.Skv);
+  int e = t + 1 + L - p.Sq;
+  e = min(e, L);
+  return max(e, 0);
+}
+
+template <int H>
+__global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(IndexerParams p, int t_begin, int t_end) {
+  constexpr int QPW = 128 / H;        // queries per wave
+  constexpr int HT = H / 32;          // M-tiles (32 heads) per query
+  constexpr int QB = 4 * QPW;         // queries per workgroup
+  static_assert(QPW * HT == 4, "four M-tiles per wave");
+  using M = Mfma<32>;
+  typedef typename M::acc_t acc_t;
+
+  // two distinct arrays (not one indexed by parity): the compiler then knows
+  // the DMA into one does not feed the operand reads of the other
+  __shared__ u32x4 s_k0[kTileSlots];
+  __shared__ u32x4 s_k1[kTileSlots];
+  // head weights of the workgroup's queries: wave w, M-tile mt, at
+  // [(w * 4 + mt) * 32 + head within the tile]
+  __shared__ float s_w[4 * 4 * 32];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nqb = (t_end - t_begin + QB - 1) / QB;
+  // heaviest (latest) query blocks first
+  const int b = blockIdx.x / nqb;
+  const int qb = nqb - 1 - (int)(blockIdx.x % nqb);
+  const int tq0 = t_begin + qb * QB;  // first query of the workgroup
+
+  // key tiles the workgroup needs: up to the largest end among its queries
+  const int t_last = min(tq0 + QB, t_end) - 1;
+  const int kend_wg = key_end(p, b, t_last);
+  const int ntiles = (kend_wg + kKT - 1) / kKT;
+
+  // ---- q operands (A: lane l holds head 32 hg + l % 32, dims 16 s + 8 (l / 32) ..) and weights
+  const int hl = lane & 31, lg = lane >> 5;
+  bf16x8 qa[4][8];
+  int tq[QPW];
+  bool qok[QPW];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    tq[i] = tq0 + wave * QPW + i;
+    qok[i] = tq[i] < t_end;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int i = mt / HT, hg = mt % HT;
+    const int t = qok[i] ? tq[i] : t_begin;
+    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)(hg * 32 + hl) * p.q_sh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qa[mt][s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * lg);
+    const float* wrow = p.w + b * p.w_sb + t * p.w_ss + hg * 32;
+    if (lg == 0) s_w[(wave * 4 + mt) * 32 + hl] = wrow[hl];
+  }
+  // weight of accumulator element e of M-tile mt: head 8 (e / 4) + 4 lg + e % 4
+  // of the tile, read as 4 consecutive floats per group of 4 elements
+  auto wq = [&](int mt, int g4) -> f32x4 {
+    return *reinterpret_cast<const f32x4*>(&s_w[(wave * 4 + mt) * 32 + 8 * g4 + 4 * lg]);
+  };
+
+  // ---- key tile DMA: slot u = 17 r + c holds chunk c of key row r (c = 16: pad)
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb);
+  const uint32_t krow = (uint32_t)(2 * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + kD)));
+  auto load_tile = [&](int kt, u32x4* dst) {
+#pragma unroll
+    for (int it = 0; it < (kTileSlots + kLogitThreads - 1) / kLogitThreads; ++it) {
+      const int u = it * kLogitThreads + tid;
+      if (u < kTileSlots) {
+        const int r = u / kPitch, c = u - r * kPitch;
+        const int key = kt * kKT + r;
+        const uint32_t off = (c < 16 && key < kend_wg) ? __umul24((uint32_t)key, krow) + 16u * (uint32_t)c : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(dst + it * kLogitThreads + wave * 64), 16, off, 0, 0,
+                                                 0);
+      }
+    }
+  };
+
+  // per-query row of the logits buffer and its end
+  float* orow[QPW];
+  int qend[QPW];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    orow[i] = p.logits + b * p.g_sb + (int64_t)(qok[i] ? tq[i] - p.g_t0 : 0) * p.g_ss;
+    qend[i] = qok[i] ? key_end(p, b, tq[i]) : 0;
+  }
+
+  // one 32-key tile: 32 MFMAs per wave, then the weighted ReLU sum over the
+  // heads and the stores (the other workgroup on the CU runs its MFMAs
+  // meanwhile; the next tile's DMA is in flight)
+  auto compute = [&](int kt, const u32x4* kt_lds) {
+    acc_t acc[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] = acc_t{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      // B operand: key l % 32, dims 16 s + 8 (l / 32) .. = chunk 2 s + l / 32
+      const bf16x8 kb = lds_read_b128(kt_lds, (uint32_t)(hl * kPitch + 2 * s + lg) * 16u);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = M::mma(qa[mt][s], kb, acc[mt]);
+    }
+    float sc[QPW];
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int hg = 0; hg < HT; ++hg) {
+        const int mt = i * HT + hg;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 w4 = wq(mt, g4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x = fmaf(w4[e], fmaxf(acc[mt][4 * g4 + e], 0.f), x);
+        }
+      }
+      sc[i] = xor32_sum(x);  // lanes l and l ^ 32 hold the two halves of the heads
+    }
+    // stores: lane half lg writes query i0 + lg (lanes 0-31 only when QPW == 1)
+    const int key = kt * kKT + hl;
+#pragma unroll
+    for (int i0 = 0; i0 < QPW; i0 += 2) {
+      float v;
+      bool ok;
+      int e;
+      float* dst;
+      if constexpr (QPW == 1) {
+        v = sc[0];
+        ok = lg == 0 && qok[0];
+        e = qend[0];
+        dst = orow[0];
+      } else {
+        v = lg ? sc[i0 + 1] : sc[i0];
+        ok = lg ? qok[i0 + 1] : qok[i0];
+        e = lg ? qend[i0 + 1] : qend[i0];
+        dst = lg ? orow[i0 + 1] : orow[i0];
+      }
+      if (ok && key < p.Skv) dst[key] = key < e ? v : kNegInf;
+    }
+  };
+
+  if (ntiles > 0) load_tile(0, s_k0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();                     // tile 0 and the weights are in place
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    if (kt + 1 < ntiles) load_tile(kt + 1, s_k1);
+    compute(kt, s_k0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // tile kt + 1 has landed
+    __syncthreads();                     // and every wave is done with tile kt
+    if (kt + 1 < ntiles) {
+      if (kt + 2 < ntiles) load_tile(kt + 2, s_k0);
+      compute(kt + 1, s_k1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+    }
+  }
+}
+
+// Order-preserving map of a float to u32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Block-wide sum of one wave-uniform count per wave (kSelThreads threads);
+// `red` holds 2 x 16 ints, alternated by the caller's parity so one barrier
+// per call suffices.
+__device__ __forceinline__ int block_sum_waves(int wave_count, int* red, int parity) {
+  const int wave = threadIdx.x >> 6;
+  int* r = red + 16 * parity;
+  if ((threadIdx.x & 63) == 0) r[wave] = wave_count;
+  __syncthreads();
+  int s = 0;
+#pragma unroll
+  for (int w = 0; w < kSelThreads / 64; ++w) s += r[w];
+  return s;
+}
+
+// Exclusive block scan of one int per thread, and the total.
+__device__ __forceinline__ int block_exscan(int x, int* red, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += y;
+  }
+  __syncthreads();  // earlier readers of red are done
+  if (lane == 63) red[wave] = inc;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelThreads / 64; ++w) {
+    const int v = red[w];
+    base += (w < wave) ? v : 0;
+    tot += v;
+  }
+  *total = tot;
+  return base + inc - x;
+}
+
+// Selection over one row of n > K scores held as NG groups of 4 per thread
+// (thread tid owns keys [4 NG tid, 4 NG tid + 4 NG)); NG is fixed per
+// instantiation, so the bisection steps are straight-line code.
+template <int NG>
+__device__ __forceinline__ void select_row(const float* row, int n, int K, int32_t* out, int* red) {
+  constexpr int EPT = 4 * NG;
+  const int tid = threadIdx.x;
+  const int i0 = tid * EPT;
+  const int cnt = min(max(n - i0, 0), EPT);
+  // order keys (0 = absent: every real key is >= order_key(-inf) > 0)
+  uint32_t u[EPT];
+#pragma unroll
+  for (int v = 0; v < NG; ++v) {
+    f32x4 x = {kNegInf, kNegInf, kNegInf, kNegInf};
+    if (4 * v < cnt) x = *reinterpret_cast<const f32x4*>(row + i0 + 4 * v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) u[4 * v + e] = (4 * v + e < cnt) ? order_key(x[e]) : 0u;
+  }
+  // the K-th largest key, bit by bit from the top (a wave counts with
+  // ballots: one compare and a scalar popcount per score register)
+  uint32_t thr = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) c += __popcll(__ballot(u[e] >= cand));
+    if (block_sum_waves(c, red, bit & 1) >= K) thr = cand;
+  }
+  // keys above the threshold, and the first (lowest-index) ties up to K
+  int gt = 0, eq = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    gt += (u[e] > thr) ? 1 : 0;
+    eq += (u[e] == thr) ? 1 : 0;
+  }
+  int gt_total, eq_total, sel_total;
+  (void)block_exscan(gt, red + 32, &gt_total);  // (only the total is used)
+  const int eq_before = block_exscan(eq, red, &eq_total);
+  const int take = K - gt_total;  // >= 1 ties are selected
+  const int my_eq = min(max(take - eq_before, 0), eq);
+  int w = block_exscan(gt + my_eq, red + 32, &sel_total);
+  int teq = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const bool sel = u[e] > thr || (u[e] == thr && teq < my_eq);
+    teq += (u[e] == thr) ? 1 : 0;
+    if (sel) out[w++] = i0 + e;
+  }
+}
+
+__global__ __launch_bounds__(kSelThreads, 1) void topk_select_kernel(IndexerParams p, int t_begin, int t_end) {
+  __shared__ int red[64];
+  const int nt = t_end - t_begin;
+  const int b = blockIdx.x / nt;
+  const int t = t_begin + (int)(blockIdx.x % nt);
+  const int tid = threadIdx.x;
+  const int K = p.topk;
+  const int n = __builtin_amdgcn_readfirstlane(key_end(p, b, t));
+  int32_t* out = p.idx + b * p.i_sb + t * p.i_ss;
+
+  if (n <= K) {  // every allowed key, ascending, then padding
+    for (int i = tid; i < K; i += kSelThreads) out[i] = i < n ? i : -1;
+    return;
+  }
+  const float* row = p.logits + b * p.g_sb + (int64_t)(t - p.g_t0) * p.g_ss;
+  // groups of 4 scores per thread: the smallest power of two that holds n
+  const int ng = (n + 4 * kSelThreads - 1) / (4 * kSelThreads);
+  if (ng <= 1)
+    select_row<1>(row, n, K, out, red);
+  else if (ng <= 2)
+    select_row<2>(row, n, K, out, red);
+  else if (ng <= 4)
+    select_row<4>(row, n, K, out, red);
+  else if (ng <= 8)
+    select_row<8>(row, n, K, out, red);
+  else
+    select_row<16>(row, n, K, out, red);
+}
+
+}  // namespace
+
+int indexer_query_block(const IndexerParams& p) { return 4 * (128 / p.H); }
+
+hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
+  const int qb = indexer_query_block(p);
+  const int64_t n = (int64_t)p.B * ((t_end - t_begin + qb - 1) / qb);
+  if (n == 0) return hipSuccess;
+  if (p.H == 64)
+    hipLaunchKernelGGL(indexer_logits_kernel<64>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
+  else if (p.H == 32)
+    hipLaunchKernelGGL(indexer_logits_kernel<32>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
+  else if (p.H == 128)
+    hipLaunchKernelGGL(indexer_logits_kernel<128>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
+  else
+    return hipErrorNotSupported;
+  return hipGetLastError();
+}
+
+hipError_t launch_topk_select(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * (t_end - t_begin);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(topk_select_kernel, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);
+  return hipGetLastError();
+}
+
+}  // namespace sfa

@@ -39,6 +39,12 @@ Generalisations relative to the reference (the drop-in boundary's API):
   ``block_table[b, i // page_size]``; a slot whose page id lies outside
   ``[0, num_pages)`` is invalid.  The forward over a paged cache is then
   ``sfa_forward`` of the mapped cache and indices.
+* Top-k index producer (``indexer_scores``, ``indexer_topk``): also not in the
+  reference, which consumes its result (``topk_idxs``, SFA.py:88-90).  The
+  scores restate DeepSeek-V3.2's lightning indexer,
+  ``I[b,t,s] = sum_h w[b,t,h] * relu(<q[b,t,h], k[b,s]>)`` over the keys
+  ``s <= t + L_b - Sq``; a row keeps its ``topk`` best keys (equal scores: the
+  lower key first) in ascending key order, then ``-1``.
 
 Duplicated indices are counted once per slot, as in the reference, which
 processes every slot independently (SFA.py:386-467).
@@ -71,6 +77,9 @@ __all__ = [
     "valid_mask",
     "count_valid_pairs",
     "paged_to_contiguous",
+    "indexer_key_end",
+    "indexer_scores",
+    "indexer_topk",
 ]
 
 
@@ -297,3 +306,54 @@ def paged_to_contiguous(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tabl
     idx_out = torch.where(pmapped | (il < 0) | ~in_table, idx, torch.full_like(idx, -1))
     return gather(k_cache), gather(v_cache), idx_out
 
+
+
+
+def indexer_key_end(B: int, Sq: int, Skv: int, kv_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``[B, Sq]`` int64: query t of sequence b may see keys ``[0, end)``,
+    ``end = clamp(t + 1 + L_b - Sq, 0, L_b)``, ``L_b = min(kv_lens[b], Skv)`` or ``Skv``."""
+    L = torch.full((B,), Skv, dtype=torch.int64) if kv_lens is None else kv_lens.long().cpu().clamp(max=Skv)
+    t = torch.arange(Sq, dtype=torch.int64)
+    end = t[None, :] + 1 + L[:, None] - Sq
+    return torch.minimum(end, L[:, None]).clamp(min=0)
+
+
+def indexer_scores(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, kv_lens: Optional[torch.Tensor] = None,
+                   dtype: torch.dtype = torch.float32, max_chunk_bytes: int = 1 << 28) -> torch.Tensor:
+    """Lightning-indexer scores ``[B, Sq, Skv]``: ``sum_h w * relu(<q_h, k_s>)``
+    for the keys each query may see, ``-inf`` elsewhere.  ``q`` ``[B, Sq, H, D]``,
+    ``k`` ``[B, Skv, D]``, ``w`` ``[B, Sq, H]``."""
+    B, Sq, H, D = q.shape
+    Skv = k.shape[1]
+    end = indexer_key_end(B, Sq, Skv, kv_lens)
+    out = torch.empty(B, Sq, Skv, dtype=dtype)
+    rows = max(1, max_chunk_bytes // max(1, H * Skv * torch.finfo(dtype).bits // 8))
+    pos = torch.arange(Skv)
+    for b in range(B):
+        kb = k[b].to(dtype)
+        for t0 in range(0, Sq, rows):
+            t1 = min(Sq, t0 + rows)
+            dots = torch.einsum("thd,sd->ths", q[b, t0:t1].to(dtype), kb)
+            sc = torch.einsum("th,ths->ts", w[b, t0:t1].to(dtype), dots.clamp_min(0))
+            allowed = pos[None, :] < end[b, t0:t1, None]
+            out[b, t0:t1] = torch.where(allowed, sc, torch.full_like(sc, -math.inf))
+    return out
+
+
+def indexer_topk(scores: torch.Tensor, topk: int, end: torch.Tensor) -> torch.Tensor:
+    """``[B, Sq, 1, topk]`` int32 from scores ``[B, Sq, Skv]`` and the per-row
+    key ends ``[B, Sq]``: rows with ``end <= topk`` keep every allowed key;
+    others the ``topk`` keys of largest score, equal scores ordered by key
+    (a stable sort of descending scores); both in ascending key order, then -1."""
+    B, Sq, Skv = scores.shape
+    out = torch.full((B, Sq, 1, topk), -1, dtype=torch.int32)
+    for b in range(B):
+        for t in range(Sq):
+            n = int(end[b, t])
+            if n <= topk:
+                sel = torch.arange(n)
+            else:
+                order = torch.sort(scores[b, t, :n], descending=True, stable=True).indices
+                sel = torch.sort(order[:topk]).values
+            out[b, t, 0, :sel.numel()] = sel.to(torch.int32)
+    return out

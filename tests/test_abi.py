@@ -40,11 +40,14 @@ def test_struct_layout_matches_header(tmp_path):
     fields_f = [f for f, _ in _lib.FwdArgs._fields_]
     fields_b = [f for f, _ in _lib.BwdArgs._fields_]
     fields_p = [f for f, _ in _lib.KvPages._fields_]
+    fields_i = [f for f, _ in _lib.IndexerArgs._fields_]
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
-             'printf("%zu %zu %zu\\n", sizeof(sfa_fwd_args), sizeof(sfa_bwd_args), sizeof(sfa_kv_pages));']
+             'printf("%zu %zu %zu %zu\\n", sizeof(sfa_fwd_args), sizeof(sfa_bwd_args), sizeof(sfa_kv_pages), '
+             'sizeof(sfa_indexer_args));']
     lines += [f'printf("%zu\\n", offsetof(sfa_fwd_args, {f}));' for f in fields_f]
     lines += [f'printf("%zu\\n", offsetof(sfa_bwd_args, {f}));' for f in fields_b]
     lines += [f'printf("%zu\\n", offsetof(sfa_kv_pages, {f}));' for f in fields_p]
+    lines += [f'printf("%zu\\n", offsetof(sfa_indexer_args, {f}));' for f in fields_i]
     lines += ["return 0; }"]
     src.write_text("\n".join(lines))
     exe = tmp_path / "layout"
@@ -53,9 +56,10 @@ def test_struct_layout_matches_header(tmp_path):
     assert int(vals[0]) == ctypes.sizeof(_lib.FwdArgs)
     assert int(vals[1]) == ctypes.sizeof(_lib.BwdArgs)
     assert int(vals[2]) == ctypes.sizeof(_lib.KvPages)
-    offs = [int(x) for x in vals[3:]]
+    assert int(vals[3]) == ctypes.sizeof(_lib.IndexerArgs)
+    offs = [int(x) for x in vals[4:]]
     py = ([getattr(_lib.FwdArgs, f).offset for f in fields_f] + [getattr(_lib.BwdArgs, f).offset for f in fields_b]
-          + [getattr(_lib.KvPages, f).offset for f in fields_p])
+          + [getattr(_lib.KvPages, f).offset for f in fields_p] + [getattr(_lib.IndexerArgs, f).offset for f in fields_i])
     assert offs == py
 
 
