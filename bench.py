@@ -15,6 +15,9 @@ measured in the same run and reported under ``workloads``:
                   + combine, caches flushed (by a 1 GiB read) before every step (GB/s);
                   ``paged``: the same cache as a 64-row-page pool (4.8 GB, pages
                   shuffled) read through a block table
+* ``indexer``     top-k index producer for the prefill: S=32768 causal queries,
+                  64 index heads, d=128, top-k 2048 (scores + selection; TFLOP/s
+                  over the visible (query, key) pairs, 2 H d FLOP each)
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -215,12 +218,31 @@ def bench_mla_decode(args):
     return res
 
 
+def bench_indexer(args):
+    import torch
+    import ops_amd
+    B, S, H, K = 1, 32768, 64, 2048
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    q = torch.randn(B, S, H, 128, generator=g, device="cuda").bfloat16()
+    k = torch.randn(B, S, 128, generator=g, device="cuda").bfloat16()
+    w = torch.randn(B, S, H, generator=g, device="cuda") / math.sqrt(H)
+    fn = lambda: ops_amd.indexer_topk(q, k, w, K)
+    times, _ = time_steps(fn, max(2, args.steps // 2), 1)
+    ms = sum(times) / len(times)
+    flops = S * (S + 1) // 2 * H * 128 * 2.0
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"metric": "indexer scores + top-k, effective TFLOP/s (visible pairs)", "value": tf, "unit": "TFLOP/s",
+            "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+            "config": {"B": B, "S": S, "H_index": H, "d_index": 128, "topk": K, "causal": True}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--extra", default="prefill,train_gqa,mla_decode",
+    ap.add_argument("--extra", default="prefill,train_gqa,mla_decode,indexer",
                     help="comma list of additional workloads to measure ('' for none)")
     ap.add_argument("--no-bwd", action="store_true", help="skip the train_gqa backward timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -251,7 +273,7 @@ def main():
     for name in [x for x in args.extra.split(",") if x]:
         log(f"measuring {name}")
         extra[name] = {"prefill": bench_prefill, "train_gqa": bench_train_gqa,
-                       "mla_decode": bench_mla_decode}[name](args)
+                       "mla_decode": bench_mla_decode, "indexer": bench_indexer}[name](args)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
