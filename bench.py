@@ -63,6 +63,13 @@ def bwd_flops(w, pairs):
     return pairs * G * 2.0 * (3 * w.q.shape[3] + 2 * w.v.shape[3])
 
 
+def gathered_bytes(w, pairs):
+    """K and V rows read per valid pair (one read per pair serves the G
+    query heads); with G = 16 and d = 128 this stream, served mostly from
+    L2 / MALL, rather than the MFMA rate bounds the d = 128 kernels."""
+    return pairs * (w.q.shape[3] + w.v.shape[3]) * w.q.element_size()
+
+
 def time_steps(fn, steps, warmup, before=None):
     """Per-step HIP-event durations (ms) on the current stream."""
     import torch
@@ -150,7 +157,7 @@ def bench_prefill(args):
     ms = sum(times) / len(times)
     tf = flops / (ms * 1e-3) / 1e12
     return {"metric": "fwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
-            "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
             "config": {"B": 1, "S": 4096, "Hq": 16, "Hkv": 1, "d": 128, "topk": 512}}
 
 
@@ -165,6 +172,7 @@ def bench_train_gqa(args):
     ms = sum(times) / len(times)
     res = {"metric": "fwd effective TFLOP/s", "value": ff / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": ms,
            "valid_pairs": pairs, "hot_share": w.meta.get("hot_share"),
+           "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
            "config": {"B": 2, "S": 8192, "Hq": 32, "Hkv": 2, "d": 128, "topk": 1024}}
     res["frac_of_peak"] = res["value"] / PEAK_BF16_TFLOPS
     if not args.no_bwd:

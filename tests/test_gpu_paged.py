@@ -112,3 +112,21 @@ def test_full_decode_pool_beyond_4gib():
     assert torch.isfinite(l_p).all()
     del kp, vp
     torch.cuda.empty_cache()
+
+
+def test_single_row_pages_and_padded_table():
+    # page_size 1 (shift 0) and a block table whose rows are longer than the
+    # pages in use (row stride > max_pages)
+    _say("paged mla_decode: page_size 1, padded block-table rows")
+    w = make_workload("mla_decode", device=DEV, B=3, Skv=512, K=128, ctx_lo=200)
+    kp, vp, bt = page_kv(w.k, w.v, 1, seed=4, spare_pages=9)
+    wide = torch.full((bt.shape[0], bt.shape[1] + 37), -1, dtype=torch.int32, device=DEV)
+    wide[:, :bt.shape[1]] = bt
+    bt_view = wide[:, :bt.shape[1]]            # stride(0) = max_pages + 37
+    assert bt_view.stride(0) > bt_view.shape[1]
+    o_c, l_c = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, w.kv_lens)
+    o_p, l_p = ops_amd.sfa_forward_paged(w.q, kp, vp, bt_view, w.idx, w.scale, w.kv_lens)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_c)
+    assert torch.equal(l_p, l_c)
+
