@@ -17,7 +17,9 @@ measured in the same run and reported under ``workloads``:
                   shuffled) read through a block table
 * ``indexer``     top-k index producer for the prefill: S=32768 causal queries,
                   64 index heads, d=128, top-k 2048 (scores + selection; TFLOP/s
-                  over the visible (query, key) pairs, 2 H d FLOP each)
+                  over the visible (query, key) pairs, 2 H d FLOP each);
+                  ``layer_ms``: indexer + MLA forward on the indices it produced
+                  (the whole sparse attention layer of the prefill)
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -226,7 +228,7 @@ def bench_mla_decode(args):
     return res
 
 
-def bench_indexer(args):
+def bench_indexer(args, mla=None):
     import torch
     import ops_amd
     B, S, H, K = 1, 32768, 64, 2048
@@ -240,9 +242,20 @@ def bench_indexer(args):
     ms = sum(times) / len(times)
     flops = S * (S + 1) // 2 * H * 128 * 2.0
     tf = flops / (ms * 1e-3) / 1e12
-    return {"metric": "indexer scores + top-k, effective TFLOP/s (visible pairs)", "value": tf, "unit": "TFLOP/s",
-            "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
-            "config": {"B": B, "S": S, "H_index": H, "d_index": 128, "topk": K, "causal": True}}
+    res = {"metric": "indexer scores + top-k, effective TFLOP/s (visible pairs)", "value": tf, "unit": "TFLOP/s",
+           "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+           "config": {"B": B, "S": S, "H_index": H, "d_index": 128, "topk": K, "causal": True}}
+    if mla is not None:
+        out = torch.empty(mla.q.shape[:3] + (mla.v.shape[3],), dtype=mla.q.dtype, device="cuda")
+        lse = torch.empty(mla.q.shape[:3], dtype=torch.float32, device="cuda")
+
+        def layer():
+            idx = ops_amd.indexer_topk(q, k, w, K)
+            ops_amd.sfa_forward(mla.q, mla.k, mla.v, idx, mla.scale, out=out, lse=lse)
+
+        lt, _ = time_steps(layer, max(2, args.steps // 2), 1)
+        res["layer_ms"] = sum(lt) / len(lt)
+    return res
 
 
 def main():
@@ -280,8 +293,11 @@ def main():
     extra = {}
     for name in [x for x in args.extra.split(",") if x]:
         log(f"measuring {name}")
-        extra[name] = {"prefill": bench_prefill, "train_gqa": bench_train_gqa,
-                       "mla_decode": bench_mla_decode, "indexer": bench_indexer}[name](args)
+        if name == "indexer":
+            extra[name] = bench_indexer(args, w)
+        else:
+            extra[name] = {"prefill": bench_prefill, "train_gqa": bench_train_gqa,
+                           "mla_decode": bench_mla_decode}[name](args)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
