@@ -22,11 +22,12 @@
 //  * topk_select_kernel: one 1024-thread workgroup per query row, the row's
 //    scores spread over the threads in contiguous runs of 4, 8, 16, 32 or 64
 //    (the smallest that holds the row; one instantiation each) in VGPRs as
-//    order-preserving u32 keys.  The k-th largest key
-//    is found exactly by bisection over its 32 bits (per step: one compare per
-//    score and one block sum; no histogram atomics), then the selected keys are
-//    written in ascending key order: all keys above the threshold, and the
-//    lowest-index keys equal to it until k are chosen (two block scans).
+//    order-preserving u32 keys.  The k-th largest key is found exactly by
+//    bisection over its 32 bits: the top 16 block-wide (per step one compare
+//    per score and one block sum; no histogram atomics), the low 16 by one
+//    wave over the keys still in play, compacted into LDS.  Then the selected
+//    keys are written in ascending key order: all keys above the threshold,
+//    and the lowest-index keys equal to it until k are chosen (block scans).
 
 #include "sfa_common.h"
 #include "sfa_lds.h"
@@ -44,6 +45,7 @@ constexpr int kLogitThreads = 256;
 constexpr int kSelThreads = 1024;
 constexpr int kSelEpt = 64;      // scores per thread in the selection kernel
 constexpr int kSelCap = kSelThreads * kSelEpt;  // longest score row (the API admits Skv <= 65536)
+constexpr int kCompact = 4096;   // keys still in play after the top 16 bits that one wave finishes
 static_assert(kSelCap == 65536, "selection capacity");
 
 // Keys query t of sequence b may see: [0, end).
@@ -255,7 +257,7 @@ __device__ __forceinline__ int block_exscan(int x, int* red, int* total) {
 // (thread tid owns keys [4 NG tid, 4 NG tid + 4 NG)); NG is fixed per
 // instantiation, so the bisection steps are straight-line code.
 template <int NG>
-__device__ __forceinline__ void select_row(const float* row, int n, int K, int32_t* out, int* red) {
+__device__ __forceinline__ void select_row(const float* row, int n, int K, int32_t* out, int* red, uint32_t* s_c) {
   constexpr int EPT = 4 * NG;
   const int tid = threadIdx.x;
   const int i0 = tid * EPT;
@@ -272,13 +274,56 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
   // the K-th largest key, bit by bit from the top (a wave counts with
   // ballots: one compare and a scalar popcount per score register)
   uint32_t thr = 0;
+  auto block_steps = [&](int hi, int lo) {
 #pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int c = 0;
+    for (int bit = hi; bit >= lo; --bit) {
+      const uint32_t cand = thr | (1u << bit);
+      int c = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) c += __popcll(__ballot(u[e] >= cand));
-    if (block_sum_waves(c, red, bit & 1) >= K) thr = cand;
+      for (int e = 0; e < EPT; ++e) c += __popcll(__ballot(u[e] >= cand));
+      if (block_sum_waves(c, red, bit & 1) >= K) thr = cand;
+    }
+  };
+  block_steps(31, 16);
+  // Keys whose top 16 bits equal the threshold's are the only ones the low
+  // bits still decide ("in play"; typically a few hundred): compact them into
+  // LDS and let one wave finish without block barriers.  count(u >= cand)
+  // for a candidate with the same top bits = (keys above that prefix) +
+  // (in-play keys >= cand).
+  {
+    const uint32_t top = thr >> 16;
+    int above = 0, inplay = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      above += (u[e] >> 16) > top ? 1 : 0;
+      inplay += (u[e] >> 16) == top ? 1 : 0;
+    }
+    int above_total, inplay_total;
+    (void)block_exscan(above, red + 32, &above_total);
+    int w = block_exscan(inplay, red, &inplay_total);
+    if (inplay_total <= kCompact) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        if ((u[e] >> 16) == top) s_c[w++] = u[e];
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+#pragma unroll 1
+        for (int bit = 15; bit >= 0; --bit) {
+          const uint32_t cand = thr | (1u << bit);
+          int c = 0;
+          for (int i = lane; i < inplay_total; i += 64) c += s_c[i] >= cand ? 1 : 0;
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+          if (above_total + c >= K) thr = cand;
+        }
+        if (lane == 0) red[80] = (int)thr;
+      }
+      __syncthreads();
+      thr = (uint32_t)red[80];
+    } else {
+      block_steps(15, 0);
+    }
   }
   // keys above the threshold, and the first (lowest-index) ties up to K
   int gt = 0, eq = 0;
@@ -303,7 +348,8 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
 }
 
 __global__ __launch_bounds__(kSelThreads, 1) void topk_select_kernel(IndexerParams p, int t_begin, int t_end) {
-  __shared__ int red[64];
+  __shared__ int red[96];
+  __shared__ uint32_t s_c[kCompact];
   const int nt = t_end - t_begin;
   const int b = blockIdx.x / nt;
   const int t = t_begin + (int)(blockIdx.x % nt);
@@ -320,15 +366,15 @@ __global__ __launch_bounds__(kSelThreads, 1) void topk_select_kernel(IndexerPara
   // groups of 4 scores per thread: the smallest power of two that holds n
   const int ng = (n + 4 * kSelThreads - 1) / (4 * kSelThreads);
   if (ng <= 1)
-    select_row<1>(row, n, K, out, red);
+    select_row<1>(row, n, K, out, red, s_c);
   else if (ng <= 2)
-    select_row<2>(row, n, K, out, red);
+    select_row<2>(row, n, K, out, red, s_c);
   else if (ng <= 4)
-    select_row<4>(row, n, K, out, red);
+    select_row<4>(row, n, K, out, red, s_c);
   else if (ng <= 8)
-    select_row<8>(row, n, K, out, red);
+    select_row<8>(row, n, K, out, red, s_c);
   else
-    select_row<16>(row, n, K, out, red);
+    select_row<16>(row, n, K, out, red, s_c);
 }
 
 }  // namespace
