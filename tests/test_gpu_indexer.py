@@ -160,3 +160,19 @@ def test_indexer_feeds_mla_forward():
     o_ref, l_ref = ref_forward(q.cpu().float(), kv.cpu().float(), kv[..., :512].cpu().float(), idx.cpu(), scale)
     assert float((out.float().cpu() - o_ref).abs().max()) <= 2e-2
     assert float((lse.cpu() - l_ref).abs().max()) <= 1e-3
+
+
+def test_indexer_degenerate_rows():
+    # more queries than keys (early rows see nothing), a zero-length sequence,
+    # top-k larger than the whole context
+    B, Sq, Skv, H, K = 3, 64, 40, 64, 50
+    _say(f"indexer degenerate rows B={B} Sq={Sq} Skv={Skv} K={K}")
+    q, k, w = _inputs(B, Sq, Skv, H, seed=31)
+    kv_lens = torch.tensor([0, 40, 17], dtype=torch.int32, device=DEV)
+    idx = ops_amd.indexer_topk(q, k, w, K, kv_lens=kv_lens).cpu()
+    torch.cuda.synchronize()
+    end = indexer_key_end(B, Sq, Skv, kv_lens.cpu())
+    assert int(end[0].max()) == 0 and int(end[1, 0]) == 0 and int(end[1, -1]) == 40
+    ref = indexer_topk(indexer_scores(q.cpu(), k.cpu(), w.cpu(), kv_lens.cpu()), K, end)
+    assert torch.equal(idx, ref)  # every row keeps all of its (<= K) visible keys
+    assert bool((idx[0] == -1).all())
