@@ -245,6 +245,19 @@ def bench_indexer(args, mla=None):
     res = {"metric": "indexer scores + top-k, effective TFLOP/s (visible pairs)", "value": tf, "unit": "TFLOP/s",
            "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
            "config": {"B": B, "S": S, "H_index": H, "d_index": 128, "topk": K, "causal": True}}
+    # the same scores from fp8 e4m3 q / k (per-token k scales, q scales
+    # folded into the weights), as DeepSeek-V3.2 stores the indexer inputs
+    f8 = torch.float8_e4m3fn
+    ks = k.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    k8 = (k.float() / ks[..., None]).to(f8)
+    qs = q.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    q8 = (q.float() / qs[..., None]).to(f8)
+    w8 = (w * qs).contiguous()
+    ft, _ = time_steps(lambda: ops_amd.indexer_topk(q8, k8, w8, K, k_scale=ks), max(2, args.steps // 2), 1)
+    fms = sum(ft) / len(ft)
+    res["fp8"] = {"value": flops / (fms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": fms,
+                  "note": "fp8 e4m3 q / k, per-token k scales; TFLOP/s over the same visible pairs"}
+    del q8, k8
     if mla is not None:
         out = torch.empty(mla.q.shape[:3] + (mla.v.shape[3],), dtype=mla.q.dtype, device="cuda")
         lse = torch.empty(mla.q.shape[:3], dtype=torch.float32, device="cuda")

@@ -50,8 +50,9 @@ extern "C" {
 #define SFA_API
 #endif
 
-/* Element types of q, k, v, out, dout, dq, dk, dv. */
-enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1 };
+/* Element types of q, k, v, out, dout, dq, dk, dv (F32, BF16), and of the
+ * index producer's q / k (BF16, FP8_E4M3: OCP e4m3, one byte). */
+enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1, SFA_DTYPE_FP8_E4M3 = 2 };
 
 /* How the backward produces dK/dV. */
 enum {
@@ -128,11 +129,16 @@ typedef struct sfa_kv_pages {
  * for a single decode query.  Row idx[b,t,:] receives the min(topk, allowed)
  * allowed keys with the largest scores (equal scores: the lower key first),
  * in ascending key order, then -1 padding.
- * Supported: bf16 q / k, D = 128, H in {32, 64, 128}, Skv <= 65536. */
+ * fp8 (SFA_DTYPE_FP8_E4M3) q / k, as DeepSeek-V3.2 stores them: the score is
+ *   I[b,t,s] = k_scale[b,s] * sum_h w[b,t,h] * max(0, <q[b,t,h,:], k[b,s,:]>)
+ * with positive per-token k scales (NULL = 1) and the q scales folded into w.
+ * Supported: bf16 or fp8 q / k, D = 128, H in {32, 64, 128}, Skv <= 65536. */
 typedef struct sfa_indexer_args {
   int32_t B, Sq, Skv, H, D, topk;
-  const void* q;   int64_t q_sb, q_ss, q_sh;      /* [B, Sq, H, D] bf16, unit feature stride  */
-  const void* k;   int64_t k_sb, k_ss;            /* [B, Skv, D] bf16, unit feature stride    */
+  int32_t dtype;                                  /* SFA_DTYPE_BF16 or SFA_DTYPE_FP8_E4M3      */
+  const void* q;   int64_t q_sb, q_ss, q_sh;      /* [B, Sq, H, D], unit feature stride       */
+  const void* k;   int64_t k_sb, k_ss;            /* [B, Skv, D], unit feature stride         */
+  const float* k_scale; int64_t ks_sb;            /* fp8: [B, Skv] positive scales, or NULL   */
   const float* w;  int64_t w_sb, w_ss;            /* [B, Sq, H] float32, unit head stride     */
   const int32_t* kv_lens;                         /* [B] or NULL                              */
   int32_t* idx;    int64_t i_sb, i_ss;            /* [B, Sq, topk] int32 out, unit slot stride */

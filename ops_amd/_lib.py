@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsfa.so"
 SFA_ABI_VERSION = 2
 SFA_DTYPE_F32 = 0
 SFA_DTYPE_BF16 = 1
+SFA_DTYPE_FP8_E4M3 = 2
 SFA_DKV_AUTO = 0
 SFA_DKV_ATOMIC = 1
 SFA_DKV_CSR = 2
@@ -91,8 +92,10 @@ class IndexerArgs(ctypes.Structure):
     """Mirror of ``sfa_indexer_args``."""
     _fields_ = [
         ("B", _i32), ("Sq", _i32), ("Skv", _i32), ("H", _i32), ("D", _i32), ("topk", _i32),
+        ("dtype", _i32),
         ("q", _vp), ("q_sb", _i64), ("q_ss", _i64), ("q_sh", _i64),
         ("k", _vp), ("k_sb", _i64), ("k_ss", _i64),
+        ("k_scale", _vp), ("ks_sb", _i64),
         ("w", _vp), ("w_sb", _i64), ("w_ss", _i64),
         ("kv_lens", _vp),
         ("idx", _vp), ("i_sb", _i64), ("i_ss", _i64),

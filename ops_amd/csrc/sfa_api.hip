@@ -355,15 +355,19 @@ int check_indexer(const sfa_indexer_args* a) {
   if (a->topk <= 0) return fail(SFA_E_INVALID, "topk must be positive (got %d)", a->topk);
   if (!a->q || !a->k || !a->w || !a->idx) return fail(SFA_E_INVALID, "null tensor pointer");
   if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if (a->dtype != SFA_DTYPE_BF16 && a->dtype != SFA_DTYPE_FP8_E4M3)
+    return fail(SFA_E_INVALID, "indexer dtype must be SFA_DTYPE_BF16 or SFA_DTYPE_FP8_E4M3 (got %d)", a->dtype);
+  if (a->k_scale && a->dtype != SFA_DTYPE_FP8_E4M3) return fail(SFA_E_INVALID, "k_scale is for fp8 keys only");
   if (a->D != 128 || (a->H != 32 && a->H != 64 && a->H != 128))
     return fail(SFA_E_UNSUPPORTED, "the indexer supports D = 128 and H in {32, 64, 128} (got D = %d, H = %d)", a->D,
                 a->H);
   if (a->Skv > kIndexerMaxSkv) return fail(SFA_E_UNSUPPORTED, "the indexer supports Skv <= %d", kIndexerMaxSkv);
   if (!aligned16(a->q) || !aligned16(a->k)) return fail(SFA_E_INVALID, "q and k rows must be 16-byte aligned");
+  const int64_t esize = a->dtype == SFA_DTYPE_FP8_E4M3 ? 1 : 2;
   const int64_t st[] = {a->q_sb, a->q_ss, a->q_sh, a->k_sb, a->k_ss};
   for (int64_t x : st)
-    if (x % 8 != 0) return fail(SFA_E_INVALID, "q / k strides must be multiples of 8 elements");
-  if (2 * ((int64_t)(a->Skv - 1) * a->k_ss + a->D) >= (int64_t)0x80000000LL)
+    if ((x * esize) % 16 != 0) return fail(SFA_E_INVALID, "q / k strides must be multiples of 16 bytes");
+  if (esize * ((int64_t)(a->Skv - 1) * a->k_ss + a->D) >= (int64_t)0x80000000LL)
     return fail(SFA_E_UNSUPPORTED, "k rows of one sequence must lie within 2 GiB");
   if (a->logits) {
     if (!aligned16(a->logits) || a->g_ss % 4 != 0 || a->g_sb % 4 != 0 || a->g_ss < a->Skv)
@@ -376,6 +380,7 @@ sfa::IndexerParams to_iparams(const sfa_indexer_args* a) {
   sfa::IndexerParams p;
   memset(&p, 0, sizeof(p));
   p.q = a->q; p.k = a->k; p.w = a->w; p.kv_lens = a->kv_lens; p.idx = a->idx; p.logits = a->logits;
+  p.k_scale = a->k_scale; p.ks_sb = a->ks_sb; p.fp8 = a->dtype == SFA_DTYPE_FP8_E4M3;
   p.q_sb = a->q_sb; p.q_ss = a->q_ss; p.q_sh = a->q_sh;
   p.k_sb = a->k_sb; p.k_ss = a->k_ss;
   p.w_sb = a->w_sb; p.w_ss = a->w_ss;

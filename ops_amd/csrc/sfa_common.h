@@ -139,8 +139,10 @@ constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads 0
 
 // Top-k index producer (sfa_indexer.hip): indexer scores + top-k selection.
 struct IndexerParams {
-  const void* q;          // [B, Sq, H, D] bf16
-  const void* k;          // [B, Skv, D] bf16
+  const void* q;          // [B, Sq, H, D] bf16 or fp8 e4m3
+  const void* k;          // [B, Skv, D] bf16 or fp8 e4m3
+  const float* k_scale;   // fp8: [B, Skv] positive per-token scales, or nullptr
+  int64_t ks_sb;
   const float* w;         // [B, Sq, H] float32, head stride 1
   const int32_t* kv_lens; // [B] or nullptr
   int32_t* idx;           // [B, Sq, topk] int32 out, slot stride 1
@@ -152,6 +154,7 @@ struct IndexerParams {
   int64_t g_sb, g_ss;
   int g_t0;               // query of logits row 0 (the workspace holds a chunk of queries)
   int B, Sq, Skv, H, D, topk;
+  bool fp8;
 };
 
 }  // namespace sfa

@@ -39,9 +39,24 @@ namespace {
 
 constexpr int kD = 128;          // index head dim
 constexpr int kKT = 32;          // keys per tile
-constexpr int kPitch = 17;       // LDS row pitch of a key tile in 16-byte slots (16 + 1 pad)
-constexpr int kTileSlots = kKT * kPitch;
 constexpr int kLogitThreads = 256;
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// Operand geometry of the scores kernel per element type.  bf16: 32x32x16
+// MFMA, 8 contraction steps of 16 dims, a key row is 16 chunks of 16 bytes;
+// fp8 e4m3: 32x32x64 MFMA (twice the bf16 rate), 2 steps of 64 dims, a key
+// row is 8 chunks.  The LDS tile pitch is the row's chunks + 1 (odd, so the
+// operand reads of 16 consecutive rows hit distinct banks).
+template <bool F8>
+struct IdxOps {
+  static constexpr int kChunks = F8 ? 8 : 16;       // 16-byte chunks per key row
+  static constexpr int kPitch = kChunks + 1;
+  static constexpr int kTileSlots = kKT * kPitch;
+  static constexpr int kSteps = F8 ? 2 : 8;         // contraction steps over d = 128
+  static constexpr int kElem = F8 ? 1 : 2;          // bytes per element
+  typedef typename std::conditional<F8, i32x8, bf16x8>::type op_t;
+};
 constexpr int kSelThreads = 1024;
 constexpr int kSelEpt = 64;      // scores per thread in the selection kernel
 constexpr int kSelCap = kSelThreads * kSelEpt;  // longest score row (the API admits Skv <= 65536)
@@ -57,7 +72,7 @@ __device__ __forceinline__ int key_end(const IndexerParams& p, int b, int t) {
   return max(e, 0);
 }
 
-template <int H>
+template <int H, bool F8>
 __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(IndexerParams p, int t_begin, int t_end) {
   constexpr int QPW = 128 / H;        // queries per wave
   constexpr int HT = H / 32;          // M-tiles (32 heads) per query
@@ -65,6 +80,9 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   static_assert(QPW * HT == 4, "four M-tiles per wave");
   using M = Mfma<32>;
   typedef typename M::acc_t acc_t;
+  typedef IdxOps<F8> O;
+  typedef typename O::op_t op_t;
+  constexpr int kPitch = O::kPitch, kTileSlots = O::kTileSlots;
 
   // two distinct arrays (not one indexed by parity): the compiler then knows
   // the DMA into one does not feed the operand reads of the other
@@ -87,9 +105,10 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   const int kend_wg = key_end(p, b, t_last);
   const int ntiles = (kend_wg + kKT - 1) / kKT;
 
-  // ---- q operands (A: lane l holds head 32 hg + l % 32, dims 16 s + 8 (l / 32) ..) and weights
+  // ---- q operands (A: lane l holds head 32 hg + l % 32; bf16: dims
+  // 16 s + 8 (l / 32) .. + 7, fp8: dims 64 s + 32 (l / 32) .. + 31) and weights
   const int hl = lane & 31, lg = lane >> 5;
-  bf16x8 qa[4][8];
+  op_t qa[4][O::kSteps];
   int tq[QPW];
   bool qok[QPW];
 #pragma unroll
@@ -101,9 +120,18 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   for (int mt = 0; mt < 4; ++mt) {
     const int i = mt / HT, hg = mt % HT;
     const int t = qok[i] ? tq[i] : t_begin;
-    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)(hg * 32 + hl) * p.q_sh;
+    const char* qrow = reinterpret_cast<const char*>(p.q) +
+                       O::kElem * (b * p.q_sb + t * p.q_ss + (int64_t)(hg * 32 + hl) * p.q_sh);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qa[mt][s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * lg);
+    for (int s = 0; s < O::kSteps; ++s) {
+      if constexpr (F8) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(qrow + 64 * s + 32 * lg);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(qrow + 64 * s + 32 * lg + 16);
+        qa[mt][s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      } else {
+        qa[mt][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 16 * lg);
+      }
+    }
     const float* wrow = p.w + b * p.w_sb + t * p.w_ss + hg * 32;
     if (lg == 0) s_w[(wave * 4 + mt) * 32 + hl] = wrow[hl];
   }
@@ -113,10 +141,12 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
     return *reinterpret_cast<const f32x4*>(&s_w[(wave * 4 + mt) * 32 + 8 * g4 + 4 * lg]);
   };
 
-  // ---- key tile DMA: slot u = 17 r + c holds chunk c of key row r (c = 16: pad)
-  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb);
-  const uint32_t krow = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + kD)));
+  // ---- key tile DMA: slot u = kPitch r + c holds chunk c of key row r (the
+  // last chunk of a row is the pad)
+  const char* kbase = reinterpret_cast<const char*>(p.k) + O::kElem * (b * p.k_sb);
+  const uint32_t krow = (uint32_t)(O::kElem * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(kbase, (uint32_t)(O::kElem * ((int64_t)(p.Skv - 1) * p.k_ss + kD)));
   auto load_tile = [&](int kt, u32x4* dst) {
 #pragma unroll
     for (int it = 0; it < (kTileSlots + kLogitThreads - 1) / kLogitThreads; ++it) {
@@ -124,7 +154,8 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
       if (u < kTileSlots) {
         const int r = u / kPitch, c = u - r * kPitch;
         const int key = kt * kKT + r;
-        const uint32_t off = (c < 16 && key < kend_wg) ? __umul24((uint32_t)key, krow) + 16u * (uint32_t)c : kOOB;
+        const uint32_t off =
+            (c < O::kChunks && key < kend_wg) ? __umul24((uint32_t)key, krow) + 16u * (uint32_t)c : kOOB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(dst + it * kLogitThreads + wave * 64), 16, off, 0, 0,
                                                  0);
       }
@@ -148,11 +179,22 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[mt] = acc_t{};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      // B operand: key l % 32, dims 16 s + 8 (l / 32) .. = chunk 2 s + l / 32
-      const bf16x8 kb = lds_read_b128(kt_lds, (uint32_t)(hl * kPitch + 2 * s + lg) * 16u);
+    for (int s = 0; s < O::kSteps; ++s) {
+      if constexpr (F8) {
+        // B operand: key l % 32, dims 64 s + 32 (l / 32) .. = chunks 4 s + 2 (l / 32) + {0, 1}
+        const uint32_t a0 = (uint32_t)(hl * kPitch + 4 * s + 2 * lg) * 16u;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kt_lds) + a0);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kt_lds) + a0 + 16u);
+        const i32x8 kb = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt] = M::mma(qa[mt][s], kb, acc[mt]);
+        for (int mt = 0; mt < 4; ++mt)
+          acc[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mt][s], kb, acc[mt], 0, 0, 0, 0, 0, 0);
+      } else {
+        // B operand: key l % 32, dims 16 s + 8 (l / 32) .. = chunk 2 s + l / 32
+        const bf16x8 kb = lds_read_b128(kt_lds, (uint32_t)(hl * kPitch + 2 * s + lg) * 16u);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = M::mma(qa[mt][s], kb, acc[mt]);
+      }
     }
     float sc[QPW];
 #pragma unroll
@@ -172,6 +214,14 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
     }
     // stores: lane half lg writes query i0 + lg (lanes 0-31 only when QPW == 1)
     const int key = kt * kKT + hl;
+    if constexpr (F8) {
+      // positive per-key scale: k_scale * sum_h w relu(dot) = sum_h w relu(dot * k_scale)
+      if (p.k_scale) {
+        const float ks = key < p.Skv ? p.k_scale[b * p.ks_sb + key] : 0.f;
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) sc[i] *= ks;
+      }
+    }
 #pragma unroll
     for (int i0 = 0; i0 < QPW; i0 += 2) {
       float v;
@@ -385,14 +435,26 @@ hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end,
   const int qb = indexer_query_block(p);
   const int64_t n = (int64_t)p.B * ((t_end - t_begin + qb - 1) / qb);
   if (n == 0) return hipSuccess;
-  if (p.H == 64)
-    hipLaunchKernelGGL(indexer_logits_kernel<64>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
-  else if (p.H == 32)
-    hipLaunchKernelGGL(indexer_logits_kernel<32>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
-  else if (p.H == 128)
-    hipLaunchKernelGGL(indexer_logits_kernel<128>, dim3((unsigned)n), dim3(kLogitThreads), 0, s, p, t_begin, t_end);
-  else
-    return hipErrorNotSupported;
+  const dim3 g((unsigned)n), blk(kLogitThreads);
+  if (p.fp8) {
+    if (p.H == 64)
+      hipLaunchKernelGGL((indexer_logits_kernel<64, true>), g, blk, 0, s, p, t_begin, t_end);
+    else if (p.H == 32)
+      hipLaunchKernelGGL((indexer_logits_kernel<32, true>), g, blk, 0, s, p, t_begin, t_end);
+    else if (p.H == 128)
+      hipLaunchKernelGGL((indexer_logits_kernel<128, true>), g, blk, 0, s, p, t_begin, t_end);
+    else
+      return hipErrorNotSupported;
+  } else {
+    if (p.H == 64)
+      hipLaunchKernelGGL((indexer_logits_kernel<64, false>), g, blk, 0, s, p, t_begin, t_end);
+    else if (p.H == 32)
+      hipLaunchKernelGGL((indexer_logits_kernel<32, false>), g, blk, 0, s, p, t_begin, t_end);
+    else if (p.H == 128)
+      hipLaunchKernelGGL((indexer_logits_kernel<128, false>), g, blk, 0, s, p, t_begin, t_end);
+    else
+      return hipErrorNotSupported;
+  }
   return hipGetLastError();
 }
 

@@ -25,9 +25,12 @@ __all__ = ["indexer_topk"]
 
 
 def indexer_topk(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, topk: int,
-                 kv_lens: Optional[torch.Tensor] = None, return_logits: bool = False):
-    """``q`` ``[B, Sq, H, 128]`` bf16, ``k`` ``[B, Skv, 128]`` bf16 (one index
-    key per token), ``weights`` ``[B, Sq, H]`` (float32 after conversion).
+                 kv_lens: Optional[torch.Tensor] = None, return_logits: bool = False,
+                 k_scale: Optional[torch.Tensor] = None):
+    """``q`` ``[B, Sq, H, 128]``, ``k`` ``[B, Skv, 128]`` (one index key per
+    token), both bfloat16 or both float8_e4m3fn, ``weights`` ``[B, Sq, H]``
+    (float32 after conversion; with fp8, the q scales folded in).  ``k_scale``
+    ``[B, Skv]`` (fp8 only, positive): the score of key s is multiplied by it.
 
     Returns ``topk_idxs`` ``[B, Sq, 1, topk]`` int32, ready for
     :func:`ops_amd.sparse_flash_attention` with one KV head, and with
@@ -43,8 +46,16 @@ def indexer_topk(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, topk: 
     for name, t in (("q", q), ("k", k), ("weights", weights)):
         if t.device.type != "cuda":
             raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
-        raise ValueError("q and k must be bfloat16")
+    f8 = getattr(torch, "float8_e4m3fn", None)
+    if q.dtype != k.dtype or q.dtype not in (torch.bfloat16, f8):
+        raise ValueError("q and k must both be bfloat16 or both float8_e4m3fn")
+    fp8 = q.dtype == f8
+    if k_scale is not None:
+        if not fp8:
+            raise ValueError("k_scale is for float8 keys only")
+        if tuple(k_scale.shape) != (B, k.shape[1]) or k_scale.device != q.device:
+            raise ValueError("k_scale must be a [B, Skv] tensor on q's device")
+        k_scale = k_scale.to(torch.float32).contiguous()
     if int(topk) <= 0:
         raise ValueError(f"topk must be positive, got {topk}")
     Skv = k.shape[1]
@@ -64,6 +75,9 @@ def indexer_topk(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, topk: 
         logits = torch.empty((B, Sq, ld), dtype=torch.float32, device=q.device)[..., :Skv]
     a = _lib.IndexerArgs()
     a.B, a.Sq, a.Skv, a.H, a.D, a.topk = B, Sq, Skv, H, D, int(topk)
+    a.dtype = _lib.SFA_DTYPE_FP8_E4M3 if fp8 else _lib.SFA_DTYPE_BF16
+    if k_scale is not None:
+        a.k_scale, a.ks_sb = k_scale.data_ptr(), k_scale.stride(0)
     a.q, (a.q_sb, a.q_ss, a.q_sh) = q.data_ptr(), q.stride()[:3]
     a.k, (a.k_sb, a.k_ss) = k.data_ptr(), k.stride()[:2]
     a.w, (a.w_sb, a.w_ss) = w.data_ptr(), w.stride()[:2]

@@ -319,10 +319,13 @@ def indexer_key_end(B: int, Sq: int, Skv: int, kv_lens: Optional[torch.Tensor] =
 
 
 def indexer_scores(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, kv_lens: Optional[torch.Tensor] = None,
-                   dtype: torch.dtype = torch.float32, max_chunk_bytes: int = 1 << 28) -> torch.Tensor:
+                   dtype: torch.dtype = torch.float32, max_chunk_bytes: int = 1 << 28,
+                   k_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Lightning-indexer scores ``[B, Sq, Skv]``: ``sum_h w * relu(<q_h, k_s>)``
     for the keys each query may see, ``-inf`` elsewhere.  ``q`` ``[B, Sq, H, D]``,
-    ``k`` ``[B, Skv, D]``, ``w`` ``[B, Sq, H]``."""
+    ``k`` ``[B, Skv, D]`` (bf16, fp32 or fp8 e4m3: every element is exact in
+    ``dtype``), ``w`` ``[B, Sq, H]``; ``k_scale`` ``[B, Skv]`` (positive) scales
+    the keys' scores, as DeepSeek-V3.2's fp8 indexer does."""
     B, Sq, H, D = q.shape
     Skv = k.shape[1]
     end = indexer_key_end(B, Sq, Skv, kv_lens)
@@ -335,6 +338,8 @@ def indexer_scores(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, kv_lens: O
             t1 = min(Sq, t0 + rows)
             dots = torch.einsum("thd,sd->ths", q[b, t0:t1].to(dtype), kb)
             sc = torch.einsum("th,ths->ts", w[b, t0:t1].to(dtype), dots.clamp_min(0))
+            if k_scale is not None:
+                sc = sc * k_scale[b].to(dtype)[None, :]
             allowed = pos[None, :] < end[b, t0:t1, None]
             out[b, t0:t1] = torch.where(allowed, sc, torch.full_like(sc, -math.inf))
     return out

@@ -176,3 +176,55 @@ def test_indexer_degenerate_rows():
     ref = indexer_topk(indexer_scores(q.cpu(), k.cpu(), w.cpu(), kv_lens.cpu()), K, end)
     assert torch.equal(idx, ref)  # every row keeps all of its (<= K) visible keys
     assert bool((idx[0] == -1).all())
+
+
+def _fp8_inputs(B, Sq, Skv, H, seed):
+    """fp8 e4m3 q / k as DeepSeek-V3.2 stores them: per-token k scales, the
+    per-(token, head) q scales folded into the weights."""
+    q, k, w = _inputs(B, Sq, Skv, H, seed)
+    f8 = torch.float8_e4m3fn
+    ks = k.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    k8 = (k.float() / ks[..., None]).to(f8)
+    qs = q.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    q8 = (q.float() / qs[..., None]).to(f8)
+    return q8, k8, (w * qs).contiguous(), ks.contiguous()
+
+
+@pytest.mark.parametrize("H,K,kv", [(64, 32, None), (64, 48, [300, 170]), (32, 16, None), (128, 40, [250, 300])],
+                         ids=["h64", "h64-kvlens", "h32", "h128-kvlens"])
+def test_indexer_fp8_small(H, K, kv):
+    B, Sq, Skv = 2, 100, 300
+    _say(f"indexer fp8 B={B} Sq={Sq} Skv={Skv} H={H} K={K} kv_lens={kv}")
+    q8, k8, w, ks = _fp8_inputs(B, Sq, Skv, H, seed=7 * H + K)
+    kv_lens = torch.tensor(kv, dtype=torch.int32, device=DEV) if kv else None
+    idx, logits = ops_amd.indexer_topk(q8, k8, w, K, kv_lens=kv_lens, return_logits=True, k_scale=ks)
+    torch.cuda.synchronize()
+    idx, logits = idx.cpu(), logits.cpu()
+    kvc = None if kv_lens is None else kv_lens.cpu()
+    end = indexer_key_end(B, Sq, Skv, kvc)
+    ref = indexer_scores(q8.cpu().float(), k8.cpu().float(), w.cpu(), kvc, k_scale=ks.cpu())
+    vis = torch.arange(Skv)[None, None, :] < end[:, :, None]
+    scale = float(ref[vis].abs().max())
+    err = float((logits[vis] - ref[vis]).abs().max())
+    assert err <= SCORE_RTOL * scale, f"score error {err} vs scale {scale}"
+    own = torch.where(vis, logits, torch.full_like(logits, -math.inf))
+    assert torch.equal(idx, indexer_topk(own, K, end))
+    _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
+
+
+def test_indexer_fp8_prefill_full_size_rows():
+    B, S, H, K = 1, 32768, 64, 2048
+    _say(f"indexer fp8 full prefill S={S} H={H} K={K}")
+    q8, k8, w, ks = _fp8_inputs(B, S, S, H, seed=15)
+    idx, logits = ops_amd.indexer_topk(q8, k8, w, K, return_logits=True, k_scale=ks)
+    torch.cuda.synchronize()
+    end = indexer_key_end(B, S, S)
+    rows = [0, 2047, 2048, 9000, 32767]
+    own = logits[0, rows].cpu()
+    vis = torch.arange(S)[None, :] < end[0, rows][:, None]
+    own = torch.where(vis, own, torch.full_like(own, -math.inf))
+    assert torch.equal(idx[0, rows].cpu()[:, None], indexer_topk(own[None], K, end[:, rows])[0][:, None])
+    r = 32767
+    qr, kr = q8[0, r].cpu().float(), k8[0].cpu().float()
+    ref = (w[0, r].cpu()[:, None] * (qr @ kr.T).clamp_min(0)).sum(0) * ks[0].cpu()
+    assert float((own[-1] - ref).abs().max()) <= SCORE_RTOL * float(ref.abs().max())

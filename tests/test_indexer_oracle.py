@@ -122,6 +122,7 @@ def test_host_validation():
 def _valid_indexer_args():
     a = _lib.IndexerArgs()
     a.B, a.Sq, a.Skv, a.H, a.D, a.topk = 1, 4, 8, 64, 128, 4
+    a.dtype = _lib.SFA_DTYPE_BF16
     for name in ("q", "k", "w", "idx"):
         setattr(a, name, 0x10000)
     a.q_sh, a.q_ss, a.q_sb = 128, 64 * 128, 4 * 64 * 128
@@ -133,6 +134,7 @@ def _valid_indexer_args():
     ("topk", 0, _lib.SFA_E_INVALID), ("B", 0, _lib.SFA_E_INVALID), ("q", None, _lib.SFA_E_INVALID),
     ("flags", 1, _lib.SFA_E_INVALID), ("D", 64, _lib.SFA_E_UNSUPPORTED), ("H", 48, _lib.SFA_E_UNSUPPORTED),
     ("Skv", 65537, _lib.SFA_E_UNSUPPORTED), ("k_ss", 100, _lib.SFA_E_INVALID), ("q", 0x10008, _lib.SFA_E_INVALID),
+    ("dtype", 0, _lib.SFA_E_INVALID), ("k_scale", 0x10000, _lib.SFA_E_INVALID),
 ])
 def test_indexer_abi_rejects(field, value, code):
     lib = _lib.load()
@@ -155,3 +157,24 @@ def test_indexer_workspace_is_bounded():
     a.g_ss, a.g_sb = 32768, 32768 * 32768
     assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) == 0
     assert lib.sfa_indexer_topk(None, None, 0, None) == _lib.SFA_E_INVALID
+
+
+def test_fp8_key_scale_closed_form():
+    # a positive per-key scale multiplies that key's score (relu commutes with it)
+    q, k, w = _case(3)
+    ks = torch.rand(2, 9, dtype=torch.float64) + 0.5
+    end = indexer_key_end(2, 5, 9)
+    scaled = indexer_scores(q, k, w, dtype=torch.float64, k_scale=ks)
+    plain = _loop_scores(q, k * ks[..., None], w, end)
+    fin = torch.isfinite(plain)
+    assert torch.allclose(scaled[fin], plain[fin], rtol=1e-12, atol=1e-12)
+
+
+def test_fp8_indexer_abi_accepts_fp8_strides():
+    lib = _lib.load()
+    a = _valid_indexer_args()
+    a.dtype = _lib.SFA_DTYPE_FP8_E4M3
+    a.k_ss, a.k_sb = 144, 8 * 144          # 144 B rows: a multiple of 16 bytes in fp8
+    assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) > 0
+    a.k_ss = 132                            # not a multiple of 16 bytes
+    assert lib.sfa_indexer_topk(ctypes.byref(a), None, 0, None) == _lib.SFA_E_INVALID
