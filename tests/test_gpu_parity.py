@@ -370,3 +370,31 @@ def test_reference_signature_shim():
         assert _rel_l2(q.grad.permute(1, 0, 2, 3).cpu(), dq) <= GRAD_RL2
         assert _rel_l2(kv.grad.permute(1, 0, 2).unsqueeze(2).cpu(), dk + dv) <= GRAD_RL2
         assert _rel_l2(sink.grad.cpu(), ds) <= GRAD_RL2
+
+
+def test_mla_shared_kv_backward_generic():
+    """The MLA training shape (one latent KV row per token, d_qk 576, V = its
+    first 512 dims, G = 128): through autograd the shared kv's gradient is
+    dK + dV (the reference sums both into one buffer, SFA.py:849-853).  It
+    runs on the generic kernels (correct, not a performance path)."""
+    _say("MLA shared-kv backward B=1 S=48 Hq=128 d 576/512 K=24 (generic kernels)")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    B, S, H, K = 1, 48, 128, 24
+    q = torch.randn(B, S, H, 576, device=DEV, generator=g).bfloat16().requires_grad_(True)
+    kv = torch.randn(B, S, 1, 576, device=DEV, generator=g).bfloat16().requires_grad_(True)
+    idx = torch.randint(-1, S, (B, S, 1, K), device=DEV, generator=g, dtype=torch.int32)
+    sink = torch.randn(H, device=DEV, generator=g).requires_grad_(True)
+    dout = torch.randn(B, S, H, 512, device=DEV, generator=g).bfloat16()
+    scale = 1.0 / math.sqrt(576)
+    out, lse = ops_amd.sparse_flash_attention(q, kv, kv[..., :512], idx, scale, attn_sink=sink)
+    out.backward(dout)
+    qc, kc = q.detach().float().cpu(), kv.detach().float().cpu()
+    o_ref, l_ref = ref_forward(qc, kc, kc[..., :512], idx.cpu(), scale, sink=sink.detach().cpu())
+    _check_fwd(out.detach(), lse.detach(), o_ref, l_ref)
+    dq, dk, dv, ds = ref_backward(qc, kc, kc[..., :512], idx.cpu(), o_ref, l_ref, dout.float().cpu(), scale,
+                                  sink=sink.detach().cpu())
+    dkv = dk.clone()
+    dkv[..., :512] += dv
+    assert _rel_l2(q.grad.float().cpu(), dq) <= GRAD_RL2
+    assert _rel_l2(kv.grad.float().cpu(), dkv) <= GRAD_RL2
+    assert _rel_l2(sink.grad.cpu(), ds) <= GRAD_RL2
