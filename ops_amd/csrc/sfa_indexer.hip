@@ -6,19 +6,22 @@
 //   I[b,t,s] = sum_h w[b,t,h] * max(0, <q[b,t,h,:], k[b,s,:]>)
 //
 // over the keys s a query may see (s <= t + L_b - Sq, L_b = kv_lens[b] or
-// Skv), then the top-k keys of every query row.
+// Skv), then the top-k keys of every query row.  With fp8 (e4m3) q / k, a
+// positive per-token scale multiplies each key's score (DeepSeek-V3.2 stores
+// the indexer inputs that way, the q scales folded into w).
 //
 // Two kernels:
-//  * indexer_logits_kernel<H>: bf16 MFMA (32x32x16), heads as MFMA rows and
-//    keys as columns.  A wave keeps 4 M-tiles of q in VGPRs (128 / H queries
-//    x H heads, d = 128), the workgroup's 4 waves share each 32-key tile of k,
-//    DMA'd into a double-buffered LDS tile (row pitch 17 slots: the b128
-//    operand reads are bank-conflict free); the head weights sit in LDS, so
-//    two workgroups fit a CU and one's MFMAs cover the other's epilogue and
-//    tile wait.  The epilogue applies the weights
-//    and the ReLU to the fp32 accumulators and sums over the heads in
-//    registers (16 rows per lane, then the lane pair l, l ^ 32), so one
-//    coalesced 128-byte store per query writes 32 scores.
+//  * indexer_logits_kernel<H, F8>: MFMA with heads as rows and keys as
+//    columns (bf16: 32x32x16, fp8: 32x32x64 at twice the rate).  A wave keeps
+//    4 M-tiles of q in VGPRs (128 / H queries x H heads, d = 128), the
+//    workgroup's 4 waves share each 32-key tile of k, DMA'd into a
+//    double-buffered LDS tile (row pitch: the row's 16-byte chunks + 1, so
+//    the b128 operand reads are bank-conflict free); the head weights sit in
+//    LDS, so two workgroups fit a CU and one's MFMAs cover the other's
+//    epilogue and tile wait.  The epilogue applies the weights and the ReLU
+//    to the fp32 accumulators and sums over the heads in registers (16 rows
+//    per lane, then the lane pair l, l ^ 32), so one coalesced 128-byte store
+//    per query writes 32 scores.
 //  * topk_select_kernel: one 1024-thread workgroup per query row, the row's
 //    scores spread over the threads in contiguous runs of 4, 8, 16, 32 or 64
 //    (the smallest that holds the row; one instantiation each) in VGPRs as
@@ -58,7 +61,7 @@ struct IdxOps {
   typedef typename std::conditional<F8, i32x8, bf16x8>::type op_t;
 };
 constexpr int kSelThreads = 1024;
-constexpr int kSelEpt = 64;      // scores per thread in the selection kernel
+constexpr int kSelEpt = 64;      // most scores per thread in the selection kernel
 constexpr int kSelCap = kSelThreads * kSelEpt;  // longest score row (the API admits Skv <= 65536)
 constexpr int kCompact = 4096;   // keys still in play after the top 16 bits that one wave finishes
 static_assert(kSelCap == 65536, "selection capacity");
