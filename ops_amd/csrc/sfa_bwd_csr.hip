@@ -289,68 +289,97 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
         vofs[hh][d] = (uint32_t)(row * kCH + ((4 * d + cl) ^ blk_swz(row))) * 16u + (uint32_t)(cc4 & 1) * 8u;
     }
   }
+  // One query block = 4 tiles of 32 rows.  Tile t: S, dP (16 MFMAs), then P,
+  // dS (VALU), then dV, dK (16 MFMAs).  Software pipelined at one wave per
+  // SIMD: the P/dS arithmetic of tile t runs between the S/dP MFMAs of tile
+  // t + 1 (two sets of S/dP accumulators), so the VALU works while the MFMA
+  // pipe is busy.  Fully unrolled: the tile offsets fold into the LDS read
+  // immediates.
+  constexpr int kTiles = kRowBlock / 32;
   auto compute = [&](const u32x4* qt, const u32x4* dt, const float* ls, const float* dl,
                      const uint32_t (*mk)[kRowBlock]) {
     const uint32_t* msk = mk[wave];
     bf16x8 prev_a = {}, prev_b = {};
-#pragma unroll 1
-    for (int mt = 0; mt < kRowBlock / 32; ++mt) {
-      const uint32_t mrow = (uint32_t)(32 * mt * kCH) * 16u;
-      // S, dP for rows 32 mt .. +31: two interleaved VGPR chains (inline-asm
-      // MFMAs, so the operand reads of step st + PDK stay ahead of the MFMAs
-      // of step st)
-      acc_t sacc, dpacc;
-      {
-        constexpr int NS = kD / 16, PDK = 4;
-        bf16x8 qa[PDK], da[PDK];
+    acc_t sacc[2], dpacc[2];
+    bf16x8 pb[2], db[2];
+    // S, dP for rows 32 t .. +31 into (sa, dpa): two interleaved VGPR chains
+    // (inline-asm MFMAs, so the operand reads of step st + PDK stay ahead of
+    // the MFMAs of step st); mid(st) runs after step st's two MFMAs.
+    auto sdp = [&](int t, acc_t& sa, acc_t& dpa, auto&& mid) {
+      constexpr int NS = kD / 16, PDK = 4;
+      const uint32_t mrow = (uint32_t)(32 * t * kCH) * 16u;
+      bf16x8 qa[PDK], da[PDK];
 #pragma unroll
-        for (int i = 0; i < PDK; ++i) {
-          qa[i] = lds_read_b128(qt, aofs[i] + mrow);
-          da[i] = lds_read_b128(dt, aofs[i] + mrow);
-        }
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-          const bf16x8 aq = qa[st % PDK], ad = da[st % PDK];
-          if (st + PDK < NS) {
-            qa[st % PDK] = lds_read_b128(qt, aofs[st + PDK] + mrow);
-            da[st % PDK] = lds_read_b128(dt, aofs[st + PDK] + mrow);
-          }
-          if (st == 0) {
-            M::mma_v0k(aq, kB[0], sacc, prev_a, prev_b);
-            M::mma_v0k(ad, vB[0], dpacc, aq, kB[0]);
-          } else {
-            M::mma_v(aq, kB[st], sacc, prev_a, prev_b);
-            M::mma_v(ad, vB[st], dpacc, aq, kB[st]);
-          }
-          prev_a = ad;
-          prev_b = vB[st];
-        }
-        M::drain_v2(sacc, dpacc, prev_a, prev_b);
+      for (int i = 0; i < PDK; ++i) {
+        qa[i] = lds_read_b128(qt, aofs[i] + mrow);
+        da[i] = lds_read_b128(dt, aofs[i] + mrow);
       }
-      // P and dS; C-layout element e is row 32 mt + 8 (e / 4) + 4 g2 + e % 4
-      bf16x8 pb[2], db[2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r0 = 32 * mt + 8 * q + 4 * g2;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + r0);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + r0);
-        const u32x4 m4 = *reinterpret_cast<const u32x4*>(msk + r0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e = 4 * q + j;
-          const bool mem = (m4[j] >> n) & 1u;
-          const float pr = mem ? __builtin_amdgcn_exp2f(fmaf(sacc[e], p.scale_log2, -l4[j] * kLog2e)) : 0.f;
-          const float ds = pr * (dpacc[e] - d4[j]);
-          pb[e / 8][e % 8] = (bf16)pr;
-          db[e / 8][e % 8] = (bf16)ds;
+      for (int st = 0; st < NS; ++st) {
+        const bf16x8 aq = qa[st % PDK], ad = da[st % PDK];
+        if (st + PDK < NS) {
+          qa[st % PDK] = lds_read_b128(qt, aofs[st + PDK] + mrow);
+          da[st % PDK] = lds_read_b128(dt, aofs[st + PDK] + mrow);
         }
+        if (st == 0) {
+          M::mma_v0k(aq, kB[0], sa, prev_a, prev_b);
+          M::mma_v0k(ad, vB[0], dpa, aq, kB[0]);
+        } else {
+          M::mma_v(aq, kB[st], sa, prev_a, prev_b);
+          M::mma_v(ad, vB[st], dpa, aq, kB[st]);
+        }
+        prev_a = ad;
+        prev_b = vB[st];
+        mid(st);
+        // keep mid(st) between these MFMAs and the next step's (the
+        // scheduler otherwise sinks all of it below the chain)
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // dV^T += dO^T P, dK^T += Q^T dS over the tile's rows in two 16-row
-      // steps kk; step kk's B operand (lane group g2) holds rows
-      // 32 mt + 16 kk + 4 g2 + {0..3} and the same + 8, which the A operand
-      // gets from two transposing reads of those 4-row runs.  Operand
-      // i = 8 kk + 2 d + w (w = 0: dO for dV, 1: Q for dK); the reads of
-      // operand i + PD are issued before MFMA i.
+      M::drain_v2(sa, dpa, prev_a, prev_b);
+    };
+    // P and dS of tile t in 8 pieces; piece st covers C-layout elements
+    // e = 4 q + j, q = st / 2, j = 2 (st % 2) + {0, 1} (element e is row
+    // 32 t + 8 (e / 4) + 4 g2 + e % 4).  The lse / δ / mask words of row
+    // group q + 1 are read at piece 2 q, two MFMA steps before their use.
+    f32x4 l4[2], d4[2];
+    u32x4 m4[2];
+    auto pds_load = [&](int t, int q) {
+      const int r0 = 32 * t + 8 * q + 4 * g2;
+      l4[q & 1] = *reinterpret_cast<const f32x4*>(ls + r0);
+      d4[q & 1] = *reinterpret_cast<const f32x4*>(dl + r0);
+      m4[q & 1] = *reinterpret_cast<const u32x4*>(msk + r0);
+    };
+    auto pds = [&](int t, int st, const acc_t& sa, const acc_t& dpa) {
+      const int q = st >> 1;
+      if ((st & 1) == 0 && q + 1 < 4) pds_load(t, q + 1);
+      bf16x2 pp, dd;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * (st & 1) + jj, e = 4 * q + j;
+        // all ones if the pair (row, key n) is selected, else zero
+        const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)m4[q & 1][j], n, 1);
+        const float ex = __builtin_amdgcn_exp2f(fmaf(sa[e], p.scale_log2, -l4[q & 1][j] * kLog2e));
+        const float pr = __uint_as_float(__float_as_uint(ex) & keep);
+        const float ds = pr * (dpa[e] - d4[q & 1][j]);
+        pp[jj] = (bf16)pr;
+        dd[jj] = (bf16)ds;
+      }
+      // materialise the piece here: the empty volatile asm stays between the
+      // surrounding MFMA asm statements, and so does the arithmetic feeding it
+      asm volatile("" : "+v"(pp), "+v"(dd));
+      const int e0 = 4 * q + 2 * (st & 1);
+      pb[e0 / 8][e0 % 8] = pp[0];
+      pb[e0 / 8][e0 % 8 + 1] = pp[1];
+      db[e0 / 8][e0 % 8] = dd[0];
+      db[e0 / 8][e0 % 8 + 1] = dd[1];
+    };
+    // dV^T += dO^T P, dK^T += Q^T dS over tile t's rows in two 16-row steps
+    // kk; step kk's B operand (lane group g2) holds rows 32 t + 16 kk + 4 g2 +
+    // {0..3} and the same + 8, which the A operand gets from two transposing
+    // reads of those 4-row runs.  Operand i = 8 kk + 2 d + w (w = 0: dO for
+    // dV, 1: Q for dK); the reads of operand i + PD are issued before MFMA i.
+    auto dvdk = [&](int t) {
+      const uint32_t mrow = (uint32_t)(32 * t * kCH) * 16u;
       auto load_a = [&](int i) -> bf16x8 {
         const int kk = i / 8, d = (i / 2) % 4, w = i % 2;
         const uint32_t rb = mrow + (uint32_t)(16 * kk * kCH) * 16u;
@@ -370,13 +399,30 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
         if (i + PD < NA) abuf[i % PD] = load_a(i + PD);
         const bf16x8 bop = w ? db[kk] : pb[kk];
         acc_t& acc = w ? dkacc[d] : dvacc[d];
-        if (i % 8 < 2)  // first use of pb[kk] / db[kk], just written by VALU
+        if (i % 8 < 2)  // first use of pb[kk] / db[kk], written by VALU
           M::template mma_agpr<true>(a, bop, acc, prev_a, prev_b);
         else
           M::template mma_agpr<false>(a, bop, acc, prev_a, prev_b);
         prev_a = a;
         prev_b = bop;
       }
+    };
+    sdp(0, sacc[0], dpacc[0], [](int) {});
+#pragma unroll
+    for (int mt = 0; mt < kTiles; ++mt) {
+      const acc_t& sc = sacc[mt & 1];
+      const acc_t& dc = dpacc[mt & 1];
+      pds_load(mt, 0);
+      if (mt + 1 < kTiles) {
+        sdp(mt + 1, sacc[(mt + 1) & 1], dpacc[(mt + 1) & 1], [&](int st) { pds(mt, st, sc, dc); });
+      } else {
+        // no MFMA follows the previous tile's dV/dK chain here: hold its
+        // operands before the VALU may rewrite pb / db
+        M::tail(prev_a, prev_b);
+#pragma unroll
+        for (int st = 0; st < 8; ++st) pds(mt, st, sc, dc);
+      }
+      dvdk(mt);
     }
     M::tail(prev_a, prev_b);
   };
