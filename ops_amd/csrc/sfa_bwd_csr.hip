@@ -208,11 +208,11 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(
       reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + (int64_t)(g * G) * p.do_sh,
       (uint32_t)(2 * ((int64_t)(p.Sq - 1) * p.do_ss + (int64_t)(G - 1) * p.do_sh + kD)));
-  const __amdgpu_buffer_rsrc_t rl = make_rsrc(
-      p.lse + b * p.l_sb + (int64_t)(g * G) * p.l_sh,
-      (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.l_ss + (int64_t)(G - 1) * p.l_sh + 1)));
-  const __amdgpu_buffer_rsrc_t rdl = make_rsrc(
-      p.delta + (int64_t)b * p.Sq * p.Hq + g * G, (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.Hq + G)));
+  // per-row start values of the S and dP accumulators (-lse / scale, -δ)
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  const uint32_t rc_bytes = (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.Hq + G));
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(p.rowc + (int64_t)b * p.Sq * p.Hq + g * G, rc_bytes);
+  const __amdgpu_buffer_rsrc_t rdl = make_rsrc(p.rowc + nrows + (int64_t)b * p.Sq * p.Hq + g * G, rc_bytes);
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(
       p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4,
       (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.kmap_w + 4)));
@@ -244,13 +244,11 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
       const int r = 64 * k2 + lane;
       const int t = t0 + (r >> lg), h = r & (G - 1);
       const bool ok = t < p.Sq;
-      if (wave == 0) {
-        const uint32_t o = ok ? (uint32_t)(4 * (t * p.l_ss + h * p.l_sh)) : kOOB;
+      const uint32_t o = ok ? (uint32_t)(4 * (t * p.Hq + h)) : kOOB;
+      if (wave == 0)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void*)(ls + 64 * k2), 4, o, 0, 0, 0);
-      } else if (wave == 1) {
-        const uint32_t o = ok ? (uint32_t)(4 * (t * p.Hq + h)) : kOOB;
+      else if (wave == 1)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rdl, (lds_void*)(dl + 64 * k2), 4, o, 0, 0, 0);
-      }
       const uint32_t om = ok ? (uint32_t)(4 * (t * p.kmap_w + wave)) : kOOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)(&mk[wave][64 * k2]), 4, om, 0, 0, 0);
     }
@@ -308,6 +306,20 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
     auto sdp = [&](int t, acc_t& sa, acc_t& dpa, auto&& mid) {
       constexpr int NS = kD / 16, PDK = 4;
       const uint32_t mrow = (uint32_t)(32 * t * kCH) * 16u;
+      // start values: S - lse / scale and dP - δ accumulate directly (C-layout
+      // element e is row 32 t + 8 (e / 4) + 4 g2 + e % 4)
+      acc_t s0, d0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r0 = 32 * t + 8 * q + 4 * g2;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + r0);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + r0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s0[4 * q + j] = l4[j];
+          d0[4 * q + j] = d4[j];
+        }
+      }
       bf16x8 qa[PDK], da[PDK];
 #pragma unroll
       for (int i = 0; i < PDK; ++i) {
@@ -322,8 +334,10 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
           da[st % PDK] = lds_read_b128(dt, aofs[st + PDK] + mrow);
         }
         if (st == 0) {
-          M::mma_v0k(aq, kB[0], sa, prev_a, prev_b);
-          M::mma_v0k(ad, vB[0], dpa, aq, kB[0]);
+          sa = s0;
+          dpa = d0;
+          M::mma_vn(aq, kB[0], sa, prev_a, prev_b);
+          M::mma_vn(ad, vB[0], dpa, aq, kB[0]);
         } else {
           M::mma_v(aq, kB[st], sa, prev_a, prev_b);
           M::mma_v(ad, vB[st], dpa, aq, kB[st]);
@@ -338,16 +352,11 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
       M::drain_v2(sa, dpa, prev_a, prev_b);
     };
     // P and dS of tile t in 8 pieces; piece st covers C-layout elements
-    // e = 4 q + j, q = st / 2, j = 2 (st % 2) + {0, 1} (element e is row
-    // 32 t + 8 (e / 4) + 4 g2 + e % 4).  The lse / δ / mask words of row
-    // group q + 1 are read at piece 2 q, two MFMA steps before their use.
-    f32x4 l4[2], d4[2];
+    // e = 4 q + j, q = st / 2, j = 2 (st % 2) + {0, 1}.  The mask words of
+    // row group q + 1 are read at piece 2 q, two MFMA steps before their use.
     u32x4 m4[2];
     auto pds_load = [&](int t, int q) {
-      const int r0 = 32 * t + 8 * q + 4 * g2;
-      l4[q & 1] = *reinterpret_cast<const f32x4*>(ls + r0);
-      d4[q & 1] = *reinterpret_cast<const f32x4*>(dl + r0);
-      m4[q & 1] = *reinterpret_cast<const u32x4*>(msk + r0);
+      m4[q & 1] = *reinterpret_cast<const u32x4*>(msk + 32 * t + 8 * q + 4 * g2);
     };
     auto pds = [&](int t, int st, const acc_t& sa, const acc_t& dpa) {
       const int q = st >> 1;
@@ -358,9 +367,10 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
         const int j = 2 * (st & 1) + jj, e = 4 * q + j;
         // all ones if the pair (row, key n) is selected, else zero
         const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)m4[q & 1][j], n, 1);
-        const float ex = __builtin_amdgcn_exp2f(fmaf(sa[e], p.scale_log2, -l4[q & 1][j] * kLog2e));
+        // sa = S - lse / scale, dpa = dP - δ
+        const float ex = __builtin_amdgcn_exp2f(sa[e] * p.scale_log2);
         const float pr = __uint_as_float(__float_as_uint(ex) & keep);
-        const float ds = pr * (dpa[e] - d4[q & 1][j]);
+        const float ds = pr * dpa[e];
         pp[jj] = (bf16)pr;
         dd[jj] = (bf16)ds;
       }
@@ -524,7 +534,7 @@ size_t csr_workspace_bytes(const Params& p) {
   const size_t bg = (size_t)p.B * p.Hkv;
   return al256(bg * p.Sq * p.kmap_w * 4) + al256((size_t)p.B * p.Sq * p.Hkv * p.topk) +
          al256(bg * p.nkb * p.nqb * 4) + al256(bg * p.nkb * (p.max_chunks + 1) * 4) +
-         al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4);
+         al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4) + al256((size_t)2 * p.B * p.Sq * p.Hq * 4);
 }
 
 void csr_bind_workspace(Params& p, void* ws) {
@@ -539,6 +549,8 @@ void csr_bind_workspace(Params& p, void* ws) {
   p.bstart = reinterpret_cast<int*>(c);
   c += al256(bg * p.nkb * (p.max_chunks + 1) * 4);
   p.dkv_part = reinterpret_cast<float*>(c);
+  c += al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4);
+  p.rowc = reinterpret_cast<float*>(c);
 }
 
 hipError_t launch_csr_index(const Params& p, hipStream_t s) {

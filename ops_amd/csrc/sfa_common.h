@@ -63,6 +63,7 @@ struct Params {
   int* blist;         // [B][Hkv][nkb][nqb] non-empty query blocks of each key block, ascending
   int* bstart;        // [B][Hkv][nkb][max_chunks + 1] blist index of each 128-query-block chunk's first entry
   float* dkv_part;    // [B][Hkv][nkb][max_chunks][128][2 D] fp32 partial dK | dV per chunk
+  float* rowc;        // [2][B*Sq*Hq] per row: -lse / scale, then -δ (written by the δ pass)
   int nkb, nqb;       // key blocks (128 keys), query blocks (128 / G queries)
   int lg_g;           // log2(G)
   int max_chunks;     // chunks per key block (query blocks / chunk, rounded up)
@@ -185,7 +186,7 @@ hipError_t launch_bwd_dq(const Params& p, hipStream_t s);
 bool bwd_csr_supported(const Params& p);
 void csr_geometry(Params& p);                 // fills kmap_w, nkb, nqb, lg_g, max_chunks
 size_t csr_workspace_bytes(const Params& p);  // after csr_geometry
-void csr_bind_workspace(Params& p, void* ws); // carves kmap / dup / blist / bcount / dkv_part
+void csr_bind_workspace(Params& p, void* ws); // carves kmap / dup / blist / bcount / dkv_part / rowc
 hipError_t launch_csr_index(const Params& p, hipStream_t s);  // bitmap, duplicate flags, block lists
 hipError_t launch_csr_dkv(const Params& p, hipStream_t s);    // key-major dK/dV partials + reduction
 // top-k index producer: queries [t_begin, t_end) of every sequence

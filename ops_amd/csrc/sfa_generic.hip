@@ -139,7 +139,14 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(Params p) {
   acc = wave_sum(acc);
   // a gradient flowing into lse adds P·dlse to dS = P(dP - δ): fold it into δ
   if (p.dlse) acc -= p.dlse[b * p.l_sb + t * p.l_ss + h * p.l_sh];
-  if (lane == 0) p.delta[row] = acc;
+  if (lane == 0) {
+    p.delta[row] = acc;
+    // key-major dK/dV: start values of its S and dP accumulators
+    if (p.rowc) {
+      p.rowc[row] = -p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] / p.scale;
+      p.rowc[nrows + row] = -acc;
+    }
+  }
 }
 
 // Shared memory: q row [Dqk] | dout row [Dv] | per-wave dq partial [kWaves][Dqk]

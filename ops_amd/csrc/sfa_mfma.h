@@ -45,6 +45,11 @@ struct Mfma<32> {
     asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"
                  : "=&v"(c) : "v"(a), "v"(b) : "memory");
   }
+  // c += a b where c may just have been written by a VALU instruction
+  static __device__ __forceinline__ void mma_vn(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                 : "+v"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+  }
   // c = a b (fresh VGPR accumulator) with the previous MFMA's operands kept alive
   static __device__ __forceinline__ void mma_v0k(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa,
                                                  const bf16x8& pb) {
