@@ -160,14 +160,20 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
   // the 8 XCDs round-robin; when the key-block count allows, XCD x gets the
   // key blocks kb = x (mod 8) in chunk-major order, so the workgroups that run
   // together on one XCD share query blocks (its L2 serves them once loaded).
-  const int per_bg = p.nkb * p.max_chunks;
-  const int bg = blockIdx.x / per_bg, l = blockIdx.x % per_bg;
-  int kb, c;
+  // Within an XCD the order is chunk-descending across all (b, g): the long
+  // workgroups (late chunks see the most key blocks) start first, the short
+  // diagonal ones fill the tail.
+  const int nbg = p.B * p.Hkv;
+  int bg, kb, c;
   if (p.nkb % 8 == 0) {
-    const int x = l % 8, r = l / 8;
-    kb = x + 8 * (r % (p.nkb / 8));
-    c = r / (p.nkb / 8);
+    const int x = blockIdx.x % 8, r = blockIdx.x / 8, per = p.nkb / 8;
+    kb = x + 8 * (r % per);
+    bg = (r / per) % nbg;
+    c = p.max_chunks - 1 - r / (per * nbg);
   } else {
+    const int per_bg = p.nkb * p.max_chunks;
+    bg = blockIdx.x / per_bg;
+    const int l = blockIdx.x % per_bg;
     kb = l / p.max_chunks;
     c = l % p.max_chunks;
   }
