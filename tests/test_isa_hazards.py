@@ -1,0 +1,96 @@
+"""Static check of the gfx950 assembly of every kernel: no VALU instruction
+may write a register that an MFMA reads as srcA / srcB / srcC fewer than two
+wait states before that MFMA.
+
+The MFMA kernels issue their MFMAs as inline asm (to pin accumulators to
+AGPRs or VGPRs and to order operand loads), and the compiler's hazard
+recognizer does not see inside inline asm, so it inserts no wait states for
+them.  The kernels provide the wait states themselves (``s_nop`` before an
+MFMA whose operand a VALU instruction may just have written); this test
+catches code where the compiler placed a copy or a spill reload of an
+operand right in front of an MFMA (as happens when register pressure makes
+it move values between the VGPR and AGPR files).  CPU only: the assembly
+comes from hipcc's device-only compile (no GPU needed)."""
+import os
+import re
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import pytest
+
+from ops_amd import build as sfa_build
+
+HIPCC = sfa_build.hipcc()
+pytestmark = pytest.mark.skipif(shutil.which(HIPCC) is None and not os.path.exists(HIPCC),
+                                reason="hipcc not available")
+
+LOOKBACK = 5  # instructions examined before each MFMA
+
+
+def _regs(spec):
+    out = set()
+    for m in re.finditer(r"([va])\[(\d+):(\d+)\]|([va])(\d+)\b", spec):
+        if m.group(1):
+            out |= {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+        else:
+            out.add((m.group(4), int(m.group(5))))
+    return out
+
+
+def scan(asm: str):
+    """[(kernel, mfma line, offending VALU line)] for every short RAW gap."""
+    found = []
+    for fm in re.finditer(r"^(_Z\S+):", asm, re.M):
+        end = asm.find(".Lfunc_end", fm.end())
+        body = [l.strip() for l in asm[fm.end():end].split("\n")
+                if l.startswith("\t") and not l.startswith("\t;") and not l.startswith("\t.")]
+        for i, ins in enumerate(body):
+            if "v_mfma" not in ins:
+                continue
+            ops = ins.split(None, 1)[1].split(",")
+            srcs = set().union(*[_regs(o) for o in ops[1:4]])
+            waits = 0
+            for j in range(i - 1, max(i - 1 - LOOKBACK, -1), -1):
+                prev = body[j]
+                if prev.startswith("s_nop"):
+                    waits += int(prev.split()[1]) + 1
+                    continue
+                if prev.startswith("v_") and "mfma" not in prev and waits < 2:
+                    dst = _regs(prev.split(None, 1)[1].split(",")[0])
+                    if dst & srcs:
+                        found.append((fm.group(1), ins, prev))
+                waits += 1
+    return found
+
+
+def _device_asm(src: Path, out_dir: Path) -> str:
+    out = out_dir / (src.stem + ".s")
+    cmd = [HIPCC, *[f for f in sfa_build.HIPCC_FLAGS if f not in ("-shared", "-fPIC")], "--cuda-device-only",
+           "-S", "-I", str(sfa_build.HERE.parent / "include"), str(src), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    return out.read_text()
+
+
+def test_scanner_flags_a_planted_hazard():
+    # the scanner itself: a VALU write of an MFMA operand right before it is
+    # reported, the same with two wait states of s_nop is not
+    asm = ("_Zplanted:\n\tv_mov_b32_e32 v8, 0\n\tv_mfma_f32_32x32x16_bf16 v[0:15], v[8:11], a[0:3], v[0:15]\n"
+           "\tv_mov_b32_e32 v9, 0\n\ts_nop 1\n\tv_mfma_f32_32x32x16_bf16 v[0:15], v[8:11], a[0:3], v[0:15]\n"
+           "\tv_accvgpr_write_b32 a2, v1\n\tv_mfma_f32_32x32x16_bf16 v[0:15], v[8:11], a[0:3], v[0:15]\n"
+           ".Lfunc_end0:\n")
+    hits = scan(asm)
+    assert [h[2] for h in hits] == ["v_mov_b32_e32 v8, 0", "v_accvgpr_write_b32 a2, v1"]
+
+
+def test_no_valu_to_mfma_operand_hazards(tmp_path):
+    sources = sfa_build.sources()
+    assert sources
+    with ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
+        asms = list(ex.map(lambda s: _device_asm(Path(s), tmp_path), sources))
+    n_mfma = sum(a.count("v_mfma") for a in asms)
+    assert n_mfma > 500, "expected the MFMA kernels in the sources"
+    hits = [h for a in asms for h in scan(a)]
+    assert not hits, "VALU write of an MFMA operand without 2 wait states:\n" + "\n".join(
+        f"{k[-60:]}: {v}  ->  {m}" for k, m, v in hits[:10])
