@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
     const uint32_t* msk = mk[wave];
     bf16x8 prev_a = {}, prev_b = {};
     acc_t sacc[2], dpacc[2];
-    bf16x8 pb[2], db[2];
+    bf16x8 pb[2][2], db[2][2];  // [tile == last][16-row step]
     // S, dP for rows 32 t .. +31 into (sa, dpa): two interleaved VGPR chains
     // (inline-asm MFMAs, so the operand reads of step st + PDK stay ahead of
     // the MFMAs of step st); mid(st) runs after step st's two MFMAs.
@@ -365,6 +365,7 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
       m4[q & 1] = *reinterpret_cast<const u32x4*>(msk + 32 * t + 8 * q + 4 * g2);
     };
     auto pds = [&](int t, int st, const acc_t& sa, const acc_t& dpa) {
+      const int set = t == kTiles - 1;
       const int q = st >> 1;
       if ((st & 1) == 0 && q + 1 < 4) pds_load(t, q + 1);
       bf16x2 pp, dd;
@@ -384,17 +385,19 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
       // surrounding MFMA asm statements, and so does the arithmetic feeding it
       asm volatile("" : "+v"(pp), "+v"(dd));
       const int e0 = 4 * q + 2 * (st & 1);
-      pb[e0 / 8][e0 % 8] = pp[0];
-      pb[e0 / 8][e0 % 8 + 1] = pp[1];
-      db[e0 / 8][e0 % 8] = dd[0];
-      db[e0 / 8][e0 % 8 + 1] = dd[1];
+      pb[set][e0 / 8][e0 % 8] = pp[0];
+      pb[set][e0 / 8][e0 % 8 + 1] = pp[1];
+      db[set][e0 / 8][e0 % 8] = dd[0];
+      db[set][e0 / 8][e0 % 8 + 1] = dd[1];
     };
     // dV^T += dO^T P, dK^T += Q^T dS over tile t's rows in two 16-row steps
     // kk; step kk's B operand (lane group g2) holds rows 32 t + 16 kk + 4 g2 +
     // {0..3} and the same + 8, which the A operand gets from two transposing
     // reads of those 4-row runs.  Operand i = 8 kk + 2 d + w (w = 0: dO for
     // dV, 1: Q for dK); the reads of operand i + PD are issued before MFMA i.
-    auto dvdk = [&](int t) {
+    // mid(i) runs after MFMA i.
+    auto dvdk = [&](int t, auto&& mid) {
+      const int set = t == kTiles - 1;
       const uint32_t mrow = (uint32_t)(32 * t * kCH) * 16u;
       auto load_a = [&](int i) -> bf16x8 {
         const int kk = i / 8, d = (i / 2) % 4, w = i % 2;
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
         const int kk = i / 8, d = (i / 2) % 4, w = i % 2;
         const bf16x8 a = abuf[i % PD];
         if (i + PD < NA) abuf[i % PD] = load_a(i + PD);
-        const bf16x8 bop = w ? db[kk] : pb[kk];
+        const bf16x8 bop = w ? db[set][kk] : pb[set][kk];
         acc_t& acc = w ? dkacc[d] : dvacc[d];
         if (i % 8 < 2)  // first use of pb[kk] / db[kk], written by VALU
           M::template mma_agpr<true>(a, bop, acc, prev_a, prev_b);
@@ -421,6 +424,7 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
           M::template mma_agpr<false>(a, bop, acc, prev_a, prev_b);
         prev_a = a;
         prev_b = bop;
+        mid(i);
       }
     };
     sdp(0, sacc[0], dpacc[0], [](int) {});
@@ -428,17 +432,25 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
     for (int mt = 0; mt < kTiles; ++mt) {
       const acc_t& sc = sacc[mt & 1];
       const acc_t& dc = dpacc[mt & 1];
-      pds_load(mt, 0);
       if (mt + 1 < kTiles) {
+        pds_load(mt, 0);
         sdp(mt + 1, sacc[(mt + 1) & 1], dpacc[(mt + 1) & 1], [&](int st) { pds(mt, st, sc, dc); });
-      } else {
-        // no MFMA follows the previous tile's dV/dK chain here: hold its
-        // operands before the VALU may rewrite pb / db
-        M::tail(prev_a, prev_b);
-#pragma unroll
-        for (int st = 0; st < 8; ++st) pds(mt, st, sc, dc);
       }
-      dvdk(mt);
+      if (mt + 2 == kTiles) {
+        // no S/dP chain follows: the last tile's P/dS pieces run between this
+        // tile's dV/dK MFMAs instead, into their own P/dS operand set
+        const acc_t& sn = sacc[(mt + 1) & 1];
+        const acc_t& dn = dpacc[(mt + 1) & 1];
+        pds_load(mt + 1, 0);
+        dvdk(mt, [&](int i) {
+          if (i & 1) {
+            pds(mt + 1, i / 2, sn, dn);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        });
+      } else {
+        dvdk(mt, [](int) {});
+      }
     }
     M::tail(prev_a, prev_b);
   };
