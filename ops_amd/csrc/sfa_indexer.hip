@@ -361,14 +361,39 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
       __syncthreads();
       if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-#pragma unroll 1
-        for (int bit = 15; bit >= 0; --bit) {
-          const uint32_t cand = thr | (1u << bit);
-          int c = 0;
-          for (int i = lane; i < inplay_total; i += 64) c += s_c[i] >= cand ? 1 : 0;
+        // up to 64 R in-play keys in registers (absent: 0, below every
+        // candidate), counted with ballots like the block steps
+        auto finish_regs = [&](auto r_tag) {
+          constexpr int R = decltype(r_tag)::value;
+          uint32_t kv[R];
 #pragma unroll
-          for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-          if (above_total + c >= K) thr = cand;
+          for (int i = 0; i < R; ++i) {
+            const int j = lane + 64 * i;
+            kv[i] = j < inplay_total ? s_c[j] : 0u;
+          }
+#pragma unroll 1
+          for (int bit = 15; bit >= 0; --bit) {
+            const uint32_t cand = thr | (1u << bit);
+            int c = 0;
+#pragma unroll
+            for (int i = 0; i < R; ++i) c += __popcll(__ballot(kv[i] >= cand));
+            if (above_total + c >= K) thr = cand;
+          }
+        };
+        if (inplay_total <= 64 * 4) {
+          finish_regs(std::integral_constant<int, 4>());
+        } else if (inplay_total <= 64 * 16) {
+          finish_regs(std::integral_constant<int, 16>());
+        } else {
+#pragma unroll 1
+          for (int bit = 15; bit >= 0; --bit) {
+            const uint32_t cand = thr | (1u << bit);
+            int c = 0;
+            for (int i = lane; i < inplay_total; i += 64) c += s_c[i] >= cand ? 1 : 0;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+            if (above_total + c >= K) thr = cand;
+          }
         }
         if (lane == 0) red[80] = (int)thr;
       }
