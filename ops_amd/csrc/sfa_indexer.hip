@@ -309,7 +309,7 @@ __device__ __forceinline__ int block_exscan(int x, int* red, int* total) {
 // Selection over one row of n > K scores held as NG groups of 4 per thread
 // (thread tid owns keys [4 NG tid, 4 NG tid + 4 NG)); NG is fixed per
 // instantiation, so the bisection steps are straight-line code.
-template <int NG>
+template <int NG, int MAXR>
 __device__ __forceinline__ void select_row(const float* row, int n, int K, int32_t* out, int* red, uint32_t* s_c) {
   constexpr int EPT = 4 * NG;
   const int tid = threadIdx.x;
@@ -382,8 +382,8 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
         };
         if (inplay_total <= 64 * 4) {
           finish_regs(std::integral_constant<int, 4>());
-        } else if (inplay_total <= 64 * 16) {
-          finish_regs(std::integral_constant<int, 16>());
+        } else if (inplay_total <= 64 * MAXR) {
+          finish_regs(std::integral_constant<int, MAXR>());
         } else {
 #pragma unroll 1
           for (int bit = 15; bit >= 0; --bit) {
@@ -425,7 +425,14 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
   }
 }
 
-__global__ __launch_bounds__(kSelThreads, 1) void topk_select_kernel(IndexerParams p, int t_begin, int t_end) {
+// MAXNG: the largest row this instance takes is 4 MAXNG kSelThreads scores.
+// Rows of up to 32768 scores fit 64 VGPRs: two workgroups per CU, so one
+// workgroup's barrier waits overlap the other's counting.
+template <int MAXNG>
+// (second bound: minimum waves per SIMD; 8 = two 16-wave workgroups per CU)
+__global__ __launch_bounds__(kSelThreads, MAXNG <= 8 ? 8 : 1) void topk_select_kernel(IndexerParams p, int t_begin,
+                                                                                     int t_end) {
+  constexpr int MAXR = MAXNG <= 8 ? 8 : 16;  // in-play keys per lane of the register finish
   __shared__ int red[96];
   __shared__ uint32_t s_c[kCompact];
   const int nt = t_end - t_begin;
@@ -444,15 +451,15 @@ __global__ __launch_bounds__(kSelThreads, 1) void topk_select_kernel(IndexerPara
   // groups of 4 scores per thread: the smallest power of two that holds n
   const int ng = (n + 4 * kSelThreads - 1) / (4 * kSelThreads);
   if (ng <= 1)
-    select_row<1>(row, n, K, out, red, s_c);
+    select_row<1, MAXR>(row, n, K, out, red, s_c);
   else if (ng <= 2)
-    select_row<2>(row, n, K, out, red, s_c);
+    select_row<2, MAXR>(row, n, K, out, red, s_c);
   else if (ng <= 4)
-    select_row<4>(row, n, K, out, red, s_c);
-  else if (ng <= 8)
-    select_row<8>(row, n, K, out, red, s_c);
-  else
-    select_row<16>(row, n, K, out, red, s_c);
+    select_row<4, MAXR>(row, n, K, out, red, s_c);
+  else if (MAXNG <= 8 || ng <= 8)
+    select_row<8, MAXR>(row, n, K, out, red, s_c);
+  else if constexpr (MAXNG > 8)
+    select_row<16, MAXR>(row, n, K, out, red, s_c);
 }
 
 }  // namespace
@@ -489,7 +496,11 @@ hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end,
 hipError_t launch_topk_select(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
   const int64_t n = (int64_t)p.B * (t_end - t_begin);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(topk_select_kernel, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);
+  // a row holds at most Skv scores
+  if (p.Skv <= 4 * 8 * kSelThreads)
+    hipLaunchKernelGGL(topk_select_kernel<8>, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);
+  else
+    hipLaunchKernelGGL(topk_select_kernel<16>, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);
   return hipGetLastError();
 }
 
