@@ -20,6 +20,8 @@ measured in the same run and reported under ``workloads``:
                   over the visible (query, key) pairs, 2 H d FLOP each);
                   ``layer_ms``: indexer + MLA forward on the indices it produced
                   (the whole sparse attention layer of the prefill)
+* ``mla_bwd``     shared-KV (MLA) backward at S=1024 (128 heads, d_qk 576 / d_v
+                  512, top-k 2048; TFLOP/s over valid pairs): generic kernels
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -228,6 +230,25 @@ def bench_mla_decode(args):
     return res
 
 
+def bench_mla_bwd(args):
+    """Shared-KV (MLA) backward, d_qk 576 / d_v 512, 128 heads, top-k 2048,
+    at S = 1024: it runs on the generic kernels (no MLA-specific backward
+    yet), whose rate makes the full S = 32768 step take ~28 s."""
+    import torch
+    import ops_amd
+    from ops_amd.workloads import make_workload
+    S = 1024
+    w = make_workload("mla_prefill", device="cuda", S=S, with_dout=True)
+    pairs = valid_pairs(w)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+    bt, _ = time_steps(lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale), 2, 1)
+    ms = sum(bt) / len(bt)
+    tf = bwd_flops(w, pairs) / (ms * 1e-3) / 1e12
+    return {"metric": "bwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
+            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "generic",
+            "config": {"B": 1, "S": S, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
+
+
 def bench_indexer(args, mla=None):
     import torch
     import ops_amd
@@ -276,7 +297,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--extra", default="prefill,train_gqa,mla_decode,indexer",
+    ap.add_argument("--extra", default="prefill,train_gqa,mla_decode,indexer,mla_bwd",
                     help="comma list of additional workloads to measure ('' for none)")
     ap.add_argument("--no-bwd", action="store_true", help="skip the train_gqa backward timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -310,7 +331,7 @@ def main():
             extra[name] = bench_indexer(args, w)
         else:
             extra[name] = {"prefill": bench_prefill, "train_gqa": bench_train_gqa,
-                           "mla_decode": bench_mla_decode}[name](args)
+                           "mla_decode": bench_mla_decode, "mla_bwd": bench_mla_bwd}[name](args)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
