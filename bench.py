@@ -308,7 +308,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sparse attention path runs on a single MI355X "
-              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+              "(multi-GPU sharding is described as a design only, not implemented)", file=sys.stderr)
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "no GPU"

@@ -1,6 +1,7 @@
 """CPU restatement of top-k sparse flash attention (SFA) — test infrastructure only.
 
-This module is the checker for the HIP kernels in ``ops_amd``: only ``tests/``,
+This module is the reference the HIP kernels in ``ops_amd`` are compared
+against: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import
 it, and never as the thing measured or shipped.  The product path
 (``ops_amd.sfa``) never calls into it.
