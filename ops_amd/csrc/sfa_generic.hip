@@ -149,6 +149,41 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(Params p) {
   }
 }
 
+// The same for bf16 rows of DV in {128, 256, 512} elements with 16-byte
+// aligned rows: DV / 8 lanes per row, one 16-byte load of O and of dO each.
+template <int DV>
+__global__ __launch_bounds__(kThreads) void delta_vec_kernel(Params p) {
+  constexpr int LPR = DV / 8;    // lanes per row
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  static_assert(LPR * RPW == 64, "DV / 8 divides the wave");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * RPW + lane / LPR;
+  const bool live = row < nrows;
+  const int h = live ? (int)(row % p.Hq) : 0;
+  const int t = live ? (int)((row / p.Hq) % p.Sq) : 0;
+  const int b = live ? (int)(row / ((int64_t)p.Hq * p.Sq)) : 0;
+  float acc = 0.f;
+  if (live) {
+    const int c = 8 * (lane % LPR);
+    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.out) + b * p.o_sb +
+                                                       t * p.o_ss + h * p.o_sh + c);
+    const bf16x8 dv = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb +
+                                                       t * p.do_ss + h * p.do_sh + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += (float)ov[j] * (float)dv[j];
+  }
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (!live || lane % LPR != 0) return;
+  if (p.dlse) acc -= p.dlse[b * p.l_sb + t * p.l_ss + h * p.l_sh];
+  p.delta[row] = acc;
+  if (p.rowc) {
+    p.rowc[row] = -p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] / p.scale;
+    p.rowc[nrows + row] = -acc;
+  }
+}
+
 // Shared memory: q row [Dqk] | dout row [Dv] | per-wave dq partial [kWaves][Dqk]
 template <typename T>
 __global__ __launch_bounds__(kThreads) void bwd_generic_kernel(Params p) {
@@ -314,6 +349,21 @@ hipError_t launch_fwd_generic(const Params& p, int dtype, hipStream_t s) {
 hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.Sq * p.Hq;
   const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  auto al16 = [](const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; };
+  const bool vec = dtype == SFA_DTYPE_BF16 && (p.Dv == 128 || p.Dv == 256 || p.Dv == 512) && al16(p.out) &&
+                   al16(p.dout) && p.o_sb % 8 == 0 && p.o_ss % 8 == 0 && p.o_sh % 8 == 0 && p.do_sb % 8 == 0 &&
+                   p.do_ss % 8 == 0 && p.do_sh % 8 == 0;
+  if (vec) {
+    const int rpw = 64 / (p.Dv / 8);
+    const dim3 vgrid((unsigned)((rows + (int64_t)kWaves * rpw - 1) / ((int64_t)kWaves * rpw)));
+    if (p.Dv == 128)
+      hipLaunchKernelGGL(delta_vec_kernel<128>, vgrid, dim3(kThreads), 0, s, p);
+    else if (p.Dv == 256)
+      hipLaunchKernelGGL(delta_vec_kernel<256>, vgrid, dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(delta_vec_kernel<512>, vgrid, dim3(kThreads), 0, s, p);
+    return hipGetLastError();
+  }
   if (dtype == SFA_DTYPE_F32)
     hipLaunchKernelGGL(delta_kernel<float>, grid, dim3(kThreads), 0, s, p);
   else
