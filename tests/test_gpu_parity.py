@@ -163,10 +163,12 @@ def test_train_gqa_bwd_full():
         assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
 
 
-def test_generic_bf16_bwd_large_group():
-    """G = 32 has no MFMA backward variant: the generic bf16 kernels run."""
-    _say("bf16 bwd G=32 d=64 (generic kernels)")
-    w = make_workload("train_gqa", device=DEV, S=256, K=64, Hq=64, Hkv=2, Dqk=64, Dv=64)
+@pytest.mark.parametrize("D", [64, 256])
+def test_generic_bf16_bwd_large_group(D):
+    """G = 32 has no MFMA backward variant: the generic bf16 kernels run
+    (d = 64: the per-element δ kernel; d = 256: the 16-byte δ kernel)."""
+    _say(f"bf16 bwd G=32 d={D} (generic kernels)")
+    w = make_workload("train_gqa", device=DEV, S=256, K=64, Hq=64, Hkv=2, Dqk=D, Dv=D)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     q, k, v, idx, _ = _cpu(w)
     o_ref, l_ref = ref_forward(q, k, v, idx, w.scale)
