@@ -133,6 +133,42 @@ __global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
   if (tid == 0) start[p.max_chunks] = total;
 }
 
+// The same per index row, one wave per row (4 rows per workgroup, no block
+// barrier): for bitmap rows of at most kWaveMapWords words.  A wave's LDS
+// operations complete in program order, so its zeroing, its atomics and its
+// final reads need no barrier between them.
+constexpr int kWaveMapWords = 1024;  // Skv <= 32768
+__global__ __launch_bounds__(256) void csr_scatter_wave_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_map[4][kWaveMapWords];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hkv;
+  const int64_t wi = (int64_t)blockIdx.x * 4 + wave;
+  if (wi >= nrows) return;  // the whole wave
+  const int g = (int)(wi % p.Hkv);
+  const int t = (int)((wi / p.Hkv) % p.Sq);
+  const int b = (int)(wi / ((int64_t)p.Hkv * p.Sq));
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  uint32_t* mrow = p.kmap + (((int64_t)b * p.Hkv + g) * p.Sq + t) * p.kmap_w;
+  uint8_t* drow = p.dup + (((int64_t)b * p.Sq + t) * p.Hkv + g) * p.topk;
+  const int bound = bound_of(p, b);
+  uint32_t* map = s_map[wave];
+  for (int w = lane; w < p.kmap_w; w += 64) map[w] = 0u;
+  __builtin_amdgcn_wave_barrier();
+  for (int s = lane; s < p.topk; s += 64) {
+    const int id = irow[s];
+    uint8_t rep = 0;
+    if (id >= 0 && id < bound) {
+      const uint32_t bit = 1u << (id & 31);
+      rep = (atomicOr(&map[id >> 5], bit) & bit) ? 1 : 0;
+    }
+    drow[s] = rep;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // kmap_w is a multiple of 4: 16-byte stores
+  for (int w = 4 * lane; w < p.kmap_w; w += 256)
+    *reinterpret_cast<u32x4*>(mrow + w) = *reinterpret_cast<const u32x4*>(map + w);
+}
+
 // ---- 2. key-major dK / dV ---------------------------------------------------
 // LDS: Q and dO blocks double buffered (row r = query (r >> lg_g), head
 // (r & (G - 1)); swizzled, see blk_swz), each row's lse and δ, and per wave the
@@ -572,7 +608,11 @@ void csr_bind_workspace(Params& p, void* ws) {
 }
 
 hipError_t launch_csr_index(const Params& p, hipStream_t s) {
-  hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)((int64_t)p.B * p.Sq * p.Hkv)), dim3(256), 0, s, p);
+  const int64_t rows = (int64_t)p.B * p.Sq * p.Hkv;
+  if (p.kmap_w <= kWaveMapWords)
+    hipLaunchKernelGGL(csr_scatter_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)rows), dim3(256), 0, s, p);
   hipLaunchKernelGGL(csr_blocklist_kernel, dim3((unsigned)((int64_t)p.B * p.Hkv * p.nkb)), dim3(256), 0, s, p);
   return hipGetLastError();
 }

@@ -91,6 +91,15 @@ def test_csr_noncausal_rectangular_kvlens_sink():
     _check_vs_oracle(q, k, v, do, idx, res, kv_lens=kv_lens, sink=sink)
 
 
+def test_csr_long_key_range():
+    """Skv = 40000: bitmap rows of 1252 words, above the one-wave-per-row
+    scatter's 1024 (the per-row block scatter runs), non-causal indices
+    with repeats."""
+    _say("csr bwd non-causal Sq=64 Skv=40000 G=8 K=128 repeats")
+    q, k, v, do, idx = _inputs(1, 64, 40000, 16, 2, 128, seed=21, causal=False, repeats=0.05)
+    _check_vs_oracle(q, k, v, do, idx, _run(q, k, v, do, idx, "csr"))
+
+
 def test_csr_repeated_keys():
     """Rows that select the same key more than once: each slot is its own
     term (the oracle's semantics); repeats take the atomic side path."""
