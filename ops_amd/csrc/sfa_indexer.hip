@@ -306,6 +306,18 @@ __device__ __forceinline__ int block_exscan(int x, int* red, int* total) {
   return base + inc - x;
 }
 
+// Two exclusive scans at once: (hi, lo) packed as hi 2^16 + lo, valid when
+// both block totals stay below 2^16 (rows of at most 32768 scores).
+__device__ __forceinline__ void block_exscan2(int hi, int lo, int* red, int* hi_base, int* lo_base, int* hi_total,
+                                              int* lo_total) {
+  int tot;
+  const int base = block_exscan((hi << 16) | lo, red, &tot);
+  *hi_base = base >> 16;
+  *lo_base = base & 0xFFFF;
+  *hi_total = tot >> 16;
+  *lo_total = tot & 0xFFFF;
+}
+
 // Selection over one row of n > K scores held as NG groups of 4 per thread
 // (thread tid owns keys [4 NG tid, 4 NG tid + 4 NG)); NG is fixed per
 // instantiation, so the bisection steps are straight-line code.
@@ -351,9 +363,14 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
       above += (u[e] >> 16) > top ? 1 : 0;
       inplay += (u[e] >> 16) == top ? 1 : 0;
     }
-    int above_total, inplay_total;
-    (void)block_exscan(above, red + 32, &above_total);
-    int w = block_exscan(inplay, red, &inplay_total);
+    int above_total, inplay_total, w;
+    if constexpr (NG <= 8) {
+      int above_base;
+      block_exscan2(above, inplay, red, &above_base, &w, &above_total, &inplay_total);
+    } else {
+      (void)block_exscan(above, red + 32, &above_total);
+      w = block_exscan(inplay, red, &inplay_total);
+    }
     if (inplay_total <= kCompact) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e)
@@ -410,9 +427,14 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
     gt += (u[e] > thr) ? 1 : 0;
     eq += (u[e] == thr) ? 1 : 0;
   }
-  int gt_total, eq_total, sel_total;
-  (void)block_exscan(gt, red + 32, &gt_total);  // (only the total is used)
-  const int eq_before = block_exscan(eq, red, &eq_total);
+  int gt_total, eq_total, sel_total, eq_before;
+  if constexpr (NG <= 8) {
+    int gt_base;  // (only the total is used)
+    block_exscan2(gt, eq, red, &gt_base, &eq_before, &gt_total, &eq_total);
+  } else {
+    (void)block_exscan(gt, red + 32, &gt_total);  // (only the total is used)
+    eq_before = block_exscan(eq, red, &eq_total);
+  }
   const int take = K - gt_total;  // >= 1 ties are selected
   const int my_eq = min(max(take - eq_before, 0), eq);
   int w = block_exscan(gt + my_eq, red + 32, &sel_total);
