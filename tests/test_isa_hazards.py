@@ -9,8 +9,11 @@ them.  The kernels provide the wait states themselves (``s_nop`` before an
 MFMA whose operand a VALU instruction may just have written); this test
 catches code where the compiler placed a copy or a spill reload of an
 operand right in front of an MFMA (as happens when register pressure makes
-it move values between the VGPR and AGPR files).  CPU only: the assembly
-comes from hipcc's device-only compile (no GPU needed)."""
+it move values between the VGPR and AGPR files).  A second check covers the
+other direction in the kernels whose MFMAs are inline asm: no instruction
+may read a VGPR an MFMA wrote before the kernel's explicit drain (18 wait
+states) has passed.  CPU only: the assembly comes from hipcc's device-only
+compile (no GPU needed)."""
 import os
 import re
 import shutil
@@ -65,6 +68,50 @@ def scan(asm: str):
     return found
 
 
+# Kernels whose MFMAs are inline asm (the compiler inserts no wait states for
+# them); kernels built on the MFMA builtins get theirs from the compiler.
+INLINE_ASM_MFMA_KERNELS = ("dkv_keymajor_kernel", "fwd_mfma_kernel")
+DRAIN = 18  # wait states the inline-asm drains provide after an MFMA before VALU reads
+
+
+def scan_result_reads(asm: str, kernels=INLINE_ASM_MFMA_KERNELS):
+    """[(kernel, mfma, reader)] where an instruction reads a VGPR an MFMA
+    wrote fewer than DRAIN wait states later (1 per instruction, N + 1 per
+    s_nop N; the scan stops at a branch, a label, or an MFMA that writes the
+    same registers)."""
+    found = []
+    for fm in re.finditer(r"^(_Z\S+):", asm, re.M):
+        if not any(k in fm.group(1) for k in kernels):
+            continue
+        end = asm.find(".Lfunc_end", fm.end())
+        body = [l.strip() for l in asm[fm.end():end].split("\n")
+                if (l.startswith("\t") and not l.startswith("\t;") and not l.startswith("\t.")) or l.startswith(".LBB")]
+        for i, ins in enumerate(body):
+            if "v_mfma" not in ins:
+                continue
+            dst = {r for r in _regs(ins.split(None, 1)[1].split(",")[0]) if r[0] == "v"}
+            if not dst:
+                continue
+            waits = 0
+            for nxt in body[i + 1:i + 64]:
+                if nxt.startswith(".LBB") or nxt.startswith(("s_cbranch", "s_branch", "s_endpgm")) or waits >= DRAIN:
+                    break
+                if nxt.startswith("s_nop"):
+                    waits += int(nxt.split()[1]) + 1
+                    continue
+                parts = nxt.split(None, 1)
+                if "v_mfma" in nxt and _regs(parts[1].split(",")[0]) & dst:
+                    break
+                if len(parts) > 1 and nxt.startswith(("v_", "ds_", "global_", "buffer_")) and "v_mfma" not in nxt:
+                    ops = parts[1].split(",")
+                    stores = nxt.startswith(("ds_write", "global_store", "buffer_store"))
+                    reads = set().union(*[_regs(o) for o in (ops if stores else ops[1:])])
+                    if reads & dst:
+                        found.append((fm.group(1), ins, nxt))
+                waits += 1
+    return found
+
+
 def _device_asm(src: Path, out_dir: Path) -> str:
     out = out_dir / (src.stem + ".s")
     cmd = [HIPCC, *[f for f in sfa_build.HIPCC_FLAGS if f not in ("-shared", "-fPIC")], "--cuda-device-only",
@@ -94,3 +141,22 @@ def test_no_valu_to_mfma_operand_hazards(tmp_path):
     hits = [h for a in asms for h in scan(a)]
     assert not hits, "VALU write of an MFMA operand without 2 wait states:\n" + "\n".join(
         f"{k[-60:]}: {v}  ->  {m}" for k, m, v in hits[:10])
+
+
+def test_result_scanner_flags_a_planted_early_read():
+    asm = ("_Zdkv_keymajor_kernel_planted:\n\tv_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], a[0:3], v[0:15]\n"
+           "\tv_add_f32_e32 v20, v3, v3\n"
+           "\tv_mfma_f32_32x32x16_bf16 v[32:47], v[16:19], a[0:3], v[32:47]\n"
+           "\ts_nop 7\n\ts_nop 7\n\ts_nop 3\n\tv_add_f32_e32 v20, v33, v33\n.Lfunc_end0:\n")
+    hits = scan_result_reads(asm)
+    assert [h[2] for h in hits] == ["v_add_f32_e32 v20, v3, v3"]
+
+
+def test_no_early_reads_of_inline_asm_mfma_results(tmp_path):
+    srcs = [s for s in sfa_build.sources() if Path(s).stem in ("sfa_bwd_csr", "sfa_fwd_mfma")]
+    assert len(srcs) == 2
+    asms = [_device_asm(Path(s), tmp_path) for s in srcs]
+    assert sum(a.count("v_mfma") for a in asms) > 300
+    hits = [h for a in asms for h in scan_result_reads(a)]
+    assert not hits, "VGPR MFMA result read before the drain:\n" + "\n".join(
+        f"{k[-60:]}: {m}  ->  {r}" for k, m, r in hits[:10])
