@@ -57,12 +57,17 @@ enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1, SFA_DTYPE_FP8_E4M3 = 2 };
 /* How the backward produces dK/dV. */
 enum {
   SFA_DKV_AUTO = 0,    /* CSR where supported (bf16, d_qk = d_v = 128, G a power of two
-                          <= 16, top-k <= 2048, Skv <= 262144), otherwise ATOMIC       */
+                          <= 16, top-k <= 2048, Skv <= 262144) and cheaper: Skv <=
+                          64 * top-k and CSR workspace (bitmap, lists, fp32 partials,
+                          which grow as Skv * Sq * G / 16 bytes per batch and kv head)
+                          <= 4 GiB; otherwise ATOMIC                                   */
   SFA_DKV_ATOMIC = 1,  /* fp32 atomic adds into a workspace accumulator (SFA.py:853)    */
   SFA_DKV_CSR = 2      /* deterministic: membership bitmap inverted into per-key-block
                           lists of referencing query blocks, key-major recompute, fixed-
                           order reduction (index rows that repeat a key take atomics for
-                          the repeats); SFA_E_UNSUPPORTED outside the AUTO conditions   */
+                          the repeats); SFA_E_UNSUPPORTED outside the supported shapes
+                          (the cost rules of AUTO do not apply).  dsink is reduced in a
+                          fixed order in every mode                                     */
 };
 
 /* Error codes. */

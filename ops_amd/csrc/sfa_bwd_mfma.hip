@@ -103,8 +103,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
   const bool live = hvalid && lse != kNegInf;
   const float lse2 = live ? lse * kLog2e : __builtin_huge_valf();
   const float delta = live ? p.delta[row] : 0.f;
-  if (p.sink && live && wave == 0 && hq == 0)
-    atomicAdd(&p.dsink[h], -exp2f(p.sink[h] * kLog2e - lse2) * delta);
 
   const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh;
   const bf16* dorow = reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh;
@@ -283,7 +281,7 @@ bool bwd_mfma_supported(const Params& p) {
   if (p.G > 16 || p.topk > kBwdIdxCap) return false;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
-  return kb < (int64_t)kOOB && vb < (int64_t)kOOB;
+  return kb < (int64_t)kOOB && vb < (int64_t)kOOB && fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss);
 }
 
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s) {

@@ -55,7 +55,7 @@ struct Params {
   float* dv_acc;      // [B, Skv, Hkv, Dv]  fp32 accumulators
   float* delta;       // [B*Sq*Hq] Σ O·dO − dlse
   const float* dlse;  // gradient w.r.t. lse (lse's strides) or nullptr
-  float* dsink;       // [Hq] (accumulated; zeroed by the launcher)
+  float* dsink;       // [Hq] written by dsink_kernel (fixed-order reduction over the rows)
   // deterministic dK/dV (SFA_DKV_CSR): index inversion at block granularity
   uint32_t* kmap;     // [B][Hkv][Sq][kmap_w] membership bitmap: bit k of row t = key k is selected
   int kmap_w;         // 32-bit words per bitmap row (multiple of 4)
@@ -138,6 +138,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads 0
 
+// The contiguous-row gathers form row offsets with __umul24(row id, row
+// bytes), which multiplies the low 24 bits of each operand: a kernel that
+// does so is only eligible when its row byte strides are below 2^24 (row ids
+// are below 2^24 whenever the offsets fit 31 bits and a row is >= 256 bytes).
+inline bool fits_u24(int64_t x) { return x >= 0 && x < ((int64_t)1 << 24); }
+
 // Top-k index producer (sfa_indexer.hip): indexer scores + top-k selection.
 struct IndexerParams {
   const void* q;          // [B, Sq, H, D] bf16 or fp8 e4m3
@@ -166,6 +172,7 @@ hipError_t launch_fwd_generic(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_bwd_generic(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_zero_f32(float* ptr, size_t n, hipStream_t s);
 hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s);
+hipError_t launch_bwd_dsink(const Params& p, hipStream_t s);  // after launch_bwd_delta
 hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss, int64_t dk_sh,
                              void* dv, int64_t dv_sb, int64_t dv_ss, int64_t dv_sh, hipStream_t s);
 hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);

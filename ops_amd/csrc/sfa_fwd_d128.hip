@@ -284,7 +284,8 @@ bool fwd_d128_supported(const Params& p) {
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128);
   // contiguous rows use 32-bit buffer offsets, paged pools 64-bit addresses
-  const bool addressable = p.block_table != nullptr || (kb < (int64_t)kOOB && vb < (int64_t)kOOB);
+  const bool addressable = p.block_table != nullptr || (kb < (int64_t)kOOB && vb < (int64_t)kOOB &&
+                                                        fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss));
   return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && addressable;
 }
 

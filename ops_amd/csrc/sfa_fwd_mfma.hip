@@ -583,7 +583,7 @@ bool rows_fit_32bit(const Params& p) {
   if (p.block_table) return true;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
-  return kb < (int64_t)kOOB && vb < (int64_t)kOOB;
+  return kb < (int64_t)kOOB && vb < (int64_t)kOOB && fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss);
 }
 
 bool mla_supported(const Params& p) {

@@ -9,7 +9,8 @@
 // out = Σ exp(s - lse)·v[idx] (SFA.py:441-480).  Backward: δ = Σ out·dout
 // (SFA.py:590-610); dS = P(dP - δ); dq = scale·Σ dS·k (SFA.py:649-716);
 // dk[idx] += scale·dS·q, dv[idx] += P·dout (SFA.py:757-853, fp32 atomics as
-// SFA.py:853); dsink = -Σ exp(sink - lse)·δ (SFA.py:964-970).
+// SFA.py:853); dsink = -Σ exp(sink - lse)·δ (SFA.py:964-970), reduced per head in
+// a fixed order by dsink_kernel.
 
 #include "sfa_common.h"
 
@@ -214,7 +215,6 @@ __global__ __launch_bounds__(kThreads) void bwd_generic_kernel(Params p) {
     return;
   }
   const float lse2 = lse * kLog2e;
-  if (p.sink && tid == 0) atomicAdd(&p.dsink[h], -exp2f(p.sink[h] * kLog2e - lse2) * delta);
 
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
   const int bound = bound_of(p, b);
@@ -327,6 +327,26 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
   if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
 }
 
+// dsink[h] = -Σ_{b,t} 2^(sink·log2e - lse2)·δ over the rows of head h
+// (SFA.py:964-970).  One workgroup per head; each thread sums a fixed
+// stride of rows and the block reduction adds in a fixed order, so the result
+// is bitwise reproducible (no atomics).  Rows with lse = -inf contribute 0.
+__global__ __launch_bounds__(kThreads) void dsink_kernel(Params p) {
+  __shared__ float red[kWaves];
+  const int h = blockIdx.x;
+  const int64_t nbt = (int64_t)p.B * p.Sq;
+  const float sink2 = p.sink[h] * kLog2e;
+  float acc = 0.f;
+  for (int64_t r = threadIdx.x; r < nbt; r += kThreads) {
+    const int t = (int)(r % p.Sq);
+    const int b = (int)(r / p.Sq);
+    const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+    if (lse != kNegInf) acc -= exp2f(sink2 - lse * kLog2e) * p.delta[r * p.Hq + h];
+  }
+  acc = block_reduce_sum(acc, red);
+  if (threadIdx.x == 0) p.dsink[h] = acc;
+}
+
 inline int grid_for(int64_t n, int threads) {
   int64_t g = (n + threads - 1) / threads;
   if (g > 65535 * 16) g = 65535 * 16;
@@ -368,6 +388,12 @@ hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s) {
     hipLaunchKernelGGL(delta_kernel<float>, grid, dim3(kThreads), 0, s, p);
   else
     hipLaunchKernelGGL(delta_kernel<bf16>, grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dsink(const Params& p, hipStream_t s) {
+  if (p.sink == nullptr || p.dsink == nullptr) return hipSuccess;
+  hipLaunchKernelGGL(dsink_kernel, dim3((unsigned)p.Hq), dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 

@@ -168,3 +168,65 @@ def test_paged_workspace_matches_contiguous_plan():
     a.k_sb = a.v_sb = 65536 * 576
     assert ws == lib.sfa_fwd_workspace_size(ctypes.byref(a))
 
+
+
+def _d128_bwd_args(B, S, Hq, Hkv, K, mode):
+    """Backward arguments of a contiguous bf16 d=128 problem (Sq = Skv = S)."""
+    b = _lib.BwdArgs()
+    a = b.fwd
+    a.dtype = _lib.SFA_DTYPE_BF16
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = B, S, S, Hq, Hkv, 128, 128, K
+    for name in ("q", "k", "v", "idx", "out", "lse"):
+        setattr(a, name, 0x10000)
+    a.q_sh, a.q_ss, a.q_sb = 128, Hq * 128, S * Hq * 128
+    a.o_sh, a.o_ss, a.o_sb = a.q_sh, a.q_ss, a.q_sb
+    a.k_sh, a.k_ss, a.k_sb = 128, Hkv * 128, S * Hkv * 128
+    a.v_sh, a.v_ss, a.v_sb = a.k_sh, a.k_ss, a.k_sb
+    a.i_sh, a.i_ss, a.i_sb = K, Hkv * K, S * Hkv * K
+    a.l_sh, a.l_ss, a.l_sb = 1, Hq, S * Hq
+    for name in ("dout", "dq", "dk", "dv"):
+        setattr(b, name, 0x10000)
+    b.do_sh, b.do_ss, b.do_sb = a.q_sh, a.q_ss, a.q_sb
+    b.dq_sh, b.dq_ss, b.dq_sb = a.q_sh, a.q_ss, a.q_sb
+    b.dk_sh, b.dk_ss, b.dk_sb = a.k_sh, a.k_ss, a.k_sb
+    b.dv_sh, b.dv_ss, b.dv_sb = a.k_sh, a.k_ss, a.k_sb
+    b.dkv_mode = mode
+    return b
+
+
+def _bwd_ws(B, S, Hq, Hkv, K, mode):
+    lib = _lib.load()
+    b = _d128_bwd_args(B, S, Hq, Hkv, K, mode)
+    return lib.sfa_bwd_workspace_size(ctypes.byref(b))
+
+
+def test_auto_dkv_scheme_follows_the_cost_rules():
+    """AUTO takes the deterministic (CSR) scheme on the GQA training shape,
+    and the fp32 atomics where the CSR workspace would exceed 4 GiB (a 64K
+    context: its fp32 partials alone are 4.3 GB) or the key range exceeds
+    64 x top-k (dense recompute beyond ~32x the selected pairs)."""
+    args = (2, 8192, 32, 2, 1024)  # B=2, S=8192, Hq=32, Hkv=2, top-k 1024
+    csr, atomic, auto = (_bwd_ws(*args, m) for m in (_lib.SFA_DKV_CSR, _lib.SFA_DKV_ATOMIC, _lib.SFA_DKV_AUTO))
+    assert csr > atomic > 0 and auto == csr
+    for args in ((1, 65536, 16, 1, 2048), (1, 32768, 16, 1, 256)):
+        csr, atomic, auto = (_bwd_ws(*args, m) for m in (_lib.SFA_DKV_CSR, _lib.SFA_DKV_ATOMIC, _lib.SFA_DKV_AUTO))
+        assert csr > atomic > 0 and auto == atomic, args
+    # at 64K the explicitly requested CSR workspace is the one AUTO avoids
+    assert _bwd_ws(1, 65536, 16, 1, 2048, _lib.SFA_DKV_CSR) > (4 << 30)
+
+
+def test_huge_row_strides_leave_the_24_bit_gathers():
+    """A K/V row stride of 16 MiB or more cannot go through the kernels whose
+    gathers multiply row ids with __umul24: the backward then takes neither
+    the CSR scheme nor the MFMA kernels (its workspace is the atomic one)."""
+    lib = _lib.load()
+    b = _d128_bwd_args(1, 64, 16, 1, 32, _lib.SFA_DKV_AUTO)
+    small = lib.sfa_bwd_workspace_size(ctypes.byref(b))
+    b.fwd.k_ss = b.fwd.v_ss = 1 << 23  # 16 MiB rows (bf16); Skv = 64 keeps offsets < 2^31
+    b.fwd.k_sb = b.fwd.v_sb = 64 << 23
+    big = lib.sfa_bwd_workspace_size(ctypes.byref(b))
+    assert big < small  # no CSR arrays
+    b.dkv_mode = _lib.SFA_DKV_CSR
+    for name in ("dout", "dq", "dk", "dv"):
+        setattr(b, name, 0x10000)
+    assert lib.sfa_bwd(ctypes.byref(b), ctypes.c_void_p(0x10000), 1 << 40, None) == _lib.SFA_E_UNSUPPORTED

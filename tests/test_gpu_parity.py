@@ -127,14 +127,18 @@ def test_train_gqa_fwd_full():
     _check_fwd(out, lse, o_ref, l_ref, rows=rows)
 
 
-def test_train_gqa_bwd_reduced():
-    _say("train_gqa bf16 B=2 S=1024 Hq=32 Hkv=2 d=128 K=128 fwd+bwd")
+@pytest.mark.parametrize("mode", ["csr", "atomic"])
+def test_train_gqa_bwd_reduced(mode):
+    """GQA fwd + bwd at S=1024, K=128 against the oracle, with both dK/dV
+    schemes: 'csr' (key-major kernel + register-direct dQ kernel) and
+    'atomic' (bwd_mfma_kernel: dQ and fp32-atomic dK/dV in one pass)."""
+    _say(f"train_gqa bf16 B=2 S=1024 Hq=32 Hkv=2 d=128 K=128 fwd+bwd dkv_mode={mode}")
     w = make_workload("train_gqa", device=DEV, S=1024, K=128)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     q, k, v, idx, _ = _cpu(w)
     o_ref, l_ref = ref_forward(q, k, v, idx, w.scale)
     _check_fwd(out, lse, o_ref, l_ref)
-    dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale)
+    dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, dkv_mode=mode)
     g_ref = ref_backward(q, k, v, idx, out.cpu(), lse.cpu(), w.dout.cpu(), w.scale)
     for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref[:3]):
         e = _rel_l2(a.cpu(), b)
@@ -142,12 +146,11 @@ def test_train_gqa_bwd_reduced():
 
 
 def test_train_gqa_bwd_full():
-    """Full-size GQA backward (MFMA kernel); the oracle checks one (batch,
-    kv-head) slice, which is an independent problem of its own."""
-    _say("train_gqa bf16 B=2 S=8192 Hq=32 Hkv=2 d=128 K=1024 fwd+bwd (MFMA bwd)")
+    """Full-size GQA backward with both dK/dV schemes (the default
+    deterministic one and the fp32-atomic bwd_mfma_kernel); the oracle checks
+    one (batch, kv-head) slice, which is an independent problem of its own."""
     w = _workload("train_gqa")
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
-    dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale)
     torch.cuda.synchronize()
     b, g, G = 1, 1, 16
     hs = slice(g * G, (g + 1) * G)
@@ -157,10 +160,14 @@ def test_train_gqa_bwd_full():
     idx = w.idx[b:b + 1, :, g:g + 1].cpu()
     o_s, l_s, do_s = out[b:b + 1, :, hs].cpu(), lse[b:b + 1, :, hs].cpu(), w.dout[b:b + 1, :, hs].cpu()
     g_ref = ref_backward(q, k, v, idx, o_s, l_s, do_s, w.scale)
-    for name, a, ref in (("dq", dq[b:b + 1, :, hs], g_ref[0]), ("dk", dk[b:b + 1, :, g:g + 1], g_ref[1]),
-                         ("dv", dv[b:b + 1, :, g:g + 1], g_ref[2])):
-        e = _rel_l2(a.cpu(), ref)
-        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+    for mode in ("csr", "atomic"):
+        _say(f"train_gqa bf16 B=2 S=8192 Hq=32 Hkv=2 d=128 K=1024 bwd dkv_mode={mode}")
+        dq, dk, dv, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, dkv_mode=mode)
+        for name, a, ref in (("dq", dq[b:b + 1, :, hs], g_ref[0]), ("dk", dk[b:b + 1, :, g:g + 1], g_ref[1]),
+                             ("dv", dv[b:b + 1, :, g:g + 1], g_ref[2])):
+            e = _rel_l2(a.cpu(), ref)
+            assert e <= GRAD_RL2, f"{mode} {name} rel-L2 {e}"
+        del dq, dk, dv
 
 
 @pytest.mark.parametrize("D", [64, 256])
@@ -180,10 +187,28 @@ def test_generic_bf16_bwd_large_group(D):
         assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
 
 
-def test_bwd_mfma_masking_and_sink():
-    """MFMA backward with interior padding, kv_lens, a fully masked row, G < 16
-    and an attention sink."""
-    _say("MFMA bwd: padding / kv_lens / masked row / G=8 / sink")
+def _bwd_with_dlse_ref(q, k, v, idx, dout, dlse, scale, kv_lens, sink):
+    """Oracle gradients when a gradient dlse also reaches the returned LSE:
+    d(lse)/d(s_j) = P_j, so dlse adds P·dlse to dS = P(dP - δ), i.e. δ
+    becomes Σ O·dO - dlse (and dsink gains e^(sink - lse)·dlse).  Computed
+    through the oracle's autograd restatement (fp64), which differentiates
+    the forward directly and does not use that identity."""
+    from oracle.sfa_oracle import sfa_forward_autograd
+    qc, kc, vc = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v))
+    sc = sink.detach().cpu().double().requires_grad_(True) if sink is not None else None
+    o2, l2 = sfa_forward_autograd(qc, kc, vc, idx.cpu(), scale=scale,
+                                  kv_lens=None if kv_lens is None else kv_lens.cpu(), sink=sc)
+    l2f = torch.where(torch.isfinite(l2), l2, torch.zeros_like(l2))
+    ((o2 * dout.cpu().double()).sum() + (l2f * dlse.cpu().double()).sum()).backward()
+    return qc.grad, kc.grad, vc.grad, (sc.grad if sc is not None else None)
+
+
+@pytest.mark.parametrize("mode", ["csr", "atomic"])
+def test_bwd_mfma_masking_and_sink(mode):
+    """d=128 backward with interior padding, kv_lens, a fully masked row,
+    G = 8, an attention sink and a gradient into LSE, for both dK/dV schemes
+    ('atomic' runs bwd_mfma_kernel, 'csr' the key-major + dQ kernels)."""
+    _say(f"MFMA bwd: padding / kv_lens / masked row / G=8 / sink / dlse, dkv_mode={mode}")
     w = make_workload("train_gqa", device=DEV, S=512, K=128, B=1, Hq=16, Hkv=2)
     idx = w.idx.clone()
     r = torch.rand(idx.shape, generator=torch.Generator(device=DEV).manual_seed(3), device=DEV)
@@ -193,14 +218,59 @@ def test_bwd_mfma_masking_and_sink():
     sink = torch.linspace(-1, 2, 16, device=DEV)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, idx, w.scale, kv_lens=kv_lens, attn_sink=sink)
     dq, dk, dv, ds = ops_amd.sfa_backward(w.q, w.k, w.v, idx, out, lse, w.dout, w.scale, kv_lens=kv_lens,
-                                          attn_sink=sink)
+                                          attn_sink=sink, dkv_mode=mode)
     q, k, v, _, _ = _cpu(w)
     g_ref = ref_backward(q, k, v, idx.cpu(), out.cpu(), lse.cpu(), w.dout.cpu(), w.scale, kv_lens=kv_lens.cpu(),
                          sink=sink.cpu())
     for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
         e = _rel_l2(a.cpu(), b)
         assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+    # the fully masked row still gets dQ = 0 (its only probability mass is the sink)
     assert torch.all(dq[:, 7] == 0)
+    # unreferenced key rows (beyond kv_lens) get exactly zero dK / dV
+    assert torch.all(dk[:, 480:] == 0) and torch.all(dv[:, 480:] == 0)
+    # a gradient reaching LSE (autograd-derived oracle, fp64)
+    dlse = torch.randn(lse.shape, generator=torch.Generator(device=DEV).manual_seed(9), device=DEV)
+    dq, dk, dv, ds = ops_amd.sfa_backward(w.q, w.k, w.v, idx, out, lse, w.dout, w.scale, kv_lens=kv_lens,
+                                          attn_sink=sink, dlse=dlse, dkv_mode=mode)
+    g_ref = _bwd_with_dlse_ref(w.q.float(), w.k.float(), w.v.float(), idx, w.dout.float(), dlse, w.scale, kv_lens,
+                               sink)
+    for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
+        e = _rel_l2(a.cpu(), b)
+        assert e <= GRAD_RL2, f"dlse {name} rel-L2 {e}"
+
+
+@pytest.mark.parametrize("G", [3, 12])
+@pytest.mark.parametrize("mode", ["auto", "atomic"])
+def test_d128_non_power_of_two_groups(G, mode):
+    """d=128 forward and backward at group sizes that are not powers of two
+    (the deterministic scheme needs one, so 'auto' takes the atomic
+    bwd_mfma_kernel too), with interior padding, out-of-range ids, kv_lens,
+    a fully masked row, a sink and a gradient into LSE."""
+    _say(f"d=128 G={G} Hkv=2 B=2 S=96 Skv=160 K=64 fwd+bwd, dkv_mode={mode}")
+    g = torch.Generator(device="cpu").manual_seed(200 + G)
+    B, S, Skv, Hkv, K = 2, 96, 160, 2, 64
+    Hq = G * Hkv
+    q = torch.randn(B, S, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, S, Hq, 128, generator=g).to(torch.bfloat16)
+    idx = torch.randint(-20, Skv + 20, (B, S, Hkv, K), generator=g, dtype=torch.int32)
+    idx[1, 5] = -1  # a fully masked row
+    kv_lens = torch.tensor([160, 117], dtype=torch.int32)
+    sink = torch.linspace(-1.0, 2.0, Hq)
+    dlse = torch.randn(B, S, Hq, generator=g)
+    scale = 1.0 / math.sqrt(128)
+    o_ref, l_ref = ref_forward(q, k, v, idx, scale, kv_lens=kv_lens, sink=sink)
+    qd, kd, vd, idd, kld, sd = (t.to(DEV) for t in (q, k, v, idx, kv_lens, sink))
+    out, lse = ops_amd.sfa_forward(qd, kd, vd, idd, scale, kv_lens=kld, attn_sink=sd)
+    _check_fwd(out, lse, o_ref, l_ref)
+    dq, dk, dv, ds = ops_amd.sfa_backward(qd, kd, vd, idd, out, lse, dout.to(DEV), scale, kv_lens=kld,
+                                          attn_sink=sd, dlse=dlse.to(DEV), dkv_mode=mode)
+    g_ref = _bwd_with_dlse_ref(q.float(), k.float(), v.float(), idx, dout.float(), dlse, scale, kv_lens, sink)
+    for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
+        e = _rel_l2(a.cpu(), b)
+        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
 
 
 @pytest.mark.parametrize("S,K", [(300, 64), (1024, 256)])

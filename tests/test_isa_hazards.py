@@ -11,9 +11,11 @@ catches code where the compiler placed a copy or a spill reload of an
 operand right in front of an MFMA (as happens when register pressure makes
 it move values between the VGPR and AGPR files).  A second check covers the
 other direction in the kernels whose MFMAs are inline asm: no instruction
-may read a VGPR an MFMA wrote before the kernel's explicit drain (18 wait
-states) has passed.  CPU only: the assembly comes from hipcc's device-only
-compile (no GPU needed)."""
+may read a register (VGPR or AGPR) an MFMA wrote before the kernel's
+explicit drain has passed, on any control-flow path, earlier than the wait
+states the compiler itself inserts after a builtin MFMA of the same kind (a
+probe compile measures that number).  CPU only: the assembly comes from
+hipcc's device-only compile (no GPU needed)."""
 import os
 import re
 import shutil
@@ -71,44 +73,85 @@ def scan(asm: str):
 # Kernels whose MFMAs are inline asm (the compiler inserts no wait states for
 # them); kernels built on the MFMA builtins get theirs from the compiler.
 INLINE_ASM_MFMA_KERNELS = ("dkv_keymajor_kernel", "fwd_mfma_kernel")
-DRAIN = 18  # wait states the inline-asm drains provide after an MFMA before VALU reads
+DRAIN = 18  # wait states the inline-asm drains provide (at least) after an MFMA before VALU reads
 
 
-def scan_result_reads(asm: str, kernels=INLINE_ASM_MFMA_KERNELS):
-    """[(kernel, mfma, reader)] where an instruction reads a VGPR an MFMA
-    wrote fewer than DRAIN wait states later (1 per instruction, N + 1 per
-    s_nop N; the scan stops at a branch, a label, or an MFMA that writes the
-    same registers)."""
-    found = []
+def _kernel_bodies(asm: str, kernels):
+    """(kernel name, instruction/label lines, label -> index) per kernel."""
     for fm in re.finditer(r"^(_Z\S+):", asm, re.M):
         if not any(k in fm.group(1) for k in kernels):
             continue
         end = asm.find(".Lfunc_end", fm.end())
         body = [l.strip() for l in asm[fm.end():end].split("\n")
                 if (l.startswith("\t") and not l.startswith("\t;") and not l.startswith("\t.")) or l.startswith(".LBB")]
+        labels = {l[:-1]: i for i, l in enumerate(body) if l.startswith(".LBB") and l.endswith(":")}
+        yield fm.group(1), body, labels
+
+
+def _reads(ins: str):
+    """Registers an instruction reads (stores read every operand; MFMAs their
+    srcA / srcB / srcC; other instructions every operand after the first)."""
+    parts = ins.split(None, 1)
+    if len(parts) < 2:
+        return set()
+    ops = parts[1].split(",")
+    if ins.startswith(("ds_write", "global_store", "buffer_store", "flat_store")):
+        return set().union(*[_regs(o) for o in ops])
+    return set().union(*[_regs(o) for o in ops[1:]]) if len(ops) > 1 else set()
+
+
+def scan_result_reads(asm: str, kernels=INLINE_ASM_MFMA_KERNELS, drain: int = DRAIN):
+    """[(kernel, mfma, reader)] where an instruction reads a register (VGPR or
+    AGPR) an MFMA wrote fewer than ``drain`` wait states later (1 per
+    instruction, N + 1 per s_nop N).  Every control-flow path from the MFMA
+    is followed: labels fall through, s_branch jumps to its target and
+    s_cbranch_* continues on both sides (loop back-edges included); a path
+    ends at s_endpgm, after ``drain`` wait states, or at an MFMA that rewrites the
+    same registers (the hardware chains dependent accumulations).  An MFMA
+    reading the result as srcA / srcB is a reader too."""
+    found = []
+    for name, body, labels in _kernel_bodies(asm, kernels):
         for i, ins in enumerate(body):
             if "v_mfma" not in ins:
                 continue
-            dst = {r for r in _regs(ins.split(None, 1)[1].split(",")[0]) if r[0] == "v"}
+            dst = _regs(ins.split(None, 1)[1].split(",")[0])
             if not dst:
                 continue
-            waits = 0
-            for nxt in body[i + 1:i + 64]:
-                if nxt.startswith(".LBB") or nxt.startswith(("s_cbranch", "s_branch", "s_endpgm")) or waits >= DRAIN:
-                    break
-                if nxt.startswith("s_nop"):
-                    waits += int(nxt.split()[1]) + 1
-                    continue
-                parts = nxt.split(None, 1)
-                if "v_mfma" in nxt and _regs(parts[1].split(",")[0]) & dst:
-                    break
-                if len(parts) > 1 and nxt.startswith(("v_", "ds_", "global_", "buffer_")) and "v_mfma" not in nxt:
-                    ops = parts[1].split(",")
-                    stores = nxt.startswith(("ds_write", "global_store", "buffer_store"))
-                    reads = set().union(*[_regs(o) for o in (ops if stores else ops[1:])])
-                    if reads & dst:
-                        found.append((fm.group(1), ins, nxt))
-                waits += 1
+            stack, seen, hits = [(i + 1, 0)], set(), set()
+            while stack:
+                pos, waits = stack.pop()
+                while pos < len(body) and waits < drain:
+                    if (pos, waits) in seen:
+                        break
+                    seen.add((pos, waits))
+                    nxt = body[pos]
+                    if nxt.startswith(".LBB"):
+                        pos += 1
+                        continue
+                    if nxt.startswith("s_endpgm"):
+                        break
+                    if nxt.startswith("s_nop"):
+                        waits += int(nxt.split()[1]) + 1
+                        pos += 1
+                        continue
+                    if "v_mfma" in nxt:
+                        mops = nxt.split(None, 1)[1].split(",")
+                        if set().union(*[_regs(o) for o in mops[1:3]]) & dst:
+                            hits.add(nxt)
+                        if _regs(mops[0]) & dst:
+                            break
+                    elif nxt.startswith(("v_", "ds_", "global_", "buffer_", "flat_")) and _reads(nxt) & dst:
+                        hits.add(nxt)
+                    waits += 1
+                    if nxt.startswith("s_branch"):
+                        pos = labels.get(nxt.split()[1], len(body))
+                        continue
+                    if nxt.startswith("s_cbranch"):
+                        tgt = labels.get(nxt.split()[-1])
+                        if tgt is not None:
+                            stack.append((tgt, waits))
+                    pos += 1
+            found += [(name, ins, h) for h in sorted(hits)]
     return found
 
 
@@ -152,11 +195,64 @@ def test_result_scanner_flags_a_planted_early_read():
     assert [h[2] for h in hits] == ["v_add_f32_e32 v20, v3, v3"]
 
 
+def test_result_scanner_follows_branches_and_agprs():
+    # a read carried across the loop back-edge, an AGPR result read by
+    # v_accvgpr_read on the taken side of a conditional branch, and the same
+    # reads after a full drain (not reported)
+    asm = ("_Zfwd_mfma_kernel_planted:\n"
+           ".LBB0_1:\n\tv_add_f32_e32 v20, v1, v1\n"
+           "\tv_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[24:27], v[0:15]\n"
+           "\ts_cbranch_scc1 .LBB0_1\n"
+           "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[16:19], v[24:27], a[0:15]\n"
+           "\ts_cbranch_vccnz .LBB0_3\n"
+           "\ts_nop 7\n\ts_nop 7\n\ts_nop 3\n"
+           ".LBB0_3:\n\tv_accvgpr_read_b32 v30, a3\n"
+           "\ts_nop 7\n\ts_nop 7\n\ts_nop 3\n\tv_add_f32_e32 v21, v2, v30\n\ts_endpgm\n.Lfunc_end0:\n")
+    hits = scan_result_reads(asm)
+    assert sorted(h[2] for h in hits) == ["v_accvgpr_read_b32 v30, a3", "v_add_f32_e32 v20, v1, v1"]
+
+
+PROBE = """#include <hip/hip_runtime.h>
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+__global__ void probe(float* o, const bf16x8* a, const bf16x8* b) {
+  f32x16 c = {};
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[threadIdx.x], b[threadIdx.x], c, 0, 0, 0);
+  o[threadIdx.x] = c[0] * 3.0f;
+}
+"""
+
+
+def required_read_wait_states(tmp_path: Path) -> int:
+    """Wait states the compiler's own hazard recognizer puts between a
+    builtin v_mfma_f32_32x32x16_bf16 and a VALU read of its result (the
+    hardware requirement the inline-asm MFMAs must meet by hand)."""
+    src = tmp_path / "probe.hip"
+    src.write_text(PROBE)
+    asm = _device_asm(src, tmp_path)
+    lines = [l.strip() for l in asm.split("\n") if l.startswith("\t")]
+    i = next(j for j, l in enumerate(lines) if l.startswith("v_mfma_f32_32x32x16_bf16"))
+    waits = 0
+    for l in lines[i + 1:]:
+        if l.startswith("s_nop"):
+            waits += int(l.split()[1]) + 1
+        elif l.startswith("v_"):
+            return waits
+        else:
+            waits += 1
+    raise AssertionError("no VALU read after the probe MFMA")
+
+
 def test_no_early_reads_of_inline_asm_mfma_results(tmp_path):
+    """No read of an inline-asm MFMA's result (including the compiler's own
+    register copies around the tile loop, which come before the kernels'
+    explicit drains) earlier than the hardware requirement."""
+    need = required_read_wait_states(tmp_path)
+    assert 8 <= need <= DRAIN, need
     srcs = [s for s in sfa_build.sources() if Path(s).stem in ("sfa_bwd_csr", "sfa_fwd_mfma")]
     assert len(srcs) == 2
     asms = [_device_asm(Path(s), tmp_path) for s in srcs]
     assert sum(a.count("v_mfma") for a in asms) > 300
-    hits = [h for a in asms for h in scan_result_reads(a)]
+    hits = [h for a in asms for h in scan_result_reads(a, drain=need)]
     assert not hits, "VGPR MFMA result read before the drain:\n" + "\n".join(
         f"{k[-60:]}: {m}  ->  {r}" for k, m, r in hits[:10])
