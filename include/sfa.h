@@ -168,6 +168,22 @@ SFA_API size_t sfa_fwd_workspace_size(const sfa_fwd_args* a);
  * Replaces `_attn_fwd` (SFA.py:483-587 via SFA.py:122-159). */
 SFA_API int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the static per-GPU scratch of sfa_fwd_noalloc (64 MiB). */
+#define SFA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* Forward that allocates nothing and takes no workspace: the same arguments,
+ * kernels and results as sfa_fwd.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The split-k partials
+ * of the decode shape (sfa_fwd_workspace_size(a) bytes) go to a static device
+ * buffer of SFA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends; a plan that needs more returns SFA_E_WORKSPACE
+ * before any device work.  `stream` must belong to the current device; the
+ * first call on a device resolves the buffer's address (make it before any
+ * graph capture).  All calls on one GPU share the buffer: calls that may
+ * overlap on one GPU (unordered streams) race. */
+SFA_API int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream);
+
 /* Bytes of device workspace sfa_fwd_paged needs for `a` and `pages`. */
 SFA_API size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages);
 

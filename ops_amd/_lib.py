@@ -27,11 +27,14 @@ SFA_E_WORKSPACE = -2
 SFA_E_UNSUPPORTED = -3
 SFA_E_HIP = -4
 
+SFA_NOALLOC_SCRATCH_BYTES = 64 << 20
+
 EXPORTED_SYMBOLS = (
     "sfa_abi_version",
     "sfa_last_error",
     "sfa_fwd_workspace_size",
     "sfa_fwd",
+    "sfa_fwd_noalloc",
     "sfa_bwd_workspace_size",
     "sfa_bwd",
     "sfa_fwd_paged_workspace_size",
@@ -134,6 +137,8 @@ def load() -> ctypes.CDLL:
         lib.sfa_fwd_workspace_size.argtypes = [ctypes.POINTER(FwdArgs)]
         lib.sfa_fwd.restype = ctypes.c_int
         lib.sfa_fwd.argtypes = [ctypes.POINTER(FwdArgs), _vp, ctypes.c_size_t, _vp]
+        lib.sfa_fwd_noalloc.restype = ctypes.c_int
+        lib.sfa_fwd_noalloc.argtypes = [ctypes.POINTER(FwdArgs), _vp]
         lib.sfa_bwd_workspace_size.restype = ctypes.c_size_t
         lib.sfa_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.sfa_bwd.restype = ctypes.c_int

@@ -8,6 +8,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "sfa_common.h"
 
 namespace {
@@ -227,6 +230,73 @@ int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void
   const int rc = check_fwd(a);
   if (rc != SFA_OK) return rc;
   return run_fwd(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// ---- sfa_fwd_noalloc: the split-k partials in a static device buffer ----
+// One copy of `scratch` per GPU (each device that loads the library holds it
+// until the process ends).  In host code `scratch` only names the variable:
+// its device address is resolved once per device with hipGetSymbolAddress
+// (with that device current) and cached; kernels get that address.
+constexpr size_t kNoallocBytes = SFA_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the device `stream` belongs to, which must
+// be the current device.
+int noalloc_scratch(void* stream, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_fail(e, "sfa_fwd_noalloc: hipGetDevice");
+  int dev = cur;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice((hipStream_t)stream, &dev);
+    if (e != hipSuccess) return hip_fail(e, "sfa_fwd_noalloc: hipStreamGetDevice");
+  }
+  if (dev != cur) return fail(SFA_E_INVALID, "sfa_fwd_noalloc: the stream belongs to device %d, device %d is current", dev, cur);
+  if (dev < 0 || dev >= kMaxDevices) return fail(SFA_E_UNSUPPORTED, "sfa_fwd_noalloc: device %d >= %d", dev, kMaxDevices);
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "sfa_fwd_noalloc: hipGetSymbolAddress(scratch)");
+      if (ptr == nullptr) return fail(SFA_E_HIP, "sfa_fwd_noalloc: null scratch address");
+      g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return SFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream) {
+  g_err[0] = 0;
+  const int rc = check_fwd(a);
+  if (rc != SFA_OK) return rc;
+  const FwdPlan pl = plan_fwd(a, nullptr);
+  const size_t need = pl.part_o_bytes + pl.part_lse_bytes;
+  if (need > kNoallocBytes)
+    return fail(SFA_E_WORKSPACE,
+                "sfa_fwd_noalloc: the split-k partials need %zu bytes, above its static scratch of %zu bytes "
+                "(use sfa_fwd with a workspace, or fewer splits)",
+                need, kNoallocBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int r = noalloc_scratch(stream, &ws);
+    if (r != SFA_OK) return r;
+  }
+  return run_fwd(a, nullptr, ws, need > 0 ? kNoallocBytes : 0, stream);
 }
 
 size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages) {

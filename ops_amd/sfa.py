@@ -120,9 +120,12 @@ def _prep(q, k, v, topk_idxs, kv_lens, sink, validate=True):
 
 
 def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None, num_splits: int = 0,
-                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, noalloc: bool = False):
     """Forward only (no autograd): ``(out, lse)``.  ``out``/``lse`` may be
-    preallocated ([B, Sq, Hq, Dv] in q's dtype / [B, Sq, Hq] float32)."""
+    preallocated ([B, Sq, Hq, Dv] in q's dtype / [B, Sq, Hq] float32).
+    ``noalloc=True`` calls ``sfa_fwd_noalloc``: the split-k partials then live
+    in the library's static per-GPU scratch (64 MiB) instead of a workspace
+    tensor, so with preallocated ``out``/``lse`` nothing is allocated."""
     lib = _lib.load()
     q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
     B, Sq, Hq, Dqk = q.shape
@@ -133,9 +136,12 @@ def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None,
     if lse is None:
         lse = torch.empty((B, Sq, Hq), dtype=torch.float32, device=q.device)
     a = _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    if noalloc:
+        _lib.check(lib.sfa_fwd_noalloc(ctypes.byref(a), ctypes.c_void_p(stream)))
+        return out, lse
     ws = lib.sfa_fwd_workspace_size(ctypes.byref(a))
     wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
-    stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.sfa_fwd(ctypes.byref(a), _ptr(wbuf), ws, ctypes.c_void_p(stream)))
     return out, lse
 

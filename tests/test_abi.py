@@ -230,3 +230,24 @@ def test_huge_row_strides_leave_the_24_bit_gathers():
     for name in ("dout", "dq", "dk", "dv"):
         setattr(b, name, 0x10000)
     assert lib.sfa_bwd(ctypes.byref(b), ctypes.c_void_p(0x10000), 1 << 40, None) == _lib.SFA_E_UNSUPPORTED
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch():
+    """sfa_fwd_noalloc refuses a split-k plan whose partials exceed its
+    64 MiB static scratch before touching the device (so this runs without
+    a GPU): the MLA decode shape at 8 splits needs 8 x 64 x 128 x 512 bf16."""
+    lib = _lib.load()
+    a = _valid_args()
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = 64, 1, 65536, 128, 1, 576, 512, 2048
+    a.k_ss = a.v_ss = a.k_sh = a.v_sh = 576
+    a.k_sb = a.v_sb = 65536 * 576
+    a.q_sh, a.q_ss, a.q_sb = 576, 128 * 576, 128 * 576
+    a.o_sh, a.o_ss, a.o_sb = 512, 128 * 512, 128 * 512
+    a.v = a.k
+    a.num_splits = 8
+    need = lib.sfa_fwd_workspace_size(ctypes.byref(a))
+    assert need > _lib.SFA_NOALLOC_SCRATCH_BYTES
+    assert lib.sfa_fwd_noalloc(ctypes.byref(a), None) == _lib.SFA_E_WORKSPACE
+    assert b"static scratch" in lib.sfa_last_error()
+    a.topk = 0
+    assert lib.sfa_fwd_noalloc(ctypes.byref(a), None) == _lib.SFA_E_INVALID
