@@ -74,6 +74,14 @@ def gathered_bytes(w, pairs):
     return pairs * (w.q.shape[3] + w.v.shape[3]) * w.q.element_size()
 
 
+def decode_bytes(w, pairs):
+    """Algorithmic bytes of a decode step: the gathered K rows (V is their
+    prefix) + q + out + lse + idx."""
+    B, _, Hq, Dqk = w.q.shape
+    Dv = w.v.shape[3]
+    return pairs * Dqk * 2 + w.q.numel() * 2 + B * Hq * Dv * 2 + B * Hq * 4 + w.idx.numel() * 4
+
+
 def time_steps(fn, steps, warmup, before=None):
     """Per-step HIP-event durations (ms) on the current stream."""
     import torch
@@ -96,12 +104,40 @@ def time_steps(fn, steps, warmup, before=None):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
-def cpu_baseline_mla(w, pairs_total, seconds):
-    """Oracle on a strided sample of query rows, until ~``seconds`` of CPU work."""
+def cpu_model():
+    """The host CPU's model name (first ``model name`` line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _cpu_threads():
     import torch
-    from oracle.sfa_oracle import sfa_forward
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    return cores
+
+
+def _cpu_copy(w, rows=None):
+    """CPU copies of a workload's tensors, optionally only query rows ``rows``
+    (a slice of dim 1) of q / idx / dout."""
+    sl = slice(None) if rows is None else rows
+    cp = lambda t: None if t is None else t[:, sl].cpu() if t.dim() == 4 else t.cpu()
+    return dict(q=cp(w.q), k=w.k.cpu(), idx=cp(w.idx), dout=cp(w.dout),
+                kv_lens=None if w.kv_lens is None else w.kv_lens.cpu())
+
+
+def cpu_baseline_mla(w, seconds):
+    """Oracle forward on a strided sample of query rows, until ~``seconds`` of
+    CPU work; the rate (valid-pair TFLOP/s) extrapolates to the full step."""
+    from oracle.sfa_oracle import sfa_forward
+    cores = _cpu_threads()
     k = w.k.cpu()
     v = k[..., : w.v.shape[3]]
     S = w.q.shape[1]
@@ -119,9 +155,62 @@ def cpu_baseline_mla(w, pairs_total, seconds):
         if elapsed >= seconds:
             break
     flops = fwd_flops(w, done_pairs)
-    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+    rate = flops / elapsed / 1e12
+    return {"value": rate, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"oracle fp32 fwd on {nrows} query rows ({done_pairs} valid pairs) of the mla_prefill "
-                      f"workload, {elapsed:.1f} s; sfa_forward chunks of {chunk} rows"}
+                      f"workload, {elapsed:.1f} s; sfa_forward chunks of {chunk} rows",
+            "extrapolated_step_s": fwd_flops(w, valid_pairs(w)) / (rate * 1e12)}
+
+
+def cpu_fwd_bwd(w, rows=None, bwd=True):
+    """Oracle forward (+ backward) on query rows ``rows`` of workload ``w``
+    (all rows if None); returns seconds and the valid pairs covered."""
+    from oracle.sfa_oracle import sfa_backward, sfa_forward
+    c = _cpu_copy(w, rows)
+    k = c["k"]
+    v = k[..., : w.v.shape[3]] if w.v.data_ptr() == w.k.data_ptr() else w.v.cpu()
+    t0 = time.perf_counter()
+    out, lse = sfa_forward(c["q"], k, v, c["idx"], w.scale, kv_lens=c["kv_lens"])
+    t_fwd = time.perf_counter() - t0
+    t_bwd = None
+    if bwd:
+        t0 = time.perf_counter()
+        sfa_backward(c["q"], k, v, c["idx"], out, lse, c["dout"], w.scale, kv_lens=c["kv_lens"])
+        t_bwd = time.perf_counter() - t0
+    bound = c["kv_lens"].long().view(-1, 1, 1, 1) if c["kv_lens"] is not None else k.shape[1]
+    pairs = int(((c["idx"] >= 0) & (c["idx"].long() < bound)).sum())
+    return t_fwd, t_bwd, pairs
+
+
+def cpu_rate(name, w):
+    """CPU (oracle, PyTorch eager fp32) rate of workload ``name`` on this
+    host's cores: full runs where they take seconds, a bounded sample of query
+    rows otherwise (the rate is per valid pair, so it extrapolates)."""
+    _cpu_threads()
+    if name == "tiny":
+        tf, tb, pairs = cpu_fwd_bwd(w)
+        return {"value": (fwd_flops(w, pairs) + bwd_flops(w, pairs)) / (tf + tb) / 1e12, "unit": "TFLOP/s",
+                "fwd_s": tf, "bwd_s": tb, "sample": "full fwd+bwd (B=1, S=256, Hq=4, d=64, top-k 64, fp32)"}
+    if name == "prefill":
+        tf, _, pairs = cpu_fwd_bwd(w, bwd=False)
+        return {"value": fwd_flops(w, pairs) / tf / 1e12, "unit": "TFLOP/s", "fwd_s": tf,
+                "sample": "full fwd (B=1, S=4096, Hq=16, d=128, top-k 512)"}
+    if name == "train_gqa":
+        S = w.q.shape[1]
+        r0 = S - 512
+        tf, tb, pairs = cpu_fwd_bwd(w, rows=slice(r0, S))
+        full = valid_pairs(w)
+        rate_f, rate_b = fwd_flops(w, pairs) / tf / 1e12, bwd_flops(w, pairs) / tb / 1e12
+        return {"value": (fwd_flops(w, pairs) + bwd_flops(w, pairs)) / (tf + tb) / 1e12, "unit": "TFLOP/s",
+                "fwd_tflops": rate_f, "bwd_tflops": rate_b, "fwd_s": tf, "bwd_s": tb,
+                "extrapolated_step_s": fwd_flops(w, full) / (rate_f * 1e12) + bwd_flops(w, full) / (rate_b * 1e12),
+                "sample": f"fwd+bwd on query rows {r0}..{S - 1} of both sequences ({pairs} valid pairs, full "
+                          f"top-k); rate per valid pair, extrapolated to the full step"}
+    if name == "mla_decode":
+        tf, _, pairs = cpu_fwd_bwd(w, bwd=False)
+        return {"value": decode_bytes(w, pairs) / tf / 1e9, "unit": "GB/s", "tflops": fwd_flops(w, pairs) / tf / 1e12,
+                "fwd_s": tf, "sample": "full decode step (64 sequences x 128 heads, top-k 2048)"}
+    raise KeyError(name)
 
 
 def bench_mla_prefill(args):
@@ -150,8 +239,26 @@ def bench_mla_prefill(args):
     return w, res
 
 
+def bench_tiny(args):
+    """Config 1 (fp32, generic kernels): fwd + bwd TFLOP/s."""
+    import ops_amd
+    from ops_amd.workloads import make_workload
+    w = make_workload("tiny", device="cuda")
+    pairs = valid_pairs(w)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+    ft, _ = time_steps(lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale), args.steps * 4, args.warmup)
+    bt, _ = time_steps(lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale),
+                       args.steps * 4, args.warmup)
+    fms, bms = sum(ft) / len(ft), sum(bt) / len(bt)
+    res = {"metric": "fwd+bwd effective TFLOP/s", "value": (fwd_flops(w, pairs) + bwd_flops(w, pairs)) /
+           ((fms + bms) * 1e-3) / 1e12, "unit": "TFLOP/s", "fwd_ms": fms, "bwd_ms": bms, "valid_pairs": pairs,
+           "dtype": "f32", "config": {"B": 1, "S": 256, "Hq": 4, "Hkv": 1, "d": 64, "topk": 64}}
+    if not args.no_cpu:
+        res["cpu"] = cpu_rate("tiny", w)
+    return res
+
+
 def bench_prefill(args):
-    import torch
     import ops_amd
     from ops_amd.workloads import make_workload
     w = make_workload("prefill", device="cuda")
@@ -160,13 +267,15 @@ def bench_prefill(args):
     times, _ = time_steps(lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale), args.steps * 4, args.warmup)
     ms = sum(times) / len(times)
     tf = flops / (ms * 1e-3) / 1e12
-    return {"metric": "fwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
-            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
-            "config": {"B": 1, "S": 4096, "Hq": 16, "Hkv": 1, "d": 128, "topk": 512}}
+    res = {"metric": "fwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
+           "frac_of_peak": tf / PEAK_BF16_TFLOPS, "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
+           "config": {"B": 1, "S": 4096, "Hq": 16, "Hkv": 1, "d": 128, "topk": 512}}
+    if not args.no_cpu:
+        res["cpu"] = cpu_rate("prefill", w)
+    return res
 
 
 def bench_train_gqa(args):
-    import torch
     import ops_amd
     from ops_amd.workloads import make_workload
     w = make_workload("train_gqa", device="cuda")
@@ -191,7 +300,18 @@ def bench_train_gqa(args):
                                 "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
         res["bwd"]["note"] = ("TFLOP/s over valid pairs (pairs * G * 2 (3 d_qk + 2 d_v)); 'csr' = deterministic "
                               "dK/dV (the default), 'atomic' = fp32 atomics")
+    if not args.no_cpu:
+        res["cpu"] = cpu_rate("train_gqa", w)
     return res
+
+
+def decode_flush():
+    """A 1 GiB buffer whose READ before every step evicts the KV rows from the
+    256 MB Infinity Cache and L2 without leaving dirty lines behind (a
+    write-flush makes the next kernel pay for write-backs it did not cause)."""
+    import torch
+    flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    return lambda: flush.sum()
 
 
 def bench_mla_decode(args):
@@ -202,15 +322,12 @@ def bench_mla_decode(args):
     pairs = valid_pairs(w)
     B, _, Hq, Dqk = w.q.shape
     Dv = w.v.shape[3]
-    nbytes = pairs * Dqk * 2 + w.q.numel() * 2 + B * Hq * Dv * 2 + B * Hq * 4 + w.idx.numel() * 4
-    # Before every step a 1 GiB buffer is READ, which evicts the KV rows from
-    # the 256 MB Infinity Cache and L2 without leaving dirty lines behind (a
-    # write-flush makes the next kernel pay for write-backs it did not cause).
-    flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    nbytes = decode_bytes(w, pairs)
+    flush = decode_flush()
     out = torch.empty((B, 1, Hq, Dv), dtype=w.q.dtype, device="cuda")
     lse = torch.empty((B, 1, Hq), dtype=torch.float32, device="cuda")
     fn = lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
-    times, _ = time_steps(fn, args.steps * 4, args.warmup, before=lambda: flush.sum())
+    times, _ = time_steps(fn, args.steps * 4, args.warmup, before=flush)
     us = sum(times) / len(times) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
     res = {"metric": "decode GB/s (algorithmic bytes, cache flushed)", "value": gbs, "unit": "GB/s", "us": us,
@@ -221,12 +338,14 @@ def bench_mla_decode(args):
     kp, vp, bt = page_kv(w.k, w.v, 64, seed=1)
     pbytes = nbytes + pairs * 4  # one block-table entry per valid slot
     fnp = lambda: ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
-    times, _ = time_steps(fnp, args.steps * 4, args.warmup, before=lambda: flush.sum())
+    times, _ = time_steps(fnp, args.steps * 4, args.warmup, before=flush)
     pus = sum(times) / len(times) * 1e3
     res["paged"] = {"value": pbytes / (pus * 1e-6) / 1e9, "unit": "GB/s", "us": pus, "bytes": pbytes,
                     "frac_of_peak": pbytes / (pus * 1e-6) / 1e9 / PEAK_HBM_GBS, "page_size": 64,
                     "pool_bytes": kp.numel() * kp.element_size()}
     del kp, vp
+    if not args.no_cpu:
+        res["cpu"] = cpu_rate("mla_decode", w)
     return res
 
 
@@ -292,16 +411,54 @@ def bench_indexer(args, mla=None):
     return res
 
 
+def profile_targets(name):
+    """(fn, before) of one workload's kernels, for counter runs that time
+    nothing: ``python bench.py --profile NAME --steps N`` launches fn N times
+    (before() ahead of each, e.g. the decode cache flush)."""
+    import torch
+    import ops_amd
+    from ops_amd.workloads import make_workload, page_kv
+    if name == "mla_prefill":
+        w = make_workload("mla_prefill", device="cuda")
+        return lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale), None
+    if name == "prefill":
+        w = make_workload("prefill", device="cuda")
+        return lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale), None
+    if name in ("train_gqa_fwd", "train_gqa_bwd_csr", "train_gqa_bwd_atomic"):
+        w = make_workload("train_gqa", device="cuda")
+        if name == "train_gqa_fwd":
+            return lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale), None
+        out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+        mode = name.rsplit("_", 1)[1]
+        return lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, dkv_mode=mode), None
+    if name in ("mla_decode", "mla_decode_paged"):
+        w = make_workload("mla_decode", device="cuda")
+        flush = decode_flush()
+        if name == "mla_decode":
+            return lambda: ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens), flush
+        kp, vp, bt = page_kv(w.k, w.v, 64, seed=1)
+        return lambda: ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens=w.kv_lens), flush
+    if name == "mla_bwd":
+        w = make_workload("mla_prefill", device="cuda", S=1024, with_dout=True)
+        out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
+        return lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale), None
+    raise SystemExit(f"unknown --profile target {name!r}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--extra", default="prefill,train_gqa,mla_decode,indexer,mla_bwd",
+    ap.add_argument("--extra", default="tiny,prefill,train_gqa,mla_decode,indexer,mla_bwd",
                     help="comma list of additional workloads to measure ('' for none)")
     ap.add_argument("--no-bwd", action="store_true", help="skip the train_gqa backward timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", default="", metavar="NAME",
+                    help="only launch workload NAME's kernels `steps` times (for counter runs) and exit: "
+                         "mla_prefill, prefill, train_gqa_fwd, train_gqa_bwd_csr, train_gqa_bwd_atomic, "
+                         "mla_decode, mla_decode_paged, mla_bwd")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB `steps` times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -322,6 +479,16 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": args.steps}), flush=True)
         return
+    if args.profile:
+        fn, before = profile_targets(args.profile)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            if before:
+                before()
+            fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "launches": args.steps}), flush=True)
+        return
 
     w, head = bench_mla_prefill(args)
     extra = {}
@@ -330,13 +497,15 @@ def main():
         if name == "indexer":
             extra[name] = bench_indexer(args, w)
         else:
-            extra[name] = {"prefill": bench_prefill, "train_gqa": bench_train_gqa,
+            extra[name] = {"tiny": bench_tiny, "prefill": bench_prefill, "train_gqa": bench_train_gqa,
                            "mla_decode": bench_mla_decode, "mla_bwd": bench_mla_bwd}[name](args)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle) on a bounded sample")
-        cpu = cpu_baseline_mla(w, head["valid_pairs"], args.cpu_seconds)
+        cpu = cpu_baseline_mla(w, args.cpu_seconds)
+        cpu["cpu_model"] = cpu_model()
+        cpu["per_config"] = {n: r.pop("cpu") for n, r in extra.items() if isinstance(r, dict) and "cpu" in r}
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_mla_prefill.json")
     if os.path.exists(tpath):

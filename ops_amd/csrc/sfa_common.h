@@ -108,6 +108,36 @@ __device__ __forceinline__ int staged_id(const Params& p, int b, int id, int bou
   return (id >= 0 && id < bound) ? id : -1;
 }
 
+// Index row of a work item, in two phases so that its global loads are in
+// flight together with whatever the caller issues in between (a loop that
+// stores each value to LDS as it arrives compiles to one memory round trip
+// per iteration).  load(): thread tid reads slots tid, tid + THREADS, ...
+// (CAP / THREADS coalesced loads, slots past nslots read nothing); store():
+// writes the staged ids (invalid -> -1, padding -1 up to nstage <= CAP).
+template <int CAP, int THREADS>
+struct IdxStage {
+  static constexpr int IPT = CAP / THREADS;
+  static_assert(CAP % THREADS == 0, "slots split evenly over the threads");
+  int v[IPT];
+  __device__ __forceinline__ void load(const int32_t* irow, int nslots, int tid) {
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int i = tid + j * THREADS;
+      v[j] = i < nslots ? irow[i] : -1;
+    }
+  }
+  template <bool PAGED>
+  __device__ __forceinline__ void store(const Params& p, int b, int bound, int nslots, int nstage, int* s_idx,
+                                        int tid) {
+    int st[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_id<PAGED>(p, b, v[j], bound) : -1;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j)
+      if (tid + j * THREADS < nstage) s_idx[tid + j * THREADS] = st[j];
+  }
+};
+
 // Byte offset of pool row r from the pool base (paged mode): page r >> shift
 // at page_bytes, row r & mask at row_bytes (64-bit: pools may exceed 4 GiB).
 __device__ __forceinline__ uint64_t pool_row_offset(uint32_t r, int shift, uint64_t page_bytes, uint32_t row_bytes) {

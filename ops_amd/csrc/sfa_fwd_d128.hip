@@ -71,12 +71,11 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   if (nslots < 0) nslots = 0;
   const int ntiles = (nslots + 31) / 32;
 
-  // ---- stage indices (invalid -> -1) --------------------------------------
-  {
-    const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
-    const int bound = bound_of(p, b);
-    for (int i = lane; i < ntiles * 32; i += 64) s_idx[i] = (i < nslots) ? staged_id<PAGED>(p, b, irow[i], bound) : -1;
-  }
+  // ---- index row (invalid -> -1): its loads and Q's are in flight together --
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
+  const int bound = bound_of(p, b);
+  IdxStage<kIdxCapD, 64> istage;
+  istage.load(irow, nslots, lane);
 
   // ---- Q^T B operands (16x16x32: lane holds head lt, dims 32 s + 8 hq ..) ---
   const bool hvalid = lt < p.G;
@@ -101,6 +100,7 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
 
+  istage.template store<PAGED>(p, b, bound, nslots, ntiles * 32, s_idx, lane);
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
 
   // Loads of tile j (keys 32 j .. 32 j + 31): operand i = 4 mt + s holds, for

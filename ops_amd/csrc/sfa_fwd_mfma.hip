@@ -164,6 +164,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // index row is staged and Q is loaded, instead of waiting for both.
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
   const int bound = bound_of(p, b);
+  // The item's index row is requested first (coalesced, all loads in
+  // flight), then the first tile's gather and Q: loads complete in order, so
+  // the wait for the index row covers nothing issued after it.
+  IdxStage<kIdxCap, C::kThreads> istage;
+  istage.load(irow, nslots, tid);
   {
     RG rg0;
     // (unconditional loads, all in flight together: slots past the split
@@ -177,33 +182,33 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
     for (int k = 0; k < RG::NI; ++k) rg0.issue(k, ksrc, s_k0, wave, lane);
   }
-  {
-    for (int i = tid; i < ntiles * C::NKT; i += C::kThreads)
-      s_idx[i] = (i < nslots) ? staged_id<PAGED>(p, b, irow[i], bound) : -1;
-  }
 
   // ---- Q^T B operands in registers ------------------------------------
   const int hl = slice * T + (lane % T);  // head within the group
   const bool hvalid = hl < p.G;
   bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
-  // (issued after the first tile's gather, so the two latencies overlap)
+  // (issued after the first tile's gather, so the two latencies overlap;
+  // the LDS-resident steps are written once the index row is staged)
+  bf16x8 ql[C::QL > 0 ? C::QL : 1];
   auto load_q = [&]() {
     const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
                        (int64_t)(g * p.G + (hvalid ? hl : 0)) * p.q_sh + 8 * (lane / T);
 #pragma unroll
-    for (int s = 0; s < C::QREG; ++s) {
+    for (int s = 0; s < C::QSTEPS; ++s) {
       bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + s * C::KD);
       if (!hvalid) x = bf16x8{};
-      qb[s] = x;
+      if (s < C::QREG)
+        qb[s < C::QREG ? s : 0] = x;
+      else
+        ql[s >= C::QREG ? s - C::QREG : 0] = x;
     }
-    // the remaining steps' operands go to LDS: head hl's row holds its chunks
-    // (step s, lane group j) at slot (s - QREG) * LG + j
+  };
+  // the LDS-resident steps: head hl's row holds its chunks (step s, lane
+  // group j) at slot (s - QREG) * LG + j
+  auto store_q = [&]() {
 #pragma unroll
-    for (int s = C::QREG; s < C::QSTEPS; ++s) {
-      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + s * C::KD);
-      if (!hvalid) x = bf16x8{};
-      *reinterpret_cast<bf16x8*>(&s_q[hl * C::QLP + (s - C::QREG) * C::LG + lane / T]) = x;
-    }
+    for (int s = C::QREG; s < C::QSTEPS; ++s)
+      *reinterpret_cast<bf16x8*>(&s_q[hl * C::QLP + (s - C::QREG) * C::LG + lane / T]) = ql[s - C::QREG];
   };
 
   // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
@@ -465,6 +470,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     if constexpr (Src::kUntrackedDma) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   };
   load_q();
+  istage.template store<PAGED>(p, b, bound, nslots, ntiles * C::NKT, s_idx, tid);
+  store_q();
   dma_done();
   __syncthreads();  // indices staged, first tile and the LDS part of Q in place
 

@@ -115,6 +115,12 @@ def count_valid_pairs(idx: torch.Tensor, Skv: int, kv_lens: Optional[torch.Tenso
     return int(valid_mask(idx, Skv, kv_lens).sum().item())
 
 
+def _gather_rows(rows: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """``rows[ids]`` for a 2-D ``rows`` (one index_select over the flattened
+    ids: the same values as advanced indexing, many times faster on the CPU)."""
+    return rows.index_select(0, ids.reshape(-1)).view(*ids.shape, rows.shape[-1])
+
+
 def _chunk_size(Sq, G, K, D, esize, max_chunk_bytes):
     per_q = K * D * esize * 3 + G * K * esize * 4
     return max(1, min(Sq, max_chunk_bytes // max(per_q, 1)))
@@ -158,8 +164,8 @@ def sfa_forward(
             vb = v[b, :, g].to(dtype)
             vm = valid[b, s0:s1, g]                                  # [C, K]
             safe = torch.where(vm, idx[b, s0:s1, g].long(), torch.zeros_like(vm, dtype=torch.long))
-            kg = kb[safe]                                           # [C, K, Dqk]  gather, SFA.py:407-415
-            vg = vb[safe]                                           # [C, K, Dv]
+            kg = _gather_rows(kb, safe)                             # [C, K, Dqk]  gather, SFA.py:407-415
+            vg = _gather_rows(vb, safe)                             # [C, K, Dv]
             qg = q[b, s0:s1, g * G:(g + 1) * G].to(dtype)          # [C, G, Dqk]
             s = torch.einsum("cgd,ckd->cgk", qg, kg) * scale        # SFA.py:425, 435
             s = s.masked_fill(~vm[:, None, :], -math.inf)          # SFA.py:436 (−1e11 there)
@@ -215,8 +221,8 @@ def sfa_backward(
                 s1 = min(Sq, s0 + C)
                 vm = valid[b, s0:s1, g]
                 safe = torch.where(vm, idx[b, s0:s1, g].long(), torch.zeros_like(vm, dtype=torch.long))
-                kg = kb[safe]
-                vg = vb[safe]
+                kg = _gather_rows(kb, safe)
+                vg = _gather_rows(vb, safe)
                 qg = q[b, s0:s1, g * G:(g + 1) * G].to(dtype)
                 og = out[b, s0:s1, g * G:(g + 1) * G].to(dtype)
                 dog = dout[b, s0:s1, g * G:(g + 1) * G].to(dtype)
