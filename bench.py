@@ -20,8 +20,9 @@ measured in the same run and reported under ``workloads``:
                   over the visible (query, key) pairs, 2 H d FLOP each);
                   ``layer_ms``: indexer + MLA forward on the indices it produced
                   (the whole sparse attention layer of the prefill)
-* ``mla_bwd``     shared-KV (MLA) backward at S=1024 (128 heads, d_qk 576 / d_v
-                  512, top-k 2048; TFLOP/s over valid pairs): generic kernels
+* ``mla_bwd``     shared-KV (MLA) backward at the full prefill shape (S=32768,
+                  128 heads, d_qk 576 / d_v 512, top-k 2048; TFLOP/s over valid
+                  pairs): dQ and the merged dK + dV of the shared rows
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -350,22 +351,22 @@ def bench_mla_decode(args):
 
 
 def bench_mla_bwd(args):
-    """Shared-KV (MLA) backward, d_qk 576 / d_v 512, 128 heads, top-k 2048,
-    at S = 1024: it runs on the generic kernels (no MLA-specific backward
-    yet), whose rate makes the full S = 32768 step take ~28 s."""
-    import torch
+    """Shared-KV (MLA) backward at the full prefill shape (S = 32768, 128
+    heads, d_qk 576 / d_v 512, top-k 2048): dQ and the gradient of the shared
+    rows (dK + dV, as the reference sums them, SFA.py:849-853) on the MFMA
+    path; TFLOP/s over valid pairs, pairs * G * 2 (3 d_qk + 2 d_v)."""
     import ops_amd
     from ops_amd.workloads import make_workload
-    S = 1024
-    w = make_workload("mla_prefill", device="cuda", S=S, with_dout=True)
+    w = make_workload("mla_prefill", device="cuda", with_dout=True)
     pairs = valid_pairs(w)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
-    bt, _ = time_steps(lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale), 2, 1)
+    fn = lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True)
+    bt, _ = time_steps(fn, max(2, args.steps // 4), 1)
     ms = sum(bt) / len(bt)
     tf = bwd_flops(w, pairs) / (ms * 1e-3) / 1e12
     return {"metric": "bwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
-            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "generic",
-            "config": {"B": 1, "S": S, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
+            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "mla_bwd_dq_kernel + mla_bwd_dkv_kernel (fp32 atomics)",
+            "config": {"B": 1, "S": 32768, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
 
 
 def bench_indexer(args, mla=None):
@@ -439,9 +440,9 @@ def profile_targets(name):
         kp, vp, bt = page_kv(w.k, w.v, 64, seed=1)
         return lambda: ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens=w.kv_lens), flush
     if name == "mla_bwd":
-        w = make_workload("mla_prefill", device="cuda", S=1024, with_dout=True)
+        w = make_workload("mla_prefill", device="cuda", with_dout=True)
         out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
-        return lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale), None
+        return lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True), None
     raise SystemExit(f"unknown --profile target {name!r}")
 
 

@@ -70,6 +70,15 @@ enum {
                           fixed order in every mode                                     */
 };
 
+/* sfa_bwd_args.flags */
+#define SFA_BWD_MERGE_KV 1  /* v is the first Dv dims of k's rows (v == k with k's strides, Dv <= Dqk),
+                               the reference's single shared kv (SFA.py:88, 116): dk receives the
+                               gradient of the shared rows, dK + dV on their first Dv dims, as
+                               SFA.py:849-853 sums both into one buffer; dv is not written and may
+                               be NULL.  The MLA shape (d_qk 576, d_v 512, 65..128 heads per KV head,
+                               bf16) then runs its MFMA backward (fp32 atomics; SFA_DKV_CSR is
+                               not available for it)                                              */
+
 /* Error codes. */
 enum {
   SFA_OK = 0,
@@ -104,7 +113,7 @@ typedef struct sfa_bwd_args {
   const float* dlse;             /* gradient w.r.t. lse, float32, lse's strides; NULL = 0 */
   float* dsink;                  /* [Hq] float32, written (not accumulated); NULL if no sink */
   int32_t dkv_mode;              /* SFA_DKV_*                                           */
-  int32_t flags;                 /* reserved, must be 0                                 */
+  int32_t flags;                 /* 0 or SFA_BWD_MERGE_KV                               */
 } sfa_bwd_args;
 
 /* Paged KV cache (block table) for sfa_fwd_paged.  k and v then point to
@@ -203,7 +212,8 @@ SFA_API size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a);
 SFA_API int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace sfa_bwd needs for `a` (fp32 dK/dV accumulators,
- * delta, and the CSR arrays in SFA_DKV_CSR mode).
+ * delta, the CSR arrays in SFA_DKV_CSR mode, and for the MLA backward the
+ * bf16 P / dS of a chunk of about 512 MiB of queries).
  * Replaces the workspaces of SFA.py:184-194 and SFA.py:253-261. */
 SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
 

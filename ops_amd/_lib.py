@@ -20,6 +20,7 @@ SFA_DTYPE_FP8_E4M3 = 2
 SFA_DKV_AUTO = 0
 SFA_DKV_ATOMIC = 1
 SFA_DKV_CSR = 2
+SFA_BWD_MERGE_KV = 1  # sfa_bwd_args.flags: dk receives dK + dV of rows k and v share
 
 SFA_OK = 0
 SFA_E_INVALID = -1

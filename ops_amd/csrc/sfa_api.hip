@@ -352,14 +352,45 @@ size_t bwd_base_bytes(const sfa_fwd_args& f) {
   return dk + dv + delta;
 }
 
+bool merge_kv(const sfa_bwd_args* a) { return (a->flags & SFA_BWD_MERGE_KV) != 0; }
+
+// The MLA shared-KV backward: merged gradient, bf16 MFMA layout, MLA shape.
+bool use_mla(const sfa_bwd_args* a, const sfa::Params& p) {
+  if (!(merge_kv(a) && a->dkv_mode != SFA_DKV_CSR && bwd_mfma_ok(a) && sfa::bwd_mla_supported(p))) return false;
+  // the dK/dV pass stages the query's G head rows of q and dout through
+  // 32-bit buffer offsets
+  const int64_t lim = (int64_t)0x80000000LL;
+  return (int64_t)(p.G - 1) * 2 * a->fwd.q_sh + 2 * 576 < lim && (int64_t)(p.G - 1) * 2 * a->do_sh + 2 * 512 < lim;
+}
+
+// Its P / dS workspace holds one chunk of work items (a multiple of 8, so the
+// dQ pass can place both head groups of an item on one XCD).
+constexpr size_t kMlaChunkBytes = size_t(512) << 20;
+
+int mla_chunk_items(const sfa::Params& p) {
+  const int64_t items = (int64_t)p.B * p.Sq * p.Hkv;
+  int64_t n = (int64_t)(kMlaChunkBytes / sfa::bwd_mla_pd_bytes_per_item(p));
+  n = n / 8 * 8;
+  if (n < 8) n = 8;
+  return (int)(n < items ? n : items);
+}
+
+// MLA workspace: fp32 shared-row accumulators | delta | P / dS chunk
+size_t mla_bytes(const sfa_fwd_args& f, const sfa::Params& p) {
+  const size_t dk = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dqk * sizeof(float), 256);
+  const size_t delta = align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
+  return dk + delta + align_up((size_t)mla_chunk_items(p) * sfa::bwd_mla_pd_bytes_per_item(p), 256);
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t sfa_bwd_workspace_size(const sfa_bwd_args* a) {
   if (a == nullptr || check_fwd(&a->fwd) != SFA_OK) return 0;
-  size_t n = bwd_base_bytes(a->fwd);
   sfa::Params p = to_params(&a->fwd);
+  if (use_mla(a, p)) return mla_bytes(a->fwd, p);
+  size_t n = bwd_base_bytes(a->fwd);
   if (use_csr(a, p)) {
     sfa::csr_geometry(p);
     n += sfa::csr_workspace_bytes(p);
@@ -373,9 +404,12 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   int rc = check_fwd(&a->fwd);
   if (rc != SFA_OK) return rc;
   const sfa_fwd_args& f = a->fwd;
-  if (!a->dout || !a->dq || !a->dk || !a->dv) return fail(SFA_E_INVALID, "null gradient pointer");
+  if ((a->flags & ~SFA_BWD_MERGE_KV) != 0) return fail(SFA_E_INVALID, "unknown flags 0x%x", (unsigned)a->flags);
+  const bool merge = merge_kv(a);
+  if (!a->dout || !a->dq || !a->dk || (!merge && !a->dv)) return fail(SFA_E_INVALID, "null gradient pointer");
   if (f.sink && !a->dsink) return fail(SFA_E_INVALID, "dsink is required when sink is given");
-  if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if (merge && !(f.v == f.k && f.v_sb == f.k_sb && f.v_ss == f.k_ss && f.v_sh == f.k_sh && f.Dv <= f.Dqk))
+    return fail(SFA_E_INVALID, "SFA_BWD_MERGE_KV needs v to be the first Dv dims of k's rows");
   if (a->dkv_mode != SFA_DKV_AUTO && a->dkv_mode != SFA_DKV_ATOMIC && a->dkv_mode != SFA_DKV_CSR)
     return fail(SFA_E_INVALID, "unknown dkv_mode %d", a->dkv_mode);
   const size_t need = sfa_bwd_workspace_size(a);
@@ -383,6 +417,26 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
     return fail(SFA_E_WORKSPACE, "sfa_bwd needs %zu workspace bytes (got %zu)", need, workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
   sfa::Params p = to_params(&f);
+  if (use_mla(a, p)) {
+    p.dout = a->dout; p.do_sb = a->do_sb; p.do_ss = a->do_ss; p.do_sh = a->do_sh;
+    p.dq = a->dq; p.dq_sb = a->dq_sb; p.dq_ss = a->dq_ss; p.dq_sh = a->dq_sh;
+    const size_t nk = (size_t)f.B * f.Skv * f.Hkv * f.Dqk;
+    p.dk_acc = (float*)workspace;
+    p.delta = (float*)((char*)workspace + align_up(nk * sizeof(float), 256));
+    void* pd = (char*)p.delta + align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
+    p.dsink = a->dsink;
+    p.dlse = a->dlse;
+    hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
+    const int64_t items = (int64_t)f.B * f.Sq * f.Hkv;
+    const int chunk = mla_chunk_items(p);
+    for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk)
+      e = sfa::launch_bwd_mla_chunk(p, i0, (int)(items - i0 < chunk ? items - i0 : chunk), pd, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, false, s);
+    if (e != hipSuccess) return hip_fail(e, "sfa_bwd (mla)");
+    return SFA_OK;
+  }
   const bool csr = use_csr(a, p);
   if (a->dkv_mode == SFA_DKV_CSR && !csr)
     return fail(SFA_E_UNSUPPORTED,
@@ -417,9 +471,13 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
       e = sfa::launch_bwd_generic(p, f.dtype, s);
   }
   if (e == hipSuccess && csr) e = sfa::launch_csr_dkv(p, s);
-  if (e == hipSuccess)
-    e = sfa::launch_bwd_finish(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, a->dv, a->dv_sb, a->dv_ss, a->dv_sh,
-                               s);
+  if (e == hipSuccess) {
+    if (merge)
+      e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, true, s);
+    else
+      e = sfa::launch_bwd_finish(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, a->dv, a->dv_sb, a->dv_ss,
+                                 a->dv_sh, s);
+  }
   if (e != hipSuccess) return hip_fail(e, "sfa_bwd");
   return SFA_OK;
 }

@@ -205,6 +205,10 @@ hipError_t launch_bwd_delta(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_bwd_dsink(const Params& p, hipStream_t s);  // after launch_bwd_delta
 hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss, int64_t dk_sh,
                              void* dv, int64_t dv_sb, int64_t dv_ss, int64_t dv_sh, hipStream_t s);
+// shared K/V rows: dk = dK (+ dV on the first Dv dims when add_dv; the MLA
+// backward accumulates both into dk_acc itself)
+hipError_t launch_bwd_finish_merged(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss,
+                                    int64_t dk_sh, bool add_dv, hipStream_t s);
 hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
 // MFMA paths: return hipErrorNotSupported when the shape has no variant.
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);  // paged when p.block_table != nullptr
@@ -216,6 +220,11 @@ int fwd_d128_tile_keys();
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
+// MLA shared-KV backward (sfa_bwd_mla.hip): dQ pass + dK/dV pass over a chunk
+// of work items, P / dS of the chunk in `pd` (bwd_mla_pd_bytes_per_item each)
+bool bwd_mla_supported(const Params& p);
+size_t bwd_mla_pd_bytes_per_item(const Params& p);
+hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
 bool bwd_dq_supported(const Params& p);
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s);

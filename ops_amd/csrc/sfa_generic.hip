@@ -276,6 +276,16 @@ __global__ void finish_kernel(const float* acc, int B, int Skv, int Hkv, int D, 
   }
 }
 
+// Shared K/V rows (v = the first Dv dims of k): dk_acc[r][d] += dv_acc[r][d]
+// for d < Dv, so one finish writes the gradient of the shared rows.
+__global__ void add_rows_kernel(float* dk, const float* dv, int64_t rows, int Dk, int Dv) {
+  const int64_t n = rows * Dv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / Dv;
+    dk[r * Dk + (i - r * Dv)] += dv[i];
+  }
+}
+
 // Split-k combine: lse2 = log2 Σ_s 2^lse2_s, out = Σ_s 2^(lse2_s - lse2)·o_s
 // (o_s the bf16 normalised partial of split s, accumulated in fp32),
 // then the optional sink joins the denominator.  One wave per (b, t, h) row:
@@ -427,6 +437,21 @@ hipError_t launch_bwd_finish(const Params& p, int dtype, void* dk, int64_t dk_sb
     hipLaunchKernelGGL(finish_kernel<bf16>, dim3(grid_for(nv, 256 * 4)), dim3(256), 0, s, p.dv_acc, p.B, p.Skv,
                        p.Hkv, p.Dv, (bf16*)dv, dv_sb, dv_ss, dv_sh);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_finish_merged(const Params& p, int dtype, void* dk, int64_t dk_sb, int64_t dk_ss,
+                                    int64_t dk_sh, bool add_dv, hipStream_t s) {
+  const int64_t rows = (int64_t)p.B * p.Skv * p.Hkv, nk = rows * p.Dqk;
+  if (add_dv)
+    hipLaunchKernelGGL(add_rows_kernel, dim3(grid_for(rows * p.Dv, 256 * 4)), dim3(256), 0, s, p.dk_acc, p.dv_acc, rows,
+                       p.Dqk, p.Dv);
+  if (dtype == SFA_DTYPE_F32)
+    hipLaunchKernelGGL(finish_kernel<float>, dim3(grid_for(nk, 256 * 4)), dim3(256), 0, s, p.dk_acc, p.B, p.Skv,
+                       p.Hkv, p.Dqk, (float*)dk, dk_sb, dk_ss, dk_sh);
+  else
+    hipLaunchKernelGGL(finish_kernel<bf16>, dim3(grid_for(nk, 256 * 4)), dim3(256), 0, s, p.dk_acc, p.B, p.Skv,
+                       p.Hkv, p.Dqk, (bf16*)dk, dk_sb, dk_ss, dk_sh);
   return hipGetLastError();
 }
 

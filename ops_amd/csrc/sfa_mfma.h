@@ -87,6 +87,69 @@ struct Mfma<32> {
   }
 };
 
+// Inline-asm 16x16x32 bf16 MFMAs with the accumulator pinned to AGPRs, for
+// kernels whose accumulators do not fit next to their operands in the VGPR
+// file.  The hazard rules are those of Mfma<32> above: NOP = true when an
+// operand may just have been written by a VALU instruction, the previous
+// MFMA's operands are passed along so their registers stay live until this
+// one has issued, tail() after the last MFMA of a sequence, drain() before a
+// VALU (or v_accvgpr_read) use of a result.  mma_b_agpr takes its B operand
+// from AGPRs (gfx950 MFMAs read A/B from either file).
+struct Mfma16A {
+  typedef f32x4 acc_t;
+  template <bool NOP>
+  static __device__ __forceinline__ void mma(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
+    if constexpr (NOP)
+      asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                   : "+a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+  }
+  // c = a b: a fresh accumulator (srcC = 0), so no VALU write of c precedes it
+  static __device__ __forceinline__ void mma0(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa, const bf16x8& pb) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                 : "=&a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
+  }
+  static __device__ __forceinline__ void mma_b_agpr(bf16x8 a, const bf16x8& b, acc_t& c, const bf16x8& pa) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "a"(b), "v"(pa) : "memory");
+  }
+  // VGPR accumulators: c = a b (fresh) and c += a b, with B in VGPRs or AGPRs
+  static __device__ __forceinline__ void mma_v0(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b), "v"(pa) : "memory");
+  }
+  static __device__ __forceinline__ void mma_v(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b), "v"(pa) : "memory");
+  }
+  // c += a b with b just written by a VALU instruction
+  static __device__ __forceinline__ void mma_vn(bf16x8 a, bf16x8 b, acc_t& c, const bf16x8& pa) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b), "v"(pa) : "memory");
+  }
+  static __device__ __forceinline__ void drain_v1(acc_t& c) { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(c)); }
+  static __device__ __forceinline__ void mma_v0_ba(bf16x8 a, const bf16x8& b, acc_t& c, const bf16x8& pa) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "a"(b), "v"(pa) : "memory");
+  }
+  static __device__ __forceinline__ void mma_v_ba(bf16x8 a, const bf16x8& b, acc_t& c, const bf16x8& pa) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "a"(b), "v"(pa) : "memory");
+  }
+  // wait states between the last MFMA writing VGPR accumulators and VALU reads
+  static __device__ __forceinline__ void drain_v4(acc_t& c0, acc_t& c1, acc_t& c2, acc_t& c3) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+  }
+  static __device__ __forceinline__ void tail(const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 7" : : "v"(a), "v"(b));
+  }
+  static __device__ __forceinline__ void tail1(const bf16x8& a) { asm volatile("s_nop 7" : : "v"(a)); }
+  static __device__ __forceinline__ void drain(acc_t& c) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(c));
+  }
+  // bf16x8 operand kept in AGPRs (v_accvgpr_write of a VGPR value)
+  static __device__ __forceinline__ bf16x8 to_agpr(bf16x8 x) {
+    asm volatile("" : "+a"(x));
+    return x;
+  }
+};
+
 template <>
 struct Mfma<16> {
   typedef f32x4 acc_t;

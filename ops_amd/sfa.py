@@ -209,12 +209,32 @@ def sfa_forward_paged(q, k_cache, v_cache, block_table, topk_idxs, sm_scale=None
     return out, lse
 
 
+def _is_prefix_view(k: torch.Tensor, v: torch.Tensor) -> bool:
+    """v is the first v.shape[-1] dims of k's rows (same memory and strides)."""
+    return (v.data_ptr() == k.data_ptr() and v.dim() == k.dim() == 4 and v.stride()[:3] == k.stride()[:3]
+            and v.shape[:3] == k.shape[:3] and v.shape[3] <= k.shape[3] and v.stride(-1) == k.stride(-1))
+
+
 def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None, attn_sink=None,
-                 dlse: Optional[torch.Tensor] = None, dkv_mode: Optional[str] = None):
+                 dlse: Optional[torch.Tensor] = None, dkv_mode: Optional[str] = None, merge_kv: bool = False):
     """Backward only (no autograd): ``(dq, dk, dv, dsink)``; ``dsink`` is None
-    without a sink."""
+    without a sink.
+
+    ``merge_kv=True`` (``v`` must be the first ``Dv`` dims of ``k``'s rows,
+    e.g. MLA's ``kv[..., :512]``): ``dk`` is the gradient of the shared rows,
+    dK + dV on their first ``Dv`` dims, as the reference sums both into one
+    buffer (SFA.py:849-853), and ``dv`` is None.  The MLA shape (576 / 512,
+    65..128 heads per KV head, bf16) then runs its MFMA backward."""
     lib = _lib.load()
-    q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
+    if merge_kv:
+        if not _is_prefix_view(k, v):
+            raise ValueError("merge_kv needs v to be the first Dv dims of k's rows (a prefix view of k)")
+        _validate(q, k, v, topk_idxs, kv_lens, attn_sink)
+        k = _rows(k)
+        v = k[..., : v.shape[3]]
+        q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink, validate=False)
+    else:
+        q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
     B, Sq, Hq, Dqk = q.shape
     _, Skv, Hkv, _ = k.shape
     Dv = v.shape[3]
@@ -229,7 +249,7 @@ def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None
         raise ValueError(f"dkv_mode must be one of {sorted(_DKV_MODES)}")
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty((B, Skv, Hkv, Dqk), dtype=q.dtype, device=q.device)
-    dv = torch.empty((B, Skv, Hkv, Dv), dtype=q.dtype, device=q.device)
+    dv = None if merge_kv else torch.empty((B, Skv, Hkv, Dv), dtype=q.dtype, device=q.device)
     dsink = torch.empty((Hq,), dtype=torch.float32, device=q.device) if sink is not None else None
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
@@ -238,11 +258,12 @@ def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None
     a.dout, (a.do_sb, a.do_ss, a.do_sh) = dout.data_ptr(), dout.stride()[:3]
     a.dq, (a.dq_sb, a.dq_ss, a.dq_sh) = dq.data_ptr(), dq.stride()[:3]
     a.dk, (a.dk_sb, a.dk_ss, a.dk_sh) = dk.data_ptr(), dk.stride()[:3]
-    a.dv, (a.dv_sb, a.dv_ss, a.dv_sh) = dv.data_ptr(), dv.stride()[:3]
+    if dv is not None:
+        a.dv, (a.dv_sb, a.dv_ss, a.dv_sh) = dv.data_ptr(), dv.stride()[:3]
     a.dlse = dlse.data_ptr() if dlse is not None else None
     a.dsink = dsink.data_ptr() if dsink is not None else None
     a.dkv_mode = _DKV_MODES[mode]
-    a.flags = 0
+    a.flags = _lib.SFA_BWD_MERGE_KV if merge_kv else 0
     ws = lib.sfa_bwd_workspace_size(ctypes.byref(a))
     wbuf = torch.empty(ws, dtype=torch.uint8, device=q.device) if ws else None
     stream = torch.cuda.current_stream(q.device).cuda_stream
@@ -274,8 +295,11 @@ class SparseFlashAttention(torch.autograd.Function):
         q, k, v, idx, out, lse, kv_lens, sink = ctx.saved_tensors
         if grad_out is None:
             grad_out = torch.zeros_like(out)
+        # v a prefix view of k (MLA's shared kv): the merged gradient of the
+        # shared rows goes to k, nothing to v (autograd sums both into the
+        # same storage anyway)
         dq, dk, dv, dsink = sfa_backward(q, k, v, idx, out, lse, grad_out, ctx.sm_scale, kv_lens, sink,
-                                         dlse=grad_lse)
+                                         dlse=grad_lse, merge_kv=_is_prefix_view(k, v))
         if dsink is not None and sink is not None:
             dsink = dsink.to(sink.dtype)
         return dq, dk, dv, None, None, None, dsink
@@ -318,9 +342,9 @@ class SparseFlashAttentionSBHD(torch.autograd.Function):
         qb = q.permute(1, 0, 2, 3)
         kb = kv.permute(1, 0, 2).unsqueeze(2)
         idx = topk_idxs.permute(1, 0, 2).unsqueeze(2)
-        dq, dk, dv, dsink = sfa_backward(qb, kb, kb, idx, out, lse, grad_out.permute(1, 0, 2, 3), ctx.sm_scale,
-                                         attn_sink=sink)
-        grad_kv = (dk.float() + dv.float()).to(kv.dtype).squeeze(2).permute(1, 0, 2)
+        dq, dk, _, dsink = sfa_backward(qb, kb, kb, idx, out, lse, grad_out.permute(1, 0, 2, 3), ctx.sm_scale,
+                                        attn_sink=sink, merge_kv=True)
+        grad_kv = dk.squeeze(2).permute(1, 0, 2)
         if dsink is not None and sink is not None:
             dsink = dsink.to(sink.dtype)
         return dq.permute(1, 0, 2, 3), grad_kv, dsink, None, None

@@ -444,12 +444,12 @@ def test_reference_signature_shim():
         assert _rel_l2(sink.grad.cpu(), ds) <= GRAD_RL2
 
 
-def test_mla_shared_kv_backward_generic():
+def test_mla_shared_kv_backward_autograd():
     """The MLA training shape (one latent KV row per token, d_qk 576, V = its
-    first 512 dims, G = 128): through autograd the shared kv's gradient is
-    dK + dV (the reference sums both into one buffer, SFA.py:849-853).  It
-    runs on the generic kernels (correct, not a performance path)."""
-    _say("MLA shared-kv backward B=1 S=48 Hq=128 d 576/512 K=24 (generic kernels)")
+    first 512 dims, G = 128): through autograd (v a prefix view of kv, so the
+    backward takes the merged MFMA path) the shared kv's gradient is dK + dV
+    (the reference sums both into one buffer, SFA.py:849-853)."""
+    _say("MLA shared-kv backward B=1 S=48 Hq=128 d 576/512 K=24 (autograd, merged MFMA path)")
     g = torch.Generator(device=DEV).manual_seed(5)
     B, S, H, K = 1, 48, 128, 24
     q = torch.randn(B, S, H, 576, device=DEV, generator=g).bfloat16().requires_grad_(True)
