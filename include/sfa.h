@@ -76,8 +76,10 @@ enum {
                                gradient of the shared rows, dK + dV on their first Dv dims, as
                                SFA.py:849-853 sums both into one buffer; dv is not written and may
                                be NULL.  The MLA shape (d_qk 576, d_v 512, 65..128 heads per KV head,
-                               bf16) then runs its MFMA backward (fp32 atomics; SFA_DKV_CSR is
-                               not available for it)                                              */
+                               bf16) then runs its MFMA backward: AUTO and SFA_DKV_CSR sum per-slot
+                               bf16 rows of the shared rows' gradient in a fixed order (Skv <= 65536;
+                               slots repeating a key of their row take fp32 atomics), SFA_DKV_ATOMIC
+                               adds every slot's fp32 row atomically                              */
 
 /* Error codes. */
 enum {

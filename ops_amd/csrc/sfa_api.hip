@@ -356,30 +356,39 @@ bool merge_kv(const sfa_bwd_args* a) { return (a->flags & SFA_BWD_MERGE_KV) != 0
 
 // The MLA shared-KV backward: merged gradient, bf16 MFMA layout, MLA shape.
 bool use_mla(const sfa_bwd_args* a, const sfa::Params& p) {
-  if (!(merge_kv(a) && a->dkv_mode != SFA_DKV_CSR && bwd_mfma_ok(a) && sfa::bwd_mla_supported(p))) return false;
+  if (!(merge_kv(a) && bwd_mfma_ok(a) && sfa::bwd_mla_supported(p))) return false;
   // the dK/dV pass stages the query's G head rows of q and dout through
   // 32-bit buffer offsets
   const int64_t lim = (int64_t)0x80000000LL;
   return (int64_t)(p.G - 1) * 2 * a->fwd.q_sh + 2 * 576 < lim && (int64_t)(p.G - 1) * 2 * a->do_sh + 2 * 512 < lim;
 }
 
-// Its P / dS workspace holds one chunk of work items (a multiple of 8, so the
-// dQ pass can place both head groups of an item on one XCD).
-constexpr size_t kMlaChunkBytes = size_t(512) << 20;
+// Its deterministic dK/dV (index maps + ordered reduction of bf16 per-slot
+// rows) is used unless atomics are asked for or Skv exceeds its bitmap.
+bool mla_det(const sfa_bwd_args* a, const sfa::Params& p) {
+  return a->dkv_mode != SFA_DKV_ATOMIC && sfa::bwd_mla_det_supported(p);
+}
 
-int mla_chunk_items(const sfa::Params& p) {
+// Its workspace holds one chunk of work items (P / dS, and the contribution
+// rows and index maps when deterministic): up to about 2 GiB, in whole rounds
+// of 256 items (one dK/dV workgroup per CU of the 256-CU part; a partial
+// last round would leave most CUs idle), at least 8 items so the dQ pass can
+// place both head groups of an item on one XCD.
+constexpr size_t kMlaChunkBytes = size_t(2) << 30;
+constexpr int64_t kMlaChunkRound = 256;
+
+int mla_chunk_items(const sfa::Params& p, bool det) {
   const int64_t items = (int64_t)p.B * p.Sq * p.Hkv;
-  int64_t n = (int64_t)(kMlaChunkBytes / sfa::bwd_mla_pd_bytes_per_item(p));
-  n = n / 8 * 8;
-  if (n < 8) n = 8;
+  int64_t n = (int64_t)(kMlaChunkBytes / sfa::bwd_mla_bytes_per_item(p, det));
+  n = n >= kMlaChunkRound ? n / kMlaChunkRound * kMlaChunkRound : (n / 8 * 8 > 8 ? n / 8 * 8 : 8);
   return (int)(n < items ? n : items);
 }
 
-// MLA workspace: fp32 shared-row accumulators | delta | P / dS chunk
-size_t mla_bytes(const sfa_fwd_args& f, const sfa::Params& p) {
+// MLA workspace: fp32 shared-row accumulators | delta | chunk
+size_t mla_bytes(const sfa_fwd_args& f, const sfa::Params& p, bool det) {
   const size_t dk = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dqk * sizeof(float), 256);
   const size_t delta = align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
-  return dk + delta + align_up((size_t)mla_chunk_items(p) * sfa::bwd_mla_pd_bytes_per_item(p), 256);
+  return dk + delta + align_up((size_t)mla_chunk_items(p, det) * sfa::bwd_mla_bytes_per_item(p, det), 256);
 }
 
 }  // namespace
@@ -389,7 +398,7 @@ extern "C" {
 size_t sfa_bwd_workspace_size(const sfa_bwd_args* a) {
   if (a == nullptr || check_fwd(&a->fwd) != SFA_OK) return 0;
   sfa::Params p = to_params(&a->fwd);
-  if (use_mla(a, p)) return mla_bytes(a->fwd, p);
+  if (use_mla(a, p)) return mla_bytes(a->fwd, p, mla_det(a, p));
   size_t n = bwd_base_bytes(a->fwd);
   if (use_csr(a, p)) {
     sfa::csr_geometry(p);
@@ -429,10 +438,13 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
     hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
     if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
     if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
+    const bool det = mla_det(a, p);
+    if (a->dkv_mode == SFA_DKV_CSR && !det)
+      return fail(SFA_E_UNSUPPORTED, "the deterministic MLA backward supports Skv <= 65536 (got %d)", f.Skv);
     const int64_t items = (int64_t)f.B * f.Sq * f.Hkv;
-    const int chunk = mla_chunk_items(p);
+    const int chunk = mla_chunk_items(p, det);
     for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk)
-      e = sfa::launch_bwd_mla_chunk(p, i0, (int)(items - i0 < chunk ? items - i0 : chunk), pd, s);
+      e = sfa::launch_bwd_mla_chunk(p, i0, (int)(items - i0 < chunk ? items - i0 : chunk), pd, det, s);
     if (e == hipSuccess) e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, false, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_bwd (mla)");
     return SFA_OK;

@@ -309,16 +309,90 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
 }
 
 // ---------------------------------------------------------------------------
+// Index maps of a chunk (deterministic dK/dV): per work item, the membership
+// bitmap of its valid keys (bit k of word k >> 5), the number of set bits in
+// the words before each word (so a key's rank among the item's distinct keys
+// in ascending order is prefix[w] + popc(word & below)), and a flag per slot
+// that repeats a key an earlier slot of the row already selected.
+// ---------------------------------------------------------------------------
+constexpr int kMaxMapW = 2048;  // bitmap words per item: Skv <= 65536
+
+__global__ __launch_bounds__(256) void mla_map_kernel(Params p, int64_t item0, int nitems, int W, uint32_t* kmap,
+                                                      uint16_t* prefix, uint8_t* dup) {
+  __shared__ uint32_t s_map[4][kMaxMapW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = blockIdx.x * 4 + wave;
+  if (li >= nitems) return;  // the whole wave
+  const int64_t item = item0 + li;
+  const int g = (int)(item % p.Hkv);
+  const int t = (int)((item / p.Hkv) % p.Sq);
+  const int b = (int)(item / ((int64_t)p.Hkv * p.Sq));
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
+  uint32_t* map = s_map[wave];
+  for (int w = lane; w < W; w += 64) map[w] = 0u;
+  __builtin_amdgcn_wave_barrier();
+  uint8_t* drow = dup + (int64_t)li * p.topk;
+  for (int s0 = 0; s0 < p.topk; s0 += 64) {
+    const int s = s0 + lane;
+    const int id = s < p.topk ? irow[s] : -1;
+    // exactly one slot of each distinct key finds its bit clear (the first
+    // atomicOr to set it); every other slot of that key is a repeat
+    uint8_t rep = 0;
+    if (id >= 0 && id < bound) {
+      const uint32_t bit = 1u << (id & 31);
+      rep = (atomicOr(&map[id >> 5], bit) & bit) ? 1 : 0;
+    }
+    if (s < p.topk) drow[s] = rep;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // prefix popcounts: lane l sums words [l W/64, (l + 1) W/64), then a wave scan
+  const int per = W / 64;  // W is a multiple of 64
+  int cnt = 0;
+  for (int i = 0; i < per; ++i) cnt += __builtin_popcount(map[lane * per + i]);
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  int run = incl - cnt;
+  uint32_t* mrow = kmap + (int64_t)li * W;
+  uint16_t* prow = prefix + (int64_t)li * W;
+  for (int i = 0; i < per; ++i) {
+    const uint32_t x = map[lane * per + i];
+    mrow[lane * per + i] = x;
+    prow[lane * per + i] = (uint16_t)run;
+    run += __builtin_popcount(x);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // dK/dV pass
 // ---------------------------------------------------------------------------
 constexpr int kQP = 73;   // LDS row pitch (16-byte slots) of the staged Q rows: conflict-free transposing reads
 constexpr int kDP = 66;   // of the staged dO rows
+constexpr int kCP = 73;   // of the staged contribution rows (576 bf16)
 constexpr int kMaxG = 128;
-constexpr int kDN = 9;    // 16-dim column tiles per wave (dims 144 w .. 144 w + 143)
+constexpr int kDN = 9;    // 16-dim tiles per wave (dims 144 w .. 144 w + 143)
 constexpr int kHS = 4;    // 32-head contraction steps over 128 heads
+constexpr int kRankRepeat = -2;  // a slot repeating an earlier slot's key (fp32 atomics)
 
-__global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int64_t item0, const bf16* pd) {
-  constexpr int kStage = kMaxG * kQP;  // 16-byte slots: Q rows, then dO rows, then the P / dS tiles
+// Per 32-key tile the product dKV^T = Q^T (scale dS) + dO^T P (dims as MFMA
+// rows, keys as columns, heads as the contraction) leaves each lane 4
+// consecutive dims of one key.
+//  * DET: the bf16 rows go through a double-buffered LDS stage into the
+//    chunk's contribution rows, row rank(key) of the item (the key's place
+//    among the item's distinct valid keys, ascending); slots that repeat a key
+//    add fp32 atomics into the accumulators instead.  mla_bwd_reduce_kernel
+//    then sums the rows of each key in item order.
+//  * !DET: every slot's fp32 row is added with atomics.
+template <bool DET>
+__global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int64_t item0, const bf16* pd,
+                                                                   bf16* contrib, const uint32_t* kmap,
+                                                                   const uint16_t* prefix, const uint8_t* dup,
+                                                                   int W) {
+  constexpr int kStage = kMaxG * kQP;  // 16-byte slots: Q rows, then dO rows, then P / dS tiles and output rows
   __shared__ u32x4 s_stage[kStage];
   __shared__ int s_idx[kMIdxCap];
 
@@ -340,7 +414,7 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   IdxStage<kMIdxCap, kMThreads> istage;
   istage.load(irow, nslots, tid);
 
-  // ---- Q and dO of the query's heads, as B operands over heads ----------
+  // ---- Q and dO of the query's heads, as A operands over heads ----------
   // (lane: dim 144 w + 16 n + lt, heads 32 ks + 8 hq .. +7; read from the
   // staged [head][dim] rows with two transposing reads of 4 heads each)
   const bf16* q0 = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)(g * p.G) * p.q_sh;
@@ -348,7 +422,7 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   bf16x8 qB[kDN][kHS];
   bf16x8 dB[kDN][kHS];
   const int dim0 = 144 * wave;
-  const int ndv = wave < 3 ? kDN : 5;  // column tiles with dims < 512
+  const int ndv = wave < 3 ? kDN : 5;  // dim tiles below 512
   // rows [G][nch 16-byte chunks] (row stride sh elements) into LDS rows of
   // `pitch` slots by DMA (all in flight at once); pad slots and rows >= G
   // read an out-of-range offset and get zeros
@@ -388,13 +462,51 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   for (int n = 0; n < kDN; ++n)
 #pragma unroll
     for (int ks = 0; ks < kHS; ++ks) dB[n][ks] = Mfma16A::to_agpr(n < ndv ? read_b(kDP, n, ks) : bf16x8{});
-  __syncthreads();  // the stage area now holds P / dS tiles
+  __syncthreads();  // the stage area now holds P / dS tiles, output rows and ranks
+
+  // ---- LDS layout of the tile loop (16-byte slots of s_stage) -------------
+  // [0, 2048): P / dS tiles (2 x 1024); [2048, 2048 + 2 * 32 * kCP): output
+  // rows (2 x 32 rows); then the ranks of the item's slots (DET)
+  constexpr int kOutBase = 2048;
+  constexpr int kRankBase = kOutBase + 2 * kMT * kCP;
+  static_assert(kRankBase + kMIdxCap / 4 <= kStage, "tile-loop LDS fits the stage area");
+  int* s_rank = reinterpret_cast<int*>(s_stage + kRankBase);
+  if constexpr (DET) {
+    // rank of each slot's key among the item's distinct keys (ascending),
+    // -1 for an invalid slot, kRankRepeat for a repeat
+    const uint32_t* mrow = kmap + (int64_t)li * W;
+    const uint16_t* prow = prefix + (int64_t)li * W;
+    const uint8_t* drow = dup + (int64_t)li * p.topk;
+    constexpr int IPT = kMIdxCap / kMThreads;
+    int ids[IPT];
+    uint32_t words[IPT];
+    int pre[IPT];
+    uint8_t rep[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int sl = tid + j * kMThreads;
+      ids[j] = sl < ntiles * kMT ? s_idx[sl] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int id = ids[j] >= 0 ? ids[j] : 0;
+      words[j] = mrow[id >> 5];
+      pre[j] = prow[id >> 5];
+      rep[j] = (tid + j * kMThreads < nslots) ? drow[tid + j * kMThreads] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int id = ids[j];
+      int r = -1;
+      if (id >= 0) r = rep[j] ? kRankRepeat : pre[j] + __builtin_popcount(words[j] & ((1u << (id & 31)) - 1u));
+      s_rank[tid + j * kMThreads] = r;
+    }
+  }
 
   // ---- P / dS tiles: DMA of the dQ pass's blocks into LDS -----------------
-  // one tile = 2 matrices x nhg head groups x 4 waves blocks of 1 KiB
-  const int tile_slots = 2 * nhg * 4 * 64;  // 16-byte slots per tile
+  const int tile_slots = 2 * nhg * 4 * 64;  // 16-byte slots per tile (<= 1024)
   u32x4* buf0 = s_stage;
-  u32x4* buf1 = s_stage + 2 * 2 * 4 * 64;
+  u32x4* buf1 = s_stage + 1024;
   const char* pd_item = reinterpret_cast<const char*>(pd + (int64_t)li * ntiles * 2 * nhg * 4 * pd_block_elems());
   const __amdgpu_buffer_rsrc_t rpd = make_rsrc(pd_item, (uint32_t)((int64_t)ntiles * tile_slots * 16));
   auto load_tile = [&](int tile, u32x4* dst) {
@@ -405,11 +517,12 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
 
   float* const dkv = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 576;
   const int64_t acc_row = (int64_t)p.Hkv * 576;
+  bf16* const crow0 = DET ? contrib + (int64_t)li * p.topk * 576 : nullptr;
 
-  // A operands (keys 16 mt + lt, heads 32 ks + 8 hq .. +7) of matrix mat:
+  // B operands (keys 16 nt + lt, heads 32 ks + 8 hq .. +7) of matrix mat:
   // heads 32 ks + 8 hq + 4 half + rr live in head group (32 ks + 8 hq) / 64,
   // wave ((32 ks + 8 hq) % 64) / 16, head 8 (hq & 1) + 4 half + rr of it
-  auto read_a = [&](const u32x4* tb, int mat, int mt, int ks) -> bf16x8 {
+  auto read_pd = [&](const u32x4* tb, int mat, int nt, int ks) -> bf16x8 {
     const int rr = lt >> 2, cc = lt & 3;
     const int hh = 32 * ks + 8 * hq;
     const int blk = (mat * nhg + hh / 64) * 4 + (hh % 64) / 16;
@@ -417,7 +530,7 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int src_lane = 16 * cc + 8 * (hq & 1) + 4 * half + rr;
-      const uint32_t o = (uint32_t)(blk * 64 + pd_pos(src_lane)) * 16u + (uint32_t)mt * 8u;
+      const uint32_t o = (uint32_t)(blk * 64 + pd_pos(src_lane)) * 16u + (uint32_t)nt * 8u;
       part[half] = lds_read_tr16(tb, o);
     }
     return bf16x8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
@@ -430,48 +543,170 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
     if (j + 1 < ntiles) load_tile(j + 1, (j & 1) ? buf0 : buf1);
     // (the first contraction step starts each accumulator from 0 inside the
     // MFMA: no VALU write of an accumulator precedes its MFMA)
-    Mfma16A::acc_t acc[2][kDN];
+    // DET: dims as MFMA rows (lane: dims dim0 + 16 n + 4 hq .. +3 of key
+    // 16 nt + lt: 8-byte row pieces for the staged rows); atomics: keys as
+    // rows (lane: keys 16 nt + 4 hq + i of dim dim0 + 16 n + lt: each atomic
+    // instruction covers 4 keys x 16 contiguous dims)
+    Mfma16A::acc_t acc[kDN][2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int ks = 0; ks < kHS; ++ks) {
-        const bf16x8 as = read_a(tb, 1, mt, ks);
-        const bf16x8 ap = read_a(tb, 0, mt, ks);
-        bf16x8 prev = {};
+        const bf16x8 bs = read_pd(tb, 1, nt, ks);
+        const bf16x8 bp = read_pd(tb, 0, nt, ks);
 #pragma unroll
         for (int n = 0; n < kDN; ++n) {
-          if (ks == 0)
-            Mfma16A::mma0(as, qB[n][ks], acc[mt][n], prev, qB[n > 0 ? n - 1 : 0][ks]);
-          else
-            Mfma16A::mma<false>(as, qB[n][ks], acc[mt][n], prev, qB[n > 0 ? n - 1 : 0][ks]);
-          prev = as;
+          if constexpr (DET) {
+            if (ks == 0)
+              Mfma16A::mma0(qB[n][ks], bs, acc[n][nt], bp, bs);
+            else
+              Mfma16A::mma<false>(qB[n][ks], bs, acc[n][nt], bp, bs);
+          } else {
+            if (ks == 0)
+              Mfma16A::mma0(bs, qB[n][ks], acc[n][nt], bp, bs);
+            else
+              Mfma16A::mma<false>(bs, qB[n][ks], acc[n][nt], bp, bs);
+          }
         }
 #pragma unroll
         for (int n = 0; n < kDN; ++n)
-          if (n < ndv) Mfma16A::mma_b_agpr(ap, dB[n][ks], acc[mt][n], as);
-        Mfma16A::tail(as, ap);
+          if (n < ndv) {
+            if constexpr (DET)
+              Mfma16A::mma_a_agpr(dB[n][ks], bp, acc[n][nt], bs);
+            else
+              Mfma16A::mma_b_agpr(bp, dB[n][ks], acc[n][nt], bs);
+          }
+        Mfma16A::tail(bs, bp);
       }
     }
-    // the tile's rows: keys 16 mt + 4 hq + i of dims dim0 + 16 n + lt
-    int ids[2][4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int n = 0; n < kDN; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ids[mt][i] = s_idx[j * kMT + 16 * mt + 4 * hq + i];
+      for (int nt = 0; nt < 2; ++nt) Mfma16A::drain(acc[n][nt]);
+    if constexpr (DET) {
+      u32x4* orow = s_stage + kOutBase + (j & 1) * kMT * kCP;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int nt = 0; nt < 2; ++nt) {
+        const int key = 16 * nt + lt;
+        const int rk = s_rank[j * kMT + key];
+        bf16* r = reinterpret_cast<bf16*>(orow + key * kCP);
 #pragma unroll
-      for (int n = 0; n < kDN; ++n) Mfma16A::drain(acc[mt][n]);
+        for (int n = 0; n < kDN; ++n) {
+          const bf16x4 v = {(bf16)acc[n][nt][0], (bf16)acc[n][nt][1], (bf16)acc[n][nt][2], (bf16)acc[n][nt][3]};
+          *reinterpret_cast<bf16x4*>(r + dim0 + 16 * n + 4 * hq) = v;
+        }
+        if (rk == kRankRepeat) {  // rare: a key repeated in the row
+          float* dst = dkv + (int64_t)s_idx[j * kMT + key] * acc_row + dim0 + 4 * hq;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+          for (int n = 0; n < kDN; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (ids[mt][i] < 0) continue;
-        float* dst = dkv + (int64_t)ids[mt][i] * acc_row + dim0 + lt;
-#pragma unroll
-        for (int n = 0; n < kDN; ++n) atomicAdd(dst + 16 * n, acc[mt][n][i]);
+            for (int i = 0; i < 4; ++i) atomicAdd(dst + 16 * n + i, acc[n][nt][i]);
+        }
       }
-    __syncthreads();  // the next tile's DMA has landed; this tile's buffer is free
+      __syncthreads();  // output rows staged; the next tile's P / dS landed
+      // rows to their rank in the item's contribution block (72 slots a row)
+      for (int u = tid; u < kMT * kMCH; u += kMThreads) {
+        const int key = u / kMCH, c = u - key * kMCH;
+        const int rk = s_rank[j * kMT + key];
+        if (rk >= 0) reinterpret_cast<u32x4*>(crow0 + (int64_t)rk * 576)[c] = orow[key * kCP + c];
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int id = s_idx[j * kMT + 16 * nt + 4 * hq + i];
+          if (id < 0) continue;
+          float* dst = dkv + (int64_t)id * acc_row + dim0 + lt;
+#pragma unroll
+          for (int n = 0; n < kDN; ++n) atomicAdd(dst + 16 * n, acc[n][nt][i]);
+        }
+      __syncthreads();  // the next tile's P / dS landed; this tile's buffer is free
+    }
+  }
+}
+
+// Deterministic reduction of a chunk's contributions: one wave per key (b, g,
+// key), summing the key's rows of the chunk's items in item order into the
+// fp32 accumulator row (each row owned by one wave; chunks run in order).
+// Lane l holds dims 8 l .. 8 l + 7, lanes 0..7 also dims 512 + 8 l ...
+__global__ __launch_bounds__(256) void mla_bwd_reduce_kernel(Params p, int64_t item0, int nitems, int b0, int nb,
+                                                             const bf16* contrib, const uint32_t* kmap,
+                                                             const uint16_t* prefix, int W) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t wi = (int64_t)blockIdx.x * 4 + wave;
+  const int key = (int)(wi % p.Skv);
+  const int64_t r = wi / p.Skv;
+  const int g = (int)(r % p.Hkv);
+  const int b = b0 + (int)(r / p.Hkv);
+  if (r >= (int64_t)nb * p.Hkv) return;
+  // this (b, g)'s items of the chunk: item = (b Sq + t) Hkv + g
+  const int64_t first = ((int64_t)b * p.Sq) * p.Hkv + g;
+  int64_t lo = first < item0 ? item0 + ((g - item0 % p.Hkv) + p.Hkv) % p.Hkv : first;
+  const int64_t hi_b = ((int64_t)(b + 1) * p.Sq) * p.Hkv;
+  const int64_t hi = hi_b < item0 + nitems ? hi_b : item0 + nitems;
+  const int wsel = key >> 5;
+  const uint32_t bit = 1u << (key & 31);
+  float a0[8] = {}, a1[8] = {};
+  bool any = false;
+  // items in batches of 64 (one per lane); the rows of the batch's hits are
+  // loaded 8 at a time, then added in item order
+  for (int64_t base = lo; base < hi; base += 64 * (int64_t)p.Hkv) {
+    const int64_t it = base + (int64_t)lane * p.Hkv;
+    const int li = (int)(it - item0);
+    uint32_t word = 0;
+    int rank = 0;
+    if (it < hi) {
+      word = kmap[(int64_t)li * W + wsel];
+      rank = prefix[(int64_t)li * W + wsel] + __builtin_popcount(word & (bit - 1u));
+    }
+    uint64_t hits = __ballot((word & bit) != 0u);
+    while (hits) {
+      int n = 0;
+      constexpr int U = 8;
+      int lis[U], rks[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        lis[u] = -1;
+        rks[u] = 0;
+        if (hits) {
+          const int l = __builtin_ctzll(hits);
+          hits &= hits - 1;
+          lis[u] = (int)(base - item0) + l * p.Hkv;
+          rks[u] = __builtin_amdgcn_readlane(rank, l);
+          ++n;
+        }
+      }
+      u32x4 v0[U], v1[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (lis[u] >= 0) {
+          const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)lis[u] * p.topk + rks[u]) * 576);
+          v0[u] = row[lane];
+          v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (lis[u] < 0) continue;
+        const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
+        const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a0[e] += (float)x0[e];
+          a1[e] += (float)x1[e];
+        }
+      }
+      any = any || n > 0;
+    }
+  }
+  if (!any || key >= bound_of(p, b)) return;
+  float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
+  if (lane < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
   }
 }
 
@@ -484,20 +719,53 @@ bool bwd_mla_supported(const Params& p) {
   return kb < (int64_t)kOOB && fits_u24(2 * p.k_ss);
 }
 
-size_t bwd_mla_pd_bytes_per_item(const Params& p) {
+bool bwd_mla_det_supported(const Params& p) { return p.Skv <= kMaxMapW * 32; }
+
+int bwd_mla_map_words(const Params& p) { return (p.Skv + 2047) / 2048 * 64; }
+
+size_t bwd_mla_bytes_per_item(const Params& p, bool det) {
   const int64_t ntiles = (p.topk + kMT - 1) / kMT;
   const int64_t nhg = (p.G + kMHG - 1) / kMHG;
-  return (size_t)(ntiles * 2 * nhg * 4 * pd_block_elems() * 2);
+  size_t n = (size_t)(ntiles * 2 * nhg * 4 * pd_block_elems() * 2);
+  if (det) n += (size_t)p.topk * 576 * 2 + (size_t)bwd_mla_map_words(p) * 6 + (size_t)p.topk;
+  return n;
 }
 
-// Items (b, t, kv-head) of the chunk [item0, item0 + n): dQ pass, then the
-// dK/dV pass over the same items.  p.dk_acc holds [B, Skv, Hkv, 576] fp32.
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd, hipStream_t s) {
+// Work items (b, t, kv-head) [item0, item0 + n) of one chunk: dQ pass, then
+// dK/dV pass (and for det the index maps before and the reduction after).
+// ws: P / dS of the chunk, then (det) contributions, bitmaps, prefixes and
+// repeat flags.  p.dk_acc holds [B, Skv, Hkv, 576] fp32.
+hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s) {
   const int nhg = (p.G + kMHG - 1) / kMHG;
-  hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, (bf16*)pd);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(mla_bwd_dkv_kernel, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0, (const bf16*)pd);
+  const int64_t ntiles = (p.topk + kMT - 1) / kMT;
+  bf16* pd = (bf16*)ws;
+  char* c = (char*)ws + (size_t)n * ntiles * 2 * nhg * 4 * pd_block_elems() * 2;
+  const int W = bwd_mla_map_words(p);
+  bf16* contrib = (bf16*)c;
+  c += (size_t)n * p.topk * 576 * 2;
+  uint32_t* kmap = (uint32_t*)c;
+  c += (size_t)n * W * 4;
+  uint16_t* prefix = (uint16_t*)c;
+  c += (size_t)n * W * 2;
+  uint8_t* dup = (uint8_t*)c;
+  if (det) {
+    hipLaunchKernelGGL(mla_map_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p, item0, n, W, kmap, prefix,
+                       dup);
+  }
+  hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
+  if (det) {
+    hipLaunchKernelGGL(mla_bwd_dkv_kernel<true>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
+                       (const bf16*)pd, contrib, (const uint32_t*)kmap, (const uint16_t*)prefix,
+                       (const uint8_t*)dup, W);
+    const int b0 = (int)(item0 / ((int64_t)p.Hkv * p.Sq));
+    const int b1 = (int)((item0 + n - 1) / ((int64_t)p.Hkv * p.Sq));
+    const int64_t waves = (int64_t)(b1 - b0 + 1) * p.Hkv * p.Skv;
+    hipLaunchKernelGGL(mla_bwd_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, item0, n, b0,
+                       b1 - b0 + 1, (const bf16*)contrib, (const uint32_t*)kmap, (const uint16_t*)prefix, W);
+  } else {
+    hipLaunchKernelGGL(mla_bwd_dkv_kernel<false>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
+                       (const bf16*)pd, nullptr, nullptr, nullptr, nullptr, W);
+  }
   return hipGetLastError();
 }
 

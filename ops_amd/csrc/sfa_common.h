@@ -221,10 +221,12 @@ hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
 // MLA shared-KV backward (sfa_bwd_mla.hip): dQ pass + dK/dV pass over a chunk
-// of work items, P / dS of the chunk in `pd` (bwd_mla_pd_bytes_per_item each)
+// of work items (det: plus index maps and the ordered reduction); the chunk's
+// workspace holds bwd_mla_bytes_per_item per item
 bool bwd_mla_supported(const Params& p);
-size_t bwd_mla_pd_bytes_per_item(const Params& p);
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd, hipStream_t s);
+bool bwd_mla_det_supported(const Params& p);  // deterministic dK/dV: Skv <= 65536
+size_t bwd_mla_bytes_per_item(const Params& p, bool det);
+hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
 bool bwd_dq_supported(const Params& p);
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s);

@@ -111,6 +111,10 @@ struct Mfma16A {
     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
                  : "=&a"(c) : "v"(a), "v"(b), "v"(pa), "v"(pb) : "memory");
   }
+  // A operand from AGPRs, B from VGPRs (pb: the previous MFMA's B, kept live)
+  static __device__ __forceinline__ void mma_a_agpr(const bf16x8& a, bf16x8 b, acc_t& c, const bf16x8& pb) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "a"(a), "v"(b), "v"(pb) : "memory");
+  }
   static __device__ __forceinline__ void mma_b_agpr(bf16x8 a, const bf16x8& b, acc_t& c, const bf16x8& pa) {
     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "a"(b), "v"(pa) : "memory");
   }

@@ -52,10 +52,10 @@ def _ref_merged(q, kv, idx, out, lse, dout, scale, kv_lens=None, sink=None, dlse
     return dq, dkv, ds
 
 
-def _run(q, kv, idx, dout, scale, kv_lens=None, sink=None, dlse=None):
+def _run(q, kv, idx, dout, scale, kv_lens=None, sink=None, dlse=None, mode=None):
     out, lse = ops_amd.sfa_forward(q, kv, kv[..., :512], idx, scale, kv_lens=kv_lens, attn_sink=sink)
     dq, dkv, dv, ds = ops_amd.sfa_backward(q, kv, kv[..., :512], idx, out, lse, dout, scale, kv_lens=kv_lens,
-                                           attn_sink=sink, dlse=dlse, merge_kv=True)
+                                           attn_sink=sink, dlse=dlse, merge_kv=True, dkv_mode=mode)
     torch.cuda.synchronize()
     assert dv is None
     return out, lse, dq, dkv, ds
@@ -66,24 +66,27 @@ def _inputs(B, S, H, K, seed, recent=True):
     return w
 
 
-def test_mla_bwd_mfma_matches_oracle_multichunk():
-    """S = 1024, top-k 2048, G = 128: P / dS of 1 MiB per query, so the
-    backward runs as two chunks of 512 queries."""
-    _say("MLA bwd MFMA B=1 S=1024 Hq=128 K=2048 (two chunks)")
+@pytest.mark.parametrize("mode", ["auto", "atomic"])
+def test_mla_bwd_mfma_matches_oracle_multichunk(mode):
+    """S = 1024, top-k 2048, G = 128: about 3.4 MiB of chunk workspace per
+    query, so the backward runs as four chunks; 'auto' sums the per-slot rows
+    in a fixed order, 'atomic' adds them with fp32 atomics."""
+    _say(f"MLA bwd MFMA B=1 S=1024 Hq=128 K=2048 (several chunks, dkv_mode={mode})")
     w = _inputs(1, 1024, 128, 2048, seed=3)
-    out, lse, dq, dkv, _ = _run(w.q, w.k, w.idx, w.dout, w.scale)
+    out, lse, dq, dkv, _ = _run(w.q, w.k, w.idx, w.dout, w.scale, mode=mode)
     rdq, rdkv, _ = _ref_merged(w.q, w.k, w.idx, out, lse, w.dout, w.scale)
     e_q, e_kv = _rel_l2(dq.float().cpu(), rdq), _rel_l2(dkv.float().cpu(), rdkv)
     _say(f"  rel-L2 dq {e_q:.2e} dkv {e_kv:.2e}")
     assert e_q <= GRAD_RL2 and e_kv <= GRAD_RL2
 
 
+@pytest.mark.parametrize("mode", ["auto", "atomic"])
 @pytest.mark.parametrize("H", [128, 100, 72])
-def test_mla_bwd_mfma_masking_sink_dlse(H):
+def test_mla_bwd_mfma_masking_sink_dlse(H, mode):
     """Padding inside and after the valid slots, ids at or past kv_lens, a
     fully masked query row, a sink and a gradient on lse; G = 100 and 72 leave
     the last head group partly empty."""
-    _say(f"MLA bwd MFMA masking / kv_lens / sink / dlse B=2 S=96 Hq={H} K=200")
+    _say(f"MLA bwd MFMA masking / kv_lens / sink / dlse B=2 S=96 Hq={H} K=200 dkv_mode={mode}")
     g = torch.Generator(device=DEV).manual_seed(11 + H)
     B, S, K = 2, 96, 200
     q = torch.randn(B, S, H, 576, device=DEV, generator=g).bfloat16()
@@ -99,7 +102,7 @@ def test_mla_bwd_mfma_masking_sink_dlse(H):
     dlse = torch.randn(B, S, H, device=DEV, generator=g)
     dout = torch.randn(B, S, H, 512, device=DEV, generator=g).bfloat16()
     scale = 1.0 / math.sqrt(576)
-    out, lse, dq, dkv, ds = _run(q, kv, idx, dout, scale, kv_lens=kv_lens, sink=sink, dlse=dlse)
+    out, lse, dq, dkv, ds = _run(q, kv, idx, dout, scale, kv_lens=kv_lens, sink=sink, dlse=dlse, mode=mode)
     rdq, rdkv, rds = _ref_merged(q, kv, idx, out, lse, dout, scale, kv_lens=kv_lens, sink=sink, dlse=dlse)
     e_q, e_kv, e_s = _rel_l2(dq.float().cpu(), rdq), _rel_l2(dkv.float().cpu(), rdkv), _rel_l2(ds.cpu(), rds)
     _say(f"  rel-L2 dq {e_q:.2e} dkv {e_kv:.2e} dsink {e_s:.2e}")
@@ -108,21 +111,47 @@ def test_mla_bwd_mfma_masking_sink_dlse(H):
     assert torch.all(dkv[1, 61:] == 0), "rows past kv_lens get no gradient"
 
 
-def test_mla_bwd_mfma_dq_invariant_to_invalid_encoding():
-    """dQ is computed without atomics: bitwise identical when only the
-    encoding of the invalid slots changes (-1 vs ids >= Skv); dK + dV equal up
-    to the order of its atomic adds."""
-    _say("MLA bwd MFMA dQ invariance to invalid-slot encoding")
+def test_mla_bwd_invariant_to_invalid_encoding_and_deterministic():
+    """Deterministic mode: bitwise identical results when only the encoding of
+    the invalid slots changes (-1 vs ids >= Skv) and from run to run; with
+    atomics dQ is still bitwise identical and dK + dV equal up to the order
+    of the fp32 adds."""
+    _say("MLA bwd MFMA invariance to invalid-slot encoding, determinism")
     w = _inputs(1, 256, 128, 256, seed=7)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
     idx2 = torch.where(w.idx < 0, torch.full_like(w.idx, 1 << 20), w.idx)
-    dq1, dkv1, _, _ = ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True)
-    dq2, dkv2, _, _ = ops_amd.sfa_backward(w.q, w.k, w.v, idx2, out, lse, w.dout, w.scale, merge_kv=True)
+    bwd = lambda i, m: ops_amd.sfa_backward(w.q, w.k, w.v, i, out, lse, w.dout, w.scale, merge_kv=True,
+                                             dkv_mode=m)
+    dq1, dkv1, _, _ = bwd(w.idx, "csr")
+    dq2, dkv2, _, _ = bwd(idx2, "csr")
+    dq3, dkv3, _, _ = bwd(w.idx, "csr")
+    dq4, dkv4, _, _ = bwd(idx2, "atomic")
     torch.cuda.synchronize()
-    assert torch.equal(dq1, dq2)
-    # the shared rows are summed with fp32 atomics in no fixed order: equal up
-    # to that rounding (bf16 output)
-    assert _rel_l2(dkv1.float(), dkv2.float()) <= 1e-3
+    assert torch.equal(dq1, dq2) and torch.equal(dkv1, dkv2)
+    assert torch.equal(dq1, dq3) and torch.equal(dkv1, dkv3)
+    assert torch.equal(dq1, dq4)
+    # (the deterministic mode rounds each slot's row to bf16 before its fp32
+    # sum, the atomic mode adds fp32 rows: both sit within ~3e-3 of the oracle)
+    assert _rel_l2(dkv1.float(), dkv4.float()) <= GRAD_RL2
+
+
+def test_mla_bwd_repeated_keys():
+    """Index rows that select the same key more than once: every slot counts
+    (the oracle sums each slot, SFA.py:386-467); the deterministic mode sends
+    the repeats through fp32 atomics."""
+    _say("MLA bwd MFMA repeated keys B=1 S=64 Hq=128 K=96")
+    g = torch.Generator(device=DEV).manual_seed(21)
+    B, S, H, K = 1, 64, 128, 96
+    q = torch.randn(B, S, H, 576, device=DEV, generator=g).bfloat16()
+    kv = torch.randn(B, S, 1, 576, device=DEV, generator=g).bfloat16()
+    idx = torch.randint(0, 16, (B, S, 1, K), device=DEV, generator=g, dtype=torch.int32)  # many repeats
+    dout = torch.randn(B, S, H, 512, device=DEV, generator=g).bfloat16()
+    scale = 1.0 / math.sqrt(576)
+    out, lse, dq, dkv, _ = _run(q, kv, idx, dout, scale)
+    rdq, rdkv, _ = _ref_merged(q, kv, idx, out, lse, dout, scale)
+    e_q, e_kv = _rel_l2(dq.float().cpu(), rdq), _rel_l2(dkv.float().cpu(), rdkv)
+    _say(f"  rel-L2 dq {e_q:.2e} dkv {e_kv:.2e}")
+    assert e_q <= GRAD_RL2 and e_kv <= GRAD_RL2
 
 
 def test_mla_bwd_separate_dk_dv_generic():
