@@ -106,16 +106,26 @@ def time_steps(fn, steps, warmup, before=None):
 
 
 def cpu_model():
-    """The host CPU's model name (first ``model name`` line of /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: model name, family / model /
+    stepping numbers (a virtualised host may shorten the name) and the
+    logical CPU count of the host."""
+    fields, n = {}, 0
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "processor":
+                    n += 1
+                elif k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                    fields[k] = v.strip()
     except OSError:
         pass
-    import platform
-    return platform.processor() or "unknown"
+    if not fields:
+        import platform
+        return platform.processor() or "unknown"
+    return (f"{fields.get('model name', '?')} (family {fields.get('cpu family', '?')}, model "
+            f"{fields.get('model', '?')}, stepping {fields.get('stepping', '?')}; {n} logical CPUs on the host)")
 
 
 def _cpu_threads():
@@ -365,7 +375,7 @@ def bench_mla_bwd(args):
     ms = sum(bt) / len(bt)
     tf = bwd_flops(w, pairs) / (ms * 1e-3) / 1e12
     return {"metric": "bwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
-            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "mla_bwd_dq_kernel + mla_bwd_dkv_kernel (fp32 atomics)",
+            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "mla_map_kernel + mla_bwd_dq_kernel + mla_bwd_dkv_kernel<true> + mla_bwd_reduce_kernel (deterministic: per-slot bf16 rows summed per key in slot order)",
             "config": {"B": 1, "S": 32768, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
 
 
@@ -446,6 +456,212 @@ def profile_targets(name):
     raise SystemExit(f"unknown --profile target {name!r}")
 
 
+# Counter passes of the per-workload counter summaries (one rocprofv3 run
+# each; every pass stays within one run's per-block counter limits).
+PMC_PASSES = (
+    "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAVE_CYCLES SQ_WAIT_INST_ANY SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
+    "SQ_INSTS_SALU SQ_INSTS_VMEM GRBM_GUI_ACTIVE GRBM_COUNT",
+    "FETCH_SIZE TCC_HIT_sum TA_BUSY_avr TA_BUFFER_READ_LDS_WAVEFRONTS_sum TD_TD_BUSY_sum TD_TC_STALL_sum "
+    "TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum TCP_PENDING_STALL_CYCLES_sum TCP_TOTAL_CACHE_ACCESSES_sum "
+    "GRBM_GUI_ACTIVE",
+    "WRITE_SIZE TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum GRBM_GUI_ACTIVE",
+    "TCC_MISS_sum TCC_REQ_sum TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_DRAM_32B_sum SQ_LDS_BANK_CONFLICT "
+    "SQ_LDS_IDX_ACTIVE SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_INST_LEVEL_VMEM SQ_INSTS_VMEM_WR "
+    "SQ_INSTS_VMEM_RD SQ_INSTS_SMEM GRBM_GUI_ACTIVE",
+)
+N_XCD, N_CU, N_SIMD = 8, 256, 1024
+
+
+def _short_kernel(name):
+    import re
+    m = re.match(r"_ZN3sfa12_GLOBAL__N_1(\d+)", name)
+    if m:  # a mangled name (some tracer records): identifier + the bf16 / float template argument
+        n = int(m.group(1))
+        ident = name[m.end():m.end() + n]
+        rest = name[m.end() + n:]
+        targ = "<bf16>" if rest.startswith("IDF16b") else "<float>" if rest.startswith("IfE") else ""
+        return ident + targ
+    n = name.replace("void ", "").replace("sfa::(anonymous namespace)::", "").replace("sfa::", "")
+    n = re.sub(r"\(.*\)$", "", n)
+    return n.replace("FwdCfg<32, 576, 512, 4, 1, true, 18, true>", "CfgMla")
+
+
+def pmc_summary(root, copy_mib):
+    """Summarise rocprofv3 counter CSVs laid out as ROOT/<target>_<pass>/
+    (pass = 1-based index into PMC_PASSES; target "copy" is the
+    ``--copy-probe COPY_MIB`` run that calibrates the byte counters) into
+    per-dispatch means and derived figures per (target, kernel, grid).
+    Cycle-based figures use GRBM_GUI_ACTIVE / 8 (one XCD's busy cycles) as
+    the kernel's clock count; SQ wave counters count quad-cycles."""
+    import csv
+    import glob
+    import re
+    raw = {}
+    for d in sorted(glob.glob(os.path.join(root, "*_[0-9]"))):
+        target, ps = os.path.basename(d).rsplit("_", 1)
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            disp = {}
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    e = disp.setdefault(r["Dispatch_Id"], {"c": {}})
+                    e["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+                    e["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                    wg = int(r["Workgroup_Size"])
+                    e["key"] = (_short_kernel(r["Kernel_Name"]), int(r["Grid_Size"]) // max(wg, 1), wg)
+                    e["res"] = {"vgpr": int(r["VGPR_Count"]), "agpr": int(r["Accum_VGPR_Count"]),
+                                "lds": int(r["LDS_Block_Size"])}
+            for e in disp.values():
+                k = raw.setdefault(target, {}).setdefault(e["key"], {"res": e["res"], "passes": {}})
+                k["passes"].setdefault(int(ps), []).append(e)
+    def mean_pass(k, ps):
+        es = k["passes"].get(ps, [])
+        if not es:
+            return None, None
+        names = set().union(*[e["c"].keys() for e in es])
+        return ({n: sum(e["c"].get(n, 0.0) for e in es) / len(es) for n in names},
+                sum(e["ns"] for e in es) / len(es))
+    # calibration from the copy probe (its largest reader)
+    cal = {"copy_bytes": copy_mib << 20, "fetch_scale": None, "write_scale": None, "bytes_per_rdreq": None}
+    if "copy" in raw:
+        best = max(raw["copy"].values(), key=lambda k: (mean_pass(k, 2)[0] or {}).get("FETCH_SIZE", 0))
+        c2, _ = mean_pass(best, 2)
+        c3, _ = mean_pass(best, 3)
+        if c2 and c2.get("FETCH_SIZE"):
+            cal["fetch_scale"] = cal["copy_bytes"] / (c2["FETCH_SIZE"] * 1024)
+        if c3 and c3.get("WRITE_SIZE"):
+            cal["write_scale"] = cal["copy_bytes"] / (c3["WRITE_SIZE"] * 1024)
+        if c3 and c3.get("TCC_EA0_RDREQ_sum"):
+            cal["bytes_per_rdreq"] = cal["copy_bytes"] / c3["TCC_EA0_RDREQ_sum"]
+    out = {"calibration": cal, "targets": {}}
+    for target, kernels in raw.items():
+        rows = []
+        for (name, grid, wg), k in kernels.items():
+            row = {"kernel": name, "workgroups": grid, "wg_threads": wg, **k["res"]}
+            dispatches = max(len(v) for v in k["passes"].values())
+            row["dispatches_per_pass"] = dispatches
+            for ps in sorted(k["passes"]):
+                c, ns = mean_pass(k, ps)
+                row[f"pass{ps}_us"] = round(ns / 1e3, 2)
+                g = c.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD
+                if ps == 1 and g:
+                    row["clock_ghz"] = round(g / ns, 3)
+                    row["mfma_busy"] = round(c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / (g * N_SIMD), 4)
+                    row["waves_per_simd"] = round(4 * c.get("SQ_WAVE_CYCLES", 0) / (g * N_SIMD), 3)
+                    if c.get("SQ_WAVE_CYCLES"):
+                        row["wait_inst_frac"] = round(c.get("SQ_WAIT_INST_ANY", 0) / c["SQ_WAVE_CYCLES"], 3)
+                    for n in ("MFMA", "VALU", "LDS", "SALU", "VMEM"):
+                        row[f"insts_{n.lower()}"] = c.get(f"SQ_INSTS_{n}")
+                if ps == 2:
+                    fs = c.get("FETCH_SIZE", 0) * 1024
+                    row["fetch_size_kib_raw"] = c.get("FETCH_SIZE")
+                    if cal["fetch_scale"]:
+                        row["fetch_bytes"] = fs * cal["fetch_scale"]
+                        row["fetch_gbs"] = round(row["fetch_bytes"] / ns, 1)
+                    if g:
+                        row["ta_busy"] = round(c.get("TA_BUSY_avr", 0) / g, 3)
+                        row["td_busy"] = round(c.get("TD_TD_BUSY_sum", 0) / (g * N_CU), 3)
+                        row["td_tc_stall"] = round(c.get("TD_TC_STALL_sum", 0) / (g * N_CU), 3)
+                        row["tcp_pending_stall"] = round(c.get("TCP_PENDING_STALL_CYCLES_sum", 0) / (g * N_CU), 3)
+                    if c.get("TCP_TCC_READ_REQ_sum"):
+                        row["l2_read_latency_cyc"] = round(c["TCP_TCC_READ_REQ_LATENCY_sum"] / c["TCP_TCC_READ_REQ_sum"], 1)
+                    row["lds_dma_wavefronts"] = c.get("TA_BUFFER_READ_LDS_WAVEFRONTS_sum")
+                    row["tcc_hit"] = c.get("TCC_HIT_sum")
+                if ps == 3:
+                    row["write_size_kib_raw"] = c.get("WRITE_SIZE")
+                    row["ea_rdreq"] = c.get("TCC_EA0_RDREQ_sum")
+                    if cal["write_scale"]:
+                        row["write_bytes"] = c.get("WRITE_SIZE", 0) * 1024 * cal["write_scale"]
+                        row["write_gbs"] = round(row["write_bytes"] / ns, 1)
+                    if cal["bytes_per_rdreq"]:
+                        row["rdreq_bytes"] = c.get("TCC_EA0_RDREQ_sum", 0) * cal["bytes_per_rdreq"]
+                if ps == 4:
+                    row["tcc_miss"] = c.get("TCC_MISS_sum")
+                    row["tcc_req"] = c.get("TCC_REQ_sum")
+                    if cal["bytes_per_rdreq"]:
+                        row["dram_read_bytes"] = c.get("TCC_EA0_RDREQ_DRAM_sum", 0) * cal["bytes_per_rdreq"]
+                    if c.get("SQ_LDS_IDX_ACTIVE"):
+                        row["lds_bank_conflict_frac"] = round(c.get("SQ_LDS_BANK_CONFLICT", 0) / c["SQ_LDS_IDX_ACTIVE"], 4)
+                    for n in ("VMEM_RD", "VMEM_WR", "SMEM"):
+                        row[f"insts_{n.lower()}"] = c.get(f"SQ_INSTS_{n}")
+            if row.get("tcc_hit") is not None and row.get("tcc_miss") is not None:
+                row["l2_hit_frac"] = round(row["tcc_hit"] / max(row["tcc_hit"] + row["tcc_miss"], 1.0), 3)
+            rows.append(row)
+        rows.sort(key=lambda r: -r.get("pass1_us", 0) * r["dispatches_per_pass"])
+        out["targets"][target] = rows
+    return out
+
+
+def _is_library_kernel(name):
+    return (not name or name.startswith("at::") or name.startswith("__amd") or "at::native" in name
+            or name.startswith("rocprim::"))
+
+
+def pmc_markdown(summary, targets=None):
+    """The summary as markdown tables: per target (all, or those named),
+    this library's kernels (input generation, cache flushes and copies made
+    by torch / the HIP runtime are left out)."""
+    def f(x, nd=3):
+        if x is None:
+            return "-"
+        if isinstance(x, float) and (abs(x) >= 1e5 or (x and abs(x) < 1e-3)):
+            return f"{x:.4g}"
+        return f"{x:.{nd}f}" if isinstance(x, float) else str(x)
+    cal = summary["calibration"]
+    lines = [f"Calibration (plain copy of {cal['copy_bytes'] >> 20} MiB): FETCH_SIZE x {f(cal['fetch_scale'])}, "
+             f"WRITE_SIZE x {f(cal['write_scale'])}, {f(cal['bytes_per_rdreq'], 1)} B per TCC_EA0_RDREQ", ""]
+    for target, rows in summary["targets"].items():
+        if target == "copy" or (targets and target not in targets):
+            continue
+        rows = [r for r in rows if not _is_library_kernel(r["kernel"])]
+        lines += [f"### {target}", "",
+                  "| kernel | WGs x thr | VGPR/AGPR/LDS | us | GHz | waves/SIMD | MFMA busy | wait-inst | "
+                  "MFMA / VALU / LDS / SALU / VMEM insts | fetch GB (GB/s) | RDREQ GB | write GB (GB/s) | "
+                  "L2 hit | L2 lat | TA / TD busy | LDS confl |",
+                  "|" + "---|" * 16]
+        for r in rows:
+            ins = " / ".join(f(r.get(f"insts_{n}"), 0) if r.get(f"insts_{n}") is not None else "-"
+                             for n in ("mfma", "valu", "lds", "salu", "vmem"))
+            gb = lambda b: f"{b / 1e9:.3f}" if b is not None else "-"
+            lines.append(
+                f"| {r['kernel'][:60]} | {r['workgroups']} x {r['wg_threads']} | {r['vgpr']}/{r['agpr']}/{r['lds']} | "
+                f"{f(r.get('pass1_us'), 1)} | {f(r.get('clock_ghz'), 2)} | {f(r.get('waves_per_simd'), 2)} | "
+                f"{f(r.get('mfma_busy'))} | {f(r.get('wait_inst_frac'))} | {ins} | "
+                f"{gb(r.get('fetch_bytes'))} ({f(r.get('fetch_gbs'), 0)}) | {gb(r.get('rdreq_bytes'))} | "
+                f"{gb(r.get('write_bytes'))} ({f(r.get('write_gbs'), 0)}) | {f(r.get('l2_hit_frac'))} | "
+                f"{f(r.get('l2_read_latency_cyc'), 0)} | {f(r.get('ta_busy'))} / {f(r.get('td_busy'))} | "
+                f"{f(r.get('lds_bank_conflict_frac'))} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
+def trace_summary(root):
+    """Per (kernel, grid) duration statistics of the rocprofv3
+    ``--kernel-trace`` CSVs under ROOT, as a markdown table (library kernels
+    of torch and the HIP runtime left out).  Several workloads share a
+    kernel instance, so the grid tells them apart."""
+    import csv
+    import glob
+    import statistics
+    groups = {}
+    for f in glob.glob(os.path.join(root, "**", "*kernel_trace.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                name = _short_kernel(r["Kernel_Name"])
+                if _is_library_kernel(name):
+                    continue
+                wg = int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 1)) or 1)
+                grid = int(r.get("Grid_Size_X", r.get("Grid_Size", 0)) or 0) // max(wg, 1)
+                key = (name, grid, wg, r.get("Arch_VGPR_Count", r.get("VGPR_Count", "")),
+                       r.get("Accum_VGPR_Count", ""), r.get("LDS_Block_Size", r.get("Group_Segment_Size", "")))
+                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = ["| kernel | workgroups x threads | VGPR | AGPR | LDS B | launches | total ms | avg us | min | median | max |",
+             "|" + "---|" * 11]
+    for (name, grid, wg, vg, ag, lds), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {name} | {grid} x {wg} | {vg} | {ag} | {lds} | {len(d)} | {sum(d) / 1e3:.2f} | "
+                     f"{statistics.mean(d):.1f} | {min(d):.1f} | {statistics.median(d):.1f} | {max(d):.1f} |")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -460,10 +676,30 @@ def main():
                     help="only launch workload NAME's kernels `steps` times (for counter runs) and exit: "
                          "mla_prefill, prefill, train_gqa_fwd, train_gqa_bwd_csr, train_gqa_bwd_atomic, "
                          "mla_decode, mla_decode_paged, mla_bwd")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("DIR", "OUT_JSON"),
+                    help="summarise counter CSVs under DIR/<target>_<pass>/ (passes = PMC_PASSES) into "
+                         "OUT_JSON, print markdown tables, and exit (needs no GPU)")
+    ap.add_argument("--pmc-copy-mib", type=int, default=1024, help="size of the calibrating copy probe")
+    ap.add_argument("--pmc-targets", default="", help="comma list: print only these targets' tables")
+    ap.add_argument("--pmc-passes", action="store_true", help="print PMC_PASSES, one line each, and exit")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print per-(kernel, grid) durations of the --kernel-trace CSVs under DIR and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB `steps` times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.pmc_passes:
+        print("\n".join(PMC_PASSES))
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary), flush=True)
+        return
+    if args.pmc_summary:
+        summ = pmc_summary(args.pmc_summary[0], args.pmc_copy_mib)
+        with open(args.pmc_summary[1], "w") as fh:
+            json.dump(summ, fh, indent=1)
+        print(pmc_markdown(summ, [t for t in args.pmc_targets.split(",") if t]), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the sparse attention path runs on a single MI355X "
               "(multi-GPU sharding is described as a design only, not implemented)", file=sys.stderr)

@@ -14,21 +14,29 @@
 //    x 16 heads.  The query's top-k K rows are gathered into LDS 32 at a time
 //    (the forward's RowGather and swizzled tile).  Per 32-key tile a wave
 //    computes S^T = K Q^T and dP^T = V dO^T (16x16x32, keys as rows; each K
-//    operand read serves both), P = 2^(S scale log2e - lse2) and
-//    dS = P (dP - delta), then dQ^T += K^T dS^T (K^T by transposing LDS
-//    reads; the S^T accumulator layout already is dS^T's B layout) into 144
-//    AGPRs.  P and scale * dS leave as bf16 in the wave's register layout:
-//    one 16-byte store per lane and matrix.
+//    operand read serves both; Q^T and dO^T are B operands held in AGPRs),
+//    P = 2^(S scale log2e - lse2) and dS = P (dP - delta), then
+//    dQ^T += K^T dS^T (K^T by transposing LDS reads; the S^T accumulator
+//    layout already is dS^T's B layout) into 144 VGPR accumulators.  P and
+//    scale * dS leave as bf16 in the wave's register layout: one 16-byte
+//    store per lane and matrix.
 //  * dK/dV pass (mla_bwd_dkv_kernel): a workgroup owns one query with all its
-//    heads, so the contraction over heads is complete inside it.  Q and dO sit
-//    in registers as the B operands of dKV^T = (scale dS)^T Q + P^T dO
-//    (16x16x32, keys as rows, dims as columns, heads as the contraction;
-//    wave w owns dims 144 w .. 144 w + 143), staged once per query through LDS
-//    and read transposed.  Per 32-key tile the P / dS tile of the dQ pass is
-//    DMA'd into LDS and read back transposed as A operands; the 32 x 576 fp32
-//    result is added to the key rows with fp32 atomics (the reference's
-//    scheme, SFA.py:853: at this density, ~2000 queries per key, an inverted
-//    index would re-read each query's 278 KB of Q and dO per key block).
+//    heads, so the contraction over heads is complete inside it.  Q and dO,
+//    staged once per query through LDS and read transposed, sit in registers
+//    as operands of dKV^T = Q^T (scale dS) + dO^T P (16x16x32, heads as the
+//    contraction; wave w owns dims 144 w .. 144 w + 143).  Per 32-key tile
+//    the P / dS tile of the dQ pass is DMA'd into LDS and read back
+//    transposed.  The 32 x 576 result of the query is then either
+//    - (deterministic, default) rounded to bf16 and stored as one row per
+//      (query, distinct key) into the chunk's contribution rows, which
+//      mla_bwd_reduce_kernel sums per key in query order into the fp32
+//      accumulators (mla_map_kernel first ranks each query's keys; a slot
+//      repeating a key of its row adds with fp32 atomics), or
+//    - (SFA_DKV_ATOMIC) added to the key rows with fp32 atomics, the
+//      reference's scheme (SFA.py:853).
+//    An inverted index (key-major pass) does not fit this density: ~2000
+//    queries select each key, and each would re-read its 278 KB of Q and dO
+//    per key block.
 //
 // MFMA layouts (16x16x32 bf16, gfx950):
 //   A[m][k]: lane l holds m = l % 16, k = 8 (l / 16) + j        (j = 0..7)
