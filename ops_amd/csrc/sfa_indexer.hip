@@ -448,8 +448,10 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
 }
 
 // MAXNG: the largest row this instance takes is 4 MAXNG kSelThreads scores.
-// Rows of up to 32768 scores fit 64 VGPRs: two workgroups per CU, so one
-// workgroup's barrier waits overlap the other's counting.
+// Rows of up to 32768 scores are held to 64 VGPRs: two workgroups per CU, so
+// one workgroup's barrier waits overlap the other's counting.  At that bound
+// the compiler spills ~21 VGPRs to scratch; the spill-free build at one
+// workgroup per CU (84 VGPRs) was measured 7 % slower on the whole call.
 template <int MAXNG>
 // (second bound: minimum waves per SIMD; 8 = two 16-wave workgroups per CU)
 __global__ __launch_bounds__(kSelThreads, MAXNG <= 8 ? 8 : 1) void topk_select_kernel(IndexerParams p, int t_begin,
