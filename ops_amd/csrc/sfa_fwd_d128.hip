@@ -1,23 +1,28 @@
 // gfx950 forward for d_qk = d_v = 128 with G <= 16 query heads per KV head
-// (the MQA prefill and GQA training shapes): register-direct gather.
+// (the MQA prefill and GQA training shapes): register gather of whole rows.
 //
 // Reference: `_attn_fwd` / `_inner_fwd` (SFA.py:309-587); the math is the one
 // of the MLA kernel in sfa_fwd_mfma.hip (masked base-2 online softmax with a
 // lazy rescale, P V, sink, LSE, split-k partials).  The schedule follows from
 // the shape: one wave holds all G <= 16 heads of a work item, so a gathered K
-// or V row is used by exactly one wave and staging it in LDS buys no reuse.
-//  * K rows go straight from global memory into VGPRs as the A operands of
-//    S^T = K Q^T (16x16x32 MFMA: a lane needs 16 contiguous bytes of one row),
-//    double-buffered in registers one 32-key tile ahead;
-//  * V rows are loaded one tile ahead into VGPRs in the same lane layout and
-//    written to the wave's LDS area just before use, where the transposing
-//    reads (ds_read_b64_tr_b16) produce the V^T operands of O^T = V^T P^T;
+// or V row is used by exactly one wave and its load pattern, not reuse,
+// decides the gather rate.
+//  * K and V rows of a 32-key tile are loaded one tile ahead into VGPRs as
+//    whole 256-byte rows: each load instruction moves 4 rows (16 lanes per
+//    row, 16 bytes each).  Loading them straight in the MFMA operand layout
+//    (16 rows x 64 bytes per instruction) runs the texture path 3x slower per
+//    byte on L2-resident rows, and that path bounds these kernels.
+//  * At the start of a tile the K rows go to the wave's LDS tile (row pitch
+//    17 slots: the row writes, the b128 operand reads of 16 rows and the
+//    transposing reads are all bank-conflict free), are read back as the A
+//    operands of S^T = K Q^T (16x16x32 MFMA), and the V rows then overwrite
+//    the same tile (a wave's LDS operations complete in order), from where
+//    the transposing reads (ds_read_b64_tr_b16) produce the V^T operands of
+//    O^T = V^T P^T;
 //  * one wave per workgroup, no barrier inside the tile loop and ~17 KB of
 //    LDS, so two waves share each SIMD and hide each other's load latency.
 //  * paged KV (PAGED = true): indices are staged as pool rows (block table)
 //    and the rows loaded from 64-bit addresses; padding rows read kZeroRow.
-// (Measured against the LDS-staged variant of sfa_fwd_mfma.hip: MQA prefill
-// 140 -> 122 us, GQA training forward 2.00 -> 1.75 ms.)
 
 #include "sfa_common.h"
 #include "sfa_lds.h"
@@ -38,8 +43,8 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   using M = Mfma<16>;
   typedef M::acc_t acc_t;
 
-  __shared__ int s_idx[kIdxCapD];
-  __shared__ u32x4 s_v[32 * kPV];
+  __shared__ __align__(16) int s_idx[kIdxCapD];
+  __shared__ u32x4 s_v[32 * kPV];  // the K, then the V rows of the current tile
 
   const int lane = threadIdx.x;
   const int lt = lane & 15;  // head (MFMA column) / key row within a 16-row M-tile
@@ -103,50 +108,42 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   istage.template store<PAGED>(p, b, bound, nslots, ntiles * 32, s_idx, lane);
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
 
-  // Loads of tile j (keys 32 j .. 32 j + 31): operand i = 4 mt + s holds, for
-  // key row 16 mt + lt, the 16 bytes at dims 32 s + 8 hq (K: S^T A operand;
-  // V: 16-byte chunk 4 s + hq of the row, written to the staging area).
-  // Invalid keys read from an out-of-range offset and get zeros.
+  // Loads of tile j (keys 32 j .. 32 j + 31): instruction i of a lane loads
+  // the 16 bytes at chunk lt of tile row i + 8 hq, for K into kr[i] and for V
+  // into vr[i] (4 whole rows per instruction; a lane's 8 rows are consecutive,
+  // so their ids are two 16-byte LDS reads).  Invalid keys read from an
+  // out-of-range offset (paged: the zero row) and get zeros.
   auto load_tile = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 id0 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq);
+    const i32x4 id1 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq + 4);
+    const int ids[8] = {id0[0], id0[1], id0[2], id0[3], id1[0], id1[1], id1[2], id1[3]};
     if constexpr (PAGED) {
-      const char* ka[2];
-      const char* va[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int id = s_idx[32 * j + 16 * mt + lt];
-        ka[mt] = id >= 0 ? kbase + pool_row_offset((uint32_t)id, p.page_shift, (uint64_t)(2 * p.k_sb), krow_bytes)
-                         : reinterpret_cast<const char*>(kZeroRow);
-        va[mt] = id >= 0 ? vbase + pool_row_offset((uint32_t)id, p.page_shift, (uint64_t)(2 * p.v_sb), vrow_bytes)
-                         : reinterpret_cast<const char*>(kZeroRow);
+      for (int i = 0; i < 8; ++i) {
+        const char* ka = ids[i] >= 0 ? kbase + pool_row_offset((uint32_t)ids[i], p.page_shift, (uint64_t)(2 * p.k_sb),
+                                                                krow_bytes) + 16 * lt
+                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lt;
+        kr[i] = *reinterpret_cast<const bf16x8*>(ka);
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) kr[4 * mt + s] = *reinterpret_cast<const bf16x8*>(ka[mt] + 64 * s + 16 * hq);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) vr[4 * mt + s] = *reinterpret_cast<const bf16x8*>(va[mt] + 64 * s + 16 * hq);
+      for (int i = 0; i < 8; ++i) {
+        const char* va = ids[i] >= 0 ? vbase + pool_row_offset((uint32_t)ids[i], p.page_shift, (uint64_t)(2 * p.v_sb),
+                                                                vrow_bytes) + 16 * lt
+                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lt;
+        vr[i] = *reinterpret_cast<const bf16x8*>(va);
+      }
     } else {
-      uint32_t ko[2], vo[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int id = s_idx[32 * j + 16 * mt + lt];
-        ko[mt] = id >= 0 ? __umul24((uint32_t)id, krow_bytes) : kOOB;
-        vo[mt] = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) : kOOB;
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t ko = ids[i] >= 0 ? __umul24((uint32_t)ids[i], krow_bytes) + 16u * (uint32_t)lt : kOOB;
+        kr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          kr[4 * mt + s] = __builtin_bit_cast(
-              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          vr[4 * mt + s] = __builtin_bit_cast(
-              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t vo = ids[i] >= 0 ? __umul24((uint32_t)ids[i], vrow_bytes) + 16u * (uint32_t)lt : kOOB;
+        vr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+      }
     }
   };
 
@@ -164,17 +161,23 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   const uint32_t vb0 = (uint32_t)((4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
   const uint32_t vb1 = (uint32_t)((16 + 4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
 
-  auto step = [&](int j, const bf16x8 (&kc)[8], bf16x8 (&vr)[8], bf16x8 (&kn)[8]) {
-    // V of this tile into the staging area (the previous tile's reads of it
-    // are done: LDS operations of a wave complete in order), then the loads
-    // of the next tile into the freed registers
+  auto step = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+    // K rows of this tile into the LDS tile (the previous tile's reads of it
+    // are done: LDS operations of a wave complete in order), its S^T A
+    // operands (row 16 mt + lt, chunk 4 s + hq) back, then the V rows over
+    // them, then the loads of the next tile into the freed registers
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPV + lt]) = kr[i];
+    bf16x8 kc[8];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        *reinterpret_cast<bf16x8*>(&s_v[(16 * mt + lt) * kPV + 4 * s + hq]) = vr[4 * mt + s];
+        kc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPV + 4 * s + hq]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPV + lt]) = vr[i];
     const uint32_t vmask = (uint32_t)__ballot(s_idx[32 * j + (lane & 31)] >= 0);
-    if (j + 1 < ntiles) load_tile(j + 1, kn, vr);
+    if (j + 1 < ntiles) load_tile(j + 1, kr, vr);
 
     // S^T = K Q^T: two 16-key M-tiles
     acc_t sacc[2] = {acc_t{}, acc_t{}};
@@ -231,12 +234,9 @@ __global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
   };
 
   {
-    bf16x8 kA[8], kB[8], vr[8];
-    if (ntiles > 0) load_tile(0, kA, vr);
-    for (int j = 0; j < ntiles; j += 2) {
-      step(j, kA, vr, kB);
-      if (j + 1 < ntiles) step(j + 1, kB, vr, kA);
-    }
+    bf16x8 kr[8], vr[8];
+    if (ntiles > 0) load_tile(0, kr, vr);
+    for (int j = 0; j < ntiles; ++j) step(j, kr, vr);
   }
 
   // ---- finish: row sums over the lane groups sharing a head ---------------
