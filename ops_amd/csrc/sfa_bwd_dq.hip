@@ -6,13 +6,18 @@
 // only produces dQ and dsink, plus the dK/dV rows of index slots that repeat
 // an earlier slot's key (flagged in p.dup; fp32 atomics, as in the atomic
 // scheme).  As in the d = 128 forward (sfa_fwd_d128.hip), one wave holds all
-// G heads of a work item, so a gathered row is used by exactly one wave:
-//  * K and V rows of a 32-key tile go straight from global memory into the A
-//    operand registers of S^T = K Q^T and dP^T = V dO^T (16x16x32 MFMA); K
-//    double-buffered one tile ahead, V reloaded right after its MFMAs;
-//  * the K rows are also written to the wave's LDS area, from which
-//    transposing reads produce the K^T operands of dQ^T += K^T dS^T (the
-//    S^T accumulator layout is already dS^T's B-operand layout);
+// G heads of a work item, so a gathered row is used by exactly one wave and
+// the load pattern decides the gather rate:
+//  * K and V rows of a 32-key tile are loaded one tile ahead into VGPRs as
+//    whole 256-byte rows (4 rows per load instruction; the MFMA operand
+//    layout, 16 rows x 64 bytes per instruction, runs the texture path 3x
+//    slower per byte on L2-resident rows);
+//  * at the start of a tile they go to the wave's two LDS tiles (row pitch
+//    17 slots: row writes, b128 operand reads and transposing reads are all
+//    bank-conflict free), from which the A operands of S^T = K Q^T and
+//    dP^T = V dO^T (16x16x32 MFMA) are read back, and later the transposing
+//    reads of the K^T operands of dQ^T += K^T dS^T (the S^T accumulator
+//    layout is already dS^T's B-operand layout);
 //  * one wave per workgroup and no barrier inside the tile loop.
 // Per pair: P = 2^(S·scale·log2e − lse2) (masked), dS = P (dP − δ).
 
@@ -41,6 +46,7 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) int s_idx[kIdxCapQ];
   __shared__ __attribute__((aligned(16))) uint8_t s_dup[kIdxCapQ];  // slot takes the dK/dV scatter
   __shared__ u32x4 s_k[32 * kPK];
+  __shared__ u32x4 s_v[32 * kPK];
   __shared__ __attribute__((aligned(16))) bf16 s_patch[2][16 * kPStride];
 
   const int lane = threadIdx.x;
@@ -100,24 +106,25 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
 
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
 
-  // Loads of tile j (K or V rows): operand i = 4 mt + s holds, for key row
-  // 16 mt + lt, the 16 bytes at dims 32 s + 8 hq (the A operand of S^T resp.
-  // dP^T; K's is also chunk 4 s + hq of the staged row).  Invalid keys read
-  // zeros.  K is double-buffered one tile ahead; V is reloaded as soon as
-  // this tile's dP^T MFMAs have read it.
-  auto load_rows = [&](int j, const __amdgpu_buffer_rsrc_t& rs, uint32_t row_bytes, bf16x8 (&r)[8]) {
-    uint32_t o[2];
+  // Loads of tile j (K or V rows): instruction i of a lane loads the 16 bytes
+  // at chunk lt of tile row i + 8 hq (4 whole rows per instruction; a lane's 8
+  // rows are consecutive, so their ids are two 16-byte LDS reads).  Invalid
+  // keys read zeros.
+  auto load_rows = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 id0 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq);
+    const i32x4 id1 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq + 4);
+    const int ids[8] = {id0[0], id0[1], id0[2], id0[3], id1[0], id1[1], id1[2], id1[3]};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int id = s_idx[32 * j + 16 * mt + lt];
-      o[mt] = id >= 0 ? __umul24((uint32_t)id, row_bytes) : kOOB;
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t o = ids[i] >= 0 ? __umul24((uint32_t)ids[i], krow_bytes) + 16u * (uint32_t)lt : kOOB;
+      kr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0));
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        r[4 * mt + s] = __builtin_bit_cast(
-            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, o[mt] + (uint32_t)(64 * s + 16 * hq), 0, 0));
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t o = ids[i] >= 0 ? __umul24((uint32_t)ids[i], vrow_bytes) + 16u * (uint32_t)lt : kOOB;
+      vr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0));
+    }
   };
 
   float* dkb = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 128;
@@ -134,23 +141,32 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   const uint32_t r0 = (uint32_t)((4 * hq + rr) * kPK) * 16u + (uint32_t)(4 * cc) * 2u;
   const uint32_t r1 = r0 + (uint32_t)(16 * kPK) * 16u;
 
-  auto step = [&](int j, const bf16x8 (&kc)[8], bf16x8 (&vr)[8], bf16x8 (&kn)[8]) {
-    // K of this tile into the staging area (the previous tile's reads of it
-    // are done: LDS operations of a wave complete in order), then the loads
-    // of the next tile
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        *reinterpret_cast<bf16x8*>(&s_k[(16 * mt + lt) * kPK + 4 * s + hq]) = kc[4 * mt + s];
+  auto step = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
     const int* ib = s_idx + 32 * j;
     const uint32_t vmask = (uint32_t)__ballot(ib[lane & 31] >= 0);
     const bool more = j + 1 < ntiles;
-    if (more) load_rows(j + 1, rk, krow_bytes, kn);
     if (vmask == 0u) {  // wave-uniform: no valid key in this tile
-      if (more) load_rows(j + 1, rv, vrow_bytes, vr);
+      if (more) load_rows(j + 1, kr, vr);
       return;
     }
+    // K and V rows of this tile into the LDS tiles (the previous tile's reads
+    // of them are done: LDS operations of a wave complete in order), the
+    // S^T / dP^T A operands (row 16 mt + lt, chunk 4 s + hq) back, then the
+    // loads of the next tile into the freed registers
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<bf16x8*>(&s_k[(i + 8 * hq) * kPK + lt]) = kr[i];
+      *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPK + lt]) = vr[i];
+    }
+    bf16x8 kc[8], vc[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        kc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_k[(16 * mt + lt) * kPK + 4 * s + hq]);
+        vc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPK + 4 * s + hq]);
+      }
+    if (more) load_rows(j + 1, kr, vr);
 
     // S^T and dP^T: two 16-key M tiles
     f32x4 sacc[2] = {f32x4{}, f32x4{}}, dpacc[2] = {f32x4{}, f32x4{}};
@@ -159,9 +175,8 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         sacc[mt] = mma16x32(kc[4 * mt + s], qb[s], sacc[mt]);
-        dpacc[mt] = mma16x32(vr[4 * mt + s], dob[s], dpacc[mt]);
+        dpacc[mt] = mma16x32(vc[4 * mt + s], dob[s], dpacc[mt]);
       }
-    if (more) load_rows(j + 1, rv, vrow_bytes, vr);
     // P and dS (fp32), packed to bf16 in the B layout of dQ^T = K^T dS^T
     bf16x8 dsb;
     bf16x4_t pv[2], dv[2];
@@ -232,15 +247,9 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   };
 
   {
-    bf16x8 kA[8], kB[8], vr[8];
-    if (ntiles > 0) {
-      load_rows(0, rk, krow_bytes, kA);
-      load_rows(0, rv, vrow_bytes, vr);
-    }
-    for (int j = 0; j < ntiles; j += 2) {
-      step(j, kA, vr, kB);
-      if (j + 1 < ntiles) step(j + 1, kB, vr, kA);
-    }
+    bf16x8 kr[8], vr[8];
+    if (ntiles > 0) load_rows(0, kr, vr);
+    for (int j = 0; j < ntiles; ++j) step(j, kr, vr);
   }
 
   if (!hvalid) return;
