@@ -130,14 +130,14 @@ struct FwdPlan {
 };
 
 constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
-constexpr int kIdxCap = 2048;
 constexpr int kMaxSplits = 64;  // the combine kernel holds one split per lane of a wave
 
 FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
   FwdPlan pl{};
   sfa::Params p = to_params(a, pg);
-  pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p) &&
-            (a->topk + kIdxCap - 1) / kIdxCap <= kMaxSplits;
+  pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p);
+  const int idx_cap = pl.mfma ? sfa::fwd_mfma_idx_cap(p) : 1;
+  pl.mfma = pl.mfma && (a->topk + idx_cap - 1) / idx_cap <= kMaxSplits;
   int splits = 1;
   if (pl.mfma) {
     const int nk = sfa::fwd_mfma_tile_keys(p);
@@ -149,7 +149,7 @@ FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
       splits = (int)((kTargetWorkgroups / 2 + items - 1) / items);
     }
     // each split must fit the staged index window and hold at least one tile
-    const int min_splits = (a->topk + kIdxCap - 1) / kIdxCap;
+    const int min_splits = (a->topk + idx_cap - 1) / idx_cap;
     if (splits < min_splits) splits = min_splits;
     int max_splits = (a->topk + nk - 1) / nk;
     if (splits > max_splits) splits = max_splits;

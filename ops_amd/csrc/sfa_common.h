@@ -214,6 +214,8 @@ hipError_t launch_combine(const Params& p, int dtype, hipStream_t s);
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);  // paged when p.block_table != nullptr
 bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
+int fwd_mfma_idx_cap(const Params& p);  // index slots one work item (split) stages
+int fwd_d128_idx_cap();
 // d = 128, G <= 16: register-direct gather (sfa_fwd_d128.hip)
 bool fwd_d128_supported(const Params& p);
 int fwd_d128_tile_keys();

@@ -19,8 +19,10 @@
 //    the same tile (a wave's LDS operations complete in order), from where
 //    the transposing reads (ds_read_b64_tr_b16) produce the V^T operands of
 //    O^T = V^T P^T;
-//  * one wave per workgroup, no barrier inside the tile loop and ~17 KB of
-//    LDS, so two waves share each SIMD and hide each other's load latency.
+//  * one wave per workgroup, no barrier inside the tile loop, 12.5 KB of LDS
+//    (an index window of 1024 slots: longer top-k sets are split) and at most
+//    168 VGPRs, so three waves share each SIMD and hide each other's load
+//    latency (6 % faster than two).
 //  * paged KV (PAGED = true): indices are staged as pool rows (block table)
 //    and the rows loaded from 64-bit addresses; padding rows read kZeroRow.
 
@@ -32,14 +34,14 @@ namespace sfa {
 namespace {
 
 constexpr float kSlack = 8.0f;  // lazy-rescale slack (base-2 units), as in the MLA kernel
-constexpr int kIdxCapD = 2048;  // slots staged in LDS per work item
+constexpr int kIdxCapD = 1024;  // slots staged in LDS per work item (longer top-k: split-k)
 constexpr int kT = 16;          // heads per wave (MFMA N)
 constexpr int kQSteps = 4;      // 128 / 32 contraction steps of S^T
 constexpr int kOT = 8;          // 128 / 16 O^T dim tiles
 constexpr int kPV = 17;         // V staging row pitch in 16-byte slots (odd: conflict-free reads)
 
 template <bool PAGED>
-__global__ __launch_bounds__(64, 2) void fwd_d128_kernel(Params p) {
+__global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   using M = Mfma<16>;
   typedef M::acc_t acc_t;
 
@@ -288,6 +290,8 @@ bool fwd_d128_supported(const Params& p) {
                                                         fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss));
   return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && addressable;
 }
+
+int fwd_d128_idx_cap() { return kIdxCapD; }
 
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;

@@ -606,6 +606,8 @@ int fwd_mfma_tile_keys(const Params& p) {
   return 32;  // d = 128 kernel: 32-key tiles
 }
 
+int fwd_mfma_idx_cap(const Params& p) { return mla_supported(p) ? kIdxCap : fwd_d128_idx_cap(); }
+
 bool fwd_mfma_supported(const Params& p) { return mla_supported(p) || fwd_d128_supported(p); }
 
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s) {
