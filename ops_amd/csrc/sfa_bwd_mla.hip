@@ -473,11 +473,12 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   __syncthreads();  // the stage area now holds P / dS tiles, output rows and ranks
 
   // ---- LDS layout of the tile loop (16-byte slots of s_stage) -------------
-  // [0, 2048): P / dS tiles (2 x 1024); [2048, 2048 + 2 * 32 * kCP): output
-  // rows (2 x 32 rows); then the ranks of the item's slots (DET)
+  // [0, 2048): P / dS tiles 0 and 1; [2048, 2048 + 2 * 32 * kCP): output rows
+  // (2 x 32 rows); then the ranks of the item's slots (DET); then P / dS tile 2
   constexpr int kOutBase = 2048;
   constexpr int kRankBase = kOutBase + 2 * kMT * kCP;
-  static_assert(kRankBase + kMIdxCap / 4 <= kStage, "tile-loop LDS fits the stage area");
+  constexpr int kPd2Base = kRankBase + kMIdxCap / 4;
+  static_assert(kPd2Base + 1024 <= kStage, "tile-loop LDS fits the stage area");
   int* s_rank = reinterpret_cast<int*>(s_stage + kRankBase);
   if constexpr (DET) {
     // rank of each slot's key among the item's distinct keys (ascending),
@@ -511,21 +512,38 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
     }
   }
 
-  // ---- P / dS tiles: DMA of the dQ pass's blocks into LDS -----------------
+  // ---- P / dS tiles: DMA of the dQ pass's blocks into LDS, two tiles ahead -
   const int tile_slots = 2 * nhg * 4 * 64;  // 16-byte slots per tile (<= 1024)
-  u32x4* buf0 = s_stage;
-  u32x4* buf1 = s_stage + 1024;
+  auto buf = [&](int k) -> u32x4* { return s_stage + (k == 0 ? 0 : k == 1 ? 1024 : kPd2Base); };
   const char* pd_item = reinterpret_cast<const char*>(pd + (int64_t)li * ntiles * 2 * nhg * 4 * pd_block_elems());
-  const __amdgpu_buffer_rsrc_t rpd = make_rsrc(pd_item, (uint32_t)((int64_t)ntiles * tile_slots * 16));
+  // The DMA is issued as inline asm (global_load_lds_dwordx4: M0 = the wave's
+  // LDS destination, lane l writes 16 bytes at M0 + 16 l), which the compiler
+  // does not see: with both tile buffers in one LDS array it cannot tell the
+  // current tile's operand reads from the next tile's DMA target, and for the
+  // builtin form it waited for the DMA (and the previous tile's row stores)
+  // before the first MFMA of every tile.  The loop waits for vmcnt(0) itself
+  // before the barrier that publishes a tile.
   auto load_tile = [&](int tile, u32x4* dst) {
-    for (int i = wave * 64; i < tile_slots; i += kMThreads)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rpd, (lds_void*)(dst + i), 16,
-                                               (uint32_t)(tile * tile_slots + i + lane) * 16u, 0, 0, 0);
+    for (int i = wave * 64; i < tile_slots; i += kMThreads) {
+      const char* src = pd_item + ((int64_t)tile * tile_slots + i + lane) * 16;
+      const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)(dst + i);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+    }
   };
+  auto dma_done = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+  // DET: tile j's barrier needs tile j + 1's DMA, issued at the top of tile
+  // j - 1.  Issued after it: the 9 row stores of tile j - 1 per wave (buffer
+  // stores, unconditional: a row without a rank goes to an out-of-range
+  // offset and is dropped), tile j + 2's DMA, and repeat atomics, so at most
+  // 9 newer operations may still be outstanding: vmcnt(9).
+  auto dma_next_done = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70 | 9); };  // vmcnt(9)
+  static_assert(kMT * kMCH == 9 * kMThreads, "9 row stores per thread and tile");
+
 
   float* const dkv = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 576;
   const int64_t acc_row = (int64_t)p.Hkv * 576;
   bf16* const crow0 = DET ? contrib + (int64_t)li * p.topk * 576 : nullptr;
+  const __amdgpu_buffer_rsrc_t rcon = make_rsrc(crow0, DET ? (uint32_t)p.topk * 1152u : 0u);
 
   // B operands (keys 16 nt + lt, heads 32 ks + 8 hq .. +7) of matrix mat:
   // heads 32 ks + 8 hq + 4 half + rr live in head group (32 ks + 8 hq) / 64,
@@ -544,11 +562,14 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
     return bf16x8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
   };
 
-  if (ntiles > 0) load_tile(0, buf0);
+  if (ntiles > 0) load_tile(0, buf(0));
+  if (ntiles > 1) load_tile(1, buf(1));
+  dma_done();
   __syncthreads();
   for (int j = 0; j < ntiles; ++j) {
-    const u32x4* tb = (j & 1) ? buf1 : buf0;
-    if (j + 1 < ntiles) load_tile(j + 1, (j & 1) ? buf0 : buf1);
+    const u32x4* tb = buf(j % 3);
+    // (tile j - 1's buffer: its reads ended before the last barrier)
+    if (j + 2 < ntiles) load_tile(j + 2, buf((j + 2) % 3));
     // (the first contraction step starts each accumulator from 0 inside the
     // MFMA: no VALU write of an accumulator precedes its MFMA)
     // DET: dims as MFMA rows (lane: dims dim0 + 16 n + 4 hq .. +3 of key
@@ -611,12 +632,16 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
             for (int i = 0; i < 4; ++i) atomicAdd(dst + 16 * n + i, acc[n][nt][i]);
         }
       }
+      dma_next_done();
       __syncthreads();  // output rows staged; the next tile's P / dS landed
       // rows to their rank in the item's contribution block (72 slots a row)
-      for (int u = tid; u < kMT * kMCH; u += kMThreads) {
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const int u = tid + k * kMThreads;
         const int key = u / kMCH, c = u - key * kMCH;
         const int rk = s_rank[j * kMT + key];
-        if (rk >= 0) reinterpret_cast<u32x4*>(crow0 + (int64_t)rk * 576)[c] = orow[key * kCP + c];
+        const uint32_t off = rk >= 0 ? (uint32_t)rk * 1152u + 16u * (uint32_t)c : kOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(orow[key * kCP + c], rcon, off, 0, 0);
       }
     } else {
 #pragma unroll
@@ -629,6 +654,7 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
 #pragma unroll
           for (int n = 0; n < kDN; ++n) atomicAdd(dst + 16 * n, acc[n][nt][i]);
         }
+      dma_done();
       __syncthreads();  // the next tile's P / dS landed; this tile's buffer is free
     }
   }
