@@ -148,15 +148,21 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
     const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh + 8 * hq;
     const bf16* dorow =
         reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh + 8 * hq;
+    // all loads of a row first, then the moves into AGPRs (moving each value
+    // as it arrives made every load wait for the previous one)
+    {
+      bf16x8 x[kMQS];
 #pragma unroll
-    for (int s = 0; s < kMQS; ++s) {
-      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
-      qb[s] = Mfma16A::to_agpr(hvalid ? x : bf16x8{});  // B operands read from AGPRs
+      for (int s = 0; s < kMQS; ++s) x[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+#pragma unroll
+      for (int s = 0; s < kMQS; ++s) qb[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});  // B operands read from AGPRs
     }
+    {
+      bf16x8 x[kMVS];
 #pragma unroll
-    for (int s = 0; s < kMVS; ++s) {
-      bf16x8 x = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
-      dob[s] = Mfma16A::to_agpr(hvalid ? x : bf16x8{});  // B operands read from AGPRs
+      for (int s = 0; s < kMVS; ++s) x[s] = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
+#pragma unroll
+      for (int s = 0; s < kMVS; ++s) dob[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});
     }
   }
   istage.store<false>(p, b, bound, nslots, ntiles * kMT, s_idx, tid);
