@@ -3,9 +3,10 @@
 //
 // Reference: `_attn_bwd_dq_dsink` / `_inner_dq` (SFA.py:856-1002, 613-716).
 // With the deterministic dK/dV scheme (sfa_bwd_csr.hip) the query-major pass
-// only produces dQ and dsink, plus the dK/dV rows of index slots that repeat
-// an earlier slot's key (flagged in p.dup; fp32 atomics, as in the atomic
-// scheme).  As in the d = 128 forward (sfa_fwd_d128.hip), one wave holds all
+// only produces dQ; the dK/dV rows of index slots that repeat an earlier
+// slot's key (flagged in p.dup; absent from ordinary index sets) are added
+// by bwd_dup_kernel with fp32 atomics, as in the atomic scheme, outside this
+// kernel so their registers do not cost it its second wave per SIMD.  As in the d = 128 forward (sfa_fwd_d128.hip), one wave holds all
 // G heads of a work item, so a gathered row is used by exactly one wave and
 // the load pattern decides the gather rate:
 //  * K and V rows of a 32-key tile are loaded one tile ahead into VGPRs as
@@ -27,27 +28,19 @@
 namespace sfa {
 namespace {
 
-constexpr int kIdxCapQ = 2048;  // slots staged in LDS per work item
+constexpr int kIdxCapQ = 2048;  // top-k slots a work item may have
+constexpr int kIdxWin = 512;    // slots staged in LDS at a time (a window of the index row)
 constexpr int kQS = 4;          // 128 / 32 contraction steps over the head dim
 constexpr int kDT = 8;          // 128 / 16 dim tiles
 constexpr int kPK = 17;         // K staging row pitch in 16-byte slots (odd: conflict-free reads)
-constexpr int kPStride = 36;    // P / dS patch row stride (keys) in bf16
-
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
-
 __device__ __forceinline__ f32x4 mma16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mma16x16(bf16x4_t a, bf16x4_t b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
 
-__global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) int s_idx[kIdxCapQ];
-  __shared__ __attribute__((aligned(16))) uint8_t s_dup[kIdxCapQ];  // slot takes the dK/dV scatter
+__global__ __launch_bounds__(64, 2) void bwd_dq_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) int s_idx[kIdxWin];
   __shared__ u32x4 s_k[32 * kPK];
   __shared__ u32x4 s_v[32 * kPK];
-  __shared__ __attribute__((aligned(16))) bf16 s_patch[2][16 * kPStride];
 
   const int lane = threadIdx.x;
   const int lt = lane & 15;  // head column / key row within a 16-row M-tile
@@ -59,19 +52,8 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   const int t = wi % p.Sq;
   const int b = wi / p.Sq;
   const int nslots = p.topk;
-  const int ntiles = (nslots + 31) / 32;
-
-  {
-    const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
-    const uint8_t* drow = p.dup + (((int64_t)b * p.Sq + t) * p.Hkv + g) * p.topk;
-    const int bound = bound_of(p, b);
-    for (int i = lane; i < ntiles * 32; i += 64) {
-      const int id = (i < nslots) ? irow[i] : -1;
-      const bool valid = id >= 0 && id < bound;
-      s_idx[i] = valid ? id : -1;
-      s_dup[i] = valid && drow[i] != 0;
-    }
-  }
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
 
   const bool hvalid = lt < p.G;
   const int h = g * p.G + (hvalid ? lt : 0);
@@ -104,7 +86,6 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
 
-  __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
 
   // Loads of tile j (K or V rows): instruction i of a lane loads the 16 bytes
   // at chunk lt of tile row i + 8 hq (4 whole rows per instruction; a lane's 8
@@ -127,10 +108,6 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
     }
   };
 
-  float* dkb = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 128;
-  float* dvb = p.dv_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 128;
-  const int64_t acc_row = (int64_t)p.Hkv * 128;
-
   f32x4 dqacc[kDT];
 #pragma unroll
   for (int i = 0; i < kDT; ++i) dqacc[i] = f32x4{};
@@ -141,10 +118,11 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
   const uint32_t r0 = (uint32_t)((4 * hq + rr) * kPK) * 16u + (uint32_t)(4 * cc) * 2u;
   const uint32_t r1 = r0 + (uint32_t)(16 * kPK) * 16u;
 
-  auto step = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+  // tile j of the staged window of wt tiles
+  auto step = [&](int j, int wt, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
     const int* ib = s_idx + 32 * j;
     const uint32_t vmask = (uint32_t)__ballot(ib[lane & 31] >= 0);
-    const bool more = j + 1 < ntiles;
+    const bool more = j + 1 < wt;
     if (vmask == 0u) {  // wave-uniform: no valid key in this tile
       if (more) load_rows(j + 1, kr, vr);
       return;
@@ -158,28 +136,34 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
       *reinterpret_cast<bf16x8*>(&s_k[(i + 8 * hq) * kPK + lt]) = kr[i];
       *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPK + lt]) = vr[i];
     }
-    bf16x8 kc[8], vc[8];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        kc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_k[(16 * mt + lt) * kPK + 4 * s + hq]);
-        vc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPK + 4 * s + hq]);
-      }
     if (more) load_rows(j + 1, kr, vr);
 
-    // S^T and dP^T: two 16-key M tiles
+    // S^T and dP^T: two 16-key M tiles; the A operands (row 16 mt + lt,
+    // chunk 4 s + hq) are read one contraction step ahead of their MFMAs
+    // (the pins keep the compiler from hoisting all 16 reads, whose registers
+    // would not fit next to a second wave on the SIMD)
     f32x4 sacc[2] = {f32x4{}, f32x4{}}, dpacc[2] = {f32x4{}, f32x4{}};
-#pragma unroll
-    for (int s = 0; s < kQS; ++s)
+    auto read_ops = [&](int s, bf16x8 (&kc)[2], bf16x8 (&vc)[2]) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        sacc[mt] = mma16x32(kc[4 * mt + s], qb[s], sacc[mt]);
-        dpacc[mt] = mma16x32(vc[4 * mt + s], dob[s], dpacc[mt]);
+        kc[mt] = *reinterpret_cast<const bf16x8*>(&s_k[(16 * mt + lt) * kPK + 4 * s + hq]);
+        vc[mt] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPK + 4 * s + hq]);
       }
-    // P and dS (fp32), packed to bf16 in the B layout of dQ^T = K^T dS^T
+    };
+    bf16x8 kc[2][2], vc[2][2];
+    read_ops(0, kc[0], vc[0]);
+#pragma unroll
+    for (int s = 0; s < kQS; ++s) {
+      if (s + 1 < kQS) read_ops(s + 1, kc[(s + 1) & 1], vc[(s + 1) & 1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        sacc[mt] = mma16x32(kc[s & 1][mt], qb[s], sacc[mt]);
+        dpacc[mt] = mma16x32(vc[s & 1][mt], dob[s], dpacc[mt]);
+      }
+      asm volatile("" ::: "memory");
+    }
+    // dS (fp32), packed to bf16 in the B layout of dQ^T = K^T dS^T
     bf16x8 dsb;
-    bf16x4_t pv[2], dv[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -187,10 +171,7 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
         const int key = mt * 16 + 4 * hq + e;
         const bool valid = (vmask >> key) & 1u;
         const float pr = valid ? exp2f(sacc[mt][e] * p.scale_log2 - lse2) : 0.f;
-        const float ds = pr * (dpacc[mt][e] - delta);
-        pv[mt][e] = (bf16)pr;
-        dv[mt][e] = (bf16)ds;
-        dsb[4 * mt + e] = dv[mt][e];
+        dsb[4 * mt + e] = (bf16)(pr * (dpacc[mt][e] - delta));
       }
     // dQ^T += K^T dS^T: A = K^T from the staged tile (transposing reads)
 #pragma unroll
@@ -200,56 +181,22 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
       const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       dqacc[ot] = mma16x32(a, dsb, dqacc[ot]);
     }
-    // Repeated keys: dV = P^T dO and dK = scale dS^T Q over the G heads for
-    // the flagged slots, rows scattered atomically.  P^T / dS^T go through a
-    // [head][key] patch and come back (transposing reads) as the A operands
-    // of the head contractions (16x16x16); the head-side B operands are read
-    // from global memory here (rare path).
-    const uint8_t* fb = s_dup + 32 * j;
-    if (__ballot(fb[lane & 31] != 0) == 0u) return;  // wave-uniform: nothing to scatter
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      *reinterpret_cast<bf16x4_t*>(&s_patch[0][lt * kPStride + mt * 16 + 4 * hq]) = pv[mt];
-      *reinterpret_cast<bf16x4_t*>(&s_patch[1][lt * kPStride + mt * 16 + 4 * hq]) = dv[mt];
-    }
-    const bf16* q0 = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)(g * p.G) * p.q_sh;
-    const bf16* d0 = reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)(g * p.G) * p.do_sh;
-#pragma unroll 1
-    for (int mk = 0; mk < 2; ++mk) {
-      const uint32_t poff = (uint32_t)(((4 * hq + rr) * kPStride + mk * 16 + 4 * cc) * 2);
-      const bf16x4 ap = lds_read_tr16(s_patch[0], poff);
-      const bf16x4 as = lds_read_tr16(s_patch[1], poff);
-      const int4 ids = *reinterpret_cast<const int4*>(ib + mk * 16 + 4 * hq);
-      const uchar4 fl = *reinterpret_cast<const uchar4*>(fb + mk * 16 + 4 * hq);
-      const int idv[4] = {fl.x ? ids.x : -1, fl.y ? ids.y : -1, fl.z ? ids.z : -1, fl.w ? ids.w : -1};
-#pragma unroll 1
-      for (int nd = 0; nd < kDT; ++nd) {
-        // B operands over heads: lane holds heads 4hq .. 4hq+3 of dim 16nd + lt
-        bf16x4_t qh, doh;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int hh = 4 * hq + e;
-          const bool ok = hh < p.G;
-          qh[e] = ok ? q0[(int64_t)hh * p.q_sh + 16 * nd + lt] : (bf16)0.f;
-          doh[e] = ok ? d0[(int64_t)hh * p.do_sh + 16 * nd + lt] : (bf16)0.f;
-        }
-        const f32x4 dvr = mma16x16(ap, doh, f32x4{});
-        const f32x4 dkr = mma16x16(as, qh, f32x4{});
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (idv[e] >= 0) {
-            atomicAdd(dvb + (int64_t)idv[e] * acc_row + 16 * nd + lt, dvr[e]);
-            atomicAdd(dkb + (int64_t)idv[e] * acc_row + 16 * nd + lt, dkr[e] * p.scale);
-          }
-        }
-      }
-    }
   };
 
-  {
+  // The index row in windows of kIdxWin slots (invalid -> -1), so the LDS
+  // (window + two row tiles, 19.4 KB) leaves room for two waves per SIMD.
+  for (int base = 0; base < nslots; base += kIdxWin) {
+    const int wn = min(kIdxWin, nslots - base);
+    const int wt = (wn + 31) / 32;
+    __syncthreads();  // (one wave: the previous window's reads come first)
+    for (int i = lane; i < wt * 32; i += 64) {
+      const int id = (i < wn) ? irow[base + i] : -1;
+      s_idx[i] = (id >= 0 && id < bound) ? id : -1;
+    }
+    __syncthreads();
     bf16x8 kr[8], vr[8];
-    if (ntiles > 0) load_rows(0, kr, vr);
-    for (int j = 0; j < ntiles; ++j) step(j, kr, vr);
+    load_rows(0, kr, vr);
+    for (int j = 0; j < wt; ++j) step(j, wt, kr, vr);
   }
 
   if (!hvalid) return;
@@ -260,6 +207,72 @@ __global__ __launch_bounds__(64, 1) void bwd_dq_kernel(Params p) {
     const bf16x4 v4 = {(bf16)(dqacc[ot][0] * p.scale), (bf16)(dqacc[ot][1] * p.scale), (bf16)(dqacc[ot][2] * p.scale),
                        (bf16)(dqacc[ot][3] * p.scale)};
     *reinterpret_cast<bf16x4*>(dqrow + 16 * ot + 4 * hq) = v4;
+  }
+}
+
+// dK/dV of index slots that repeat an earlier slot's key in their row (p.dup,
+// written by the index inversion; the key-major pass counts each key once
+// per row).  Such slots are absent from ordinary index sets, so this is
+// plain VALU code: one wave per work item scans its flags and, per flagged
+// slot and head, forms S and dP as dot products over the 128 dims (2 per
+// lane), P and dS, and adds P dO and scale dS Q to the key's rows with fp32
+// atomics (SFA.py:719-853 for the math).
+__global__ __launch_bounds__(256) void bwd_dup_kernel(Params p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= (int64_t)p.B * p.Sq * p.Hkv) return;  // the whole wave
+  const int g = (int)(item % p.Hkv);
+  const int t = (int)((item / p.Hkv) % p.Sq);
+  const int b = (int)(item / ((int64_t)p.Hkv * p.Sq));
+  const uint8_t* drow = p.dup + item * p.topk;
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
+  float* const dkb = p.dk_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 128 + 2 * lane;
+  float* const dvb = p.dv_acc + ((int64_t)b * p.Skv * p.Hkv + g) * 128 + 2 * lane;
+  const int64_t acc_row = (int64_t)p.Hkv * 128;
+  auto wave_sum = [](float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+  };
+  for (int i0 = 0; i0 < p.topk; i0 += 64) {
+    const int i = i0 + lane;
+    int id = -1;
+    if (i < p.topk && drow[i] != 0) id = irow[i];
+    const bool flagged = id >= 0 && id < bound;
+    uint64_t m = __ballot(flagged);
+    while (m != 0) {
+      const int sl = __builtin_ctzll(m);
+      m &= m - 1;
+      const int key = __shfl(id, sl, 64);
+      const bf16* krow = reinterpret_cast<const bf16*>(p.k) + b * p.k_sb + (int64_t)key * p.k_ss + g * p.k_sh;
+      const bf16* vrow = reinterpret_cast<const bf16*>(p.v) + b * p.v_sb + (int64_t)key * p.v_ss + g * p.v_sh;
+      const float k0 = (float)krow[2 * lane], k1 = (float)krow[2 * lane + 1];
+      const float v0 = (float)vrow[2 * lane], v1 = (float)vrow[2 * lane + 1];
+      float dv0 = 0.f, dv1 = 0.f, dk0 = 0.f, dk1 = 0.f;
+      for (int hh = 0; hh < p.G; ++hh) {
+        const int h = g * p.G + hh;
+        const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+        if (lse == kNegInf) continue;  // a row with no valid slot
+        const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh;
+        const bf16* dorow =
+            reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh;
+        const float q0 = (float)qrow[2 * lane], q1 = (float)qrow[2 * lane + 1];
+        const float d0 = (float)dorow[2 * lane], d1 = (float)dorow[2 * lane + 1];
+        const float sc = wave_sum(q0 * k0 + q1 * k1);
+        const float dp = wave_sum(d0 * v0 + d1 * v1);
+        const float pr = exp2f(sc * p.scale_log2 - lse * kLog2e);
+        const float ds = pr * (dp - p.delta[((int64_t)b * p.Sq + t) * p.Hq + h]);
+        dv0 += pr * d0;
+        dv1 += pr * d1;
+        dk0 += ds * q0;
+        dk1 += ds * q1;
+      }
+      atomicAdd(dvb + (int64_t)key * acc_row, dv0);
+      atomicAdd(dvb + (int64_t)key * acc_row + 1, dv1);
+      atomicAdd(dkb + (int64_t)key * acc_row, dk0 * p.scale);
+      atomicAdd(dkb + (int64_t)key * acc_row + 1, dk1 * p.scale);
+    }
   }
 }
 
@@ -276,6 +289,9 @@ bool bwd_dq_supported(const Params& p) {
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
   hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(bwd_dup_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -109,6 +109,19 @@ def test_csr_repeated_keys():
     _check_vs_oracle(q, k, v, do, idx, _run(q, k, v, do, idx, "csr"))
 
 
+def test_csr_topk_over_several_index_windows():
+    """K = 1700: the dQ pass stages the index row in windows of 512 slots, so
+    this row spans four windows, the last partial (164 slots, not a multiple
+    of the 32-key tile); non-causal indices with repeats, kv_lens and a
+    sink."""
+    _say("csr bwd non-causal Sq=48 Skv=4000 B=2 G=4 K=1700 repeats kv_lens sink")
+    q, k, v, do, idx = _inputs(2, 48, 4000, 8, 2, 1700, seed=31, causal=False, repeats=0.02)
+    kv_lens = torch.tensor([4000, 3100], dtype=torch.int32)
+    sink = torch.linspace(-0.5, 1.0, 8)
+    res = _run(q, k, v, do, idx, "csr", kv_lens=kv_lens, sink=sink)
+    _check_vs_oracle(q, k, v, do, idx, res, kv_lens=kv_lens, sink=sink)
+
+
 def test_csr_matches_atomic_and_is_deterministic():
     """The GQA training workload (reduced): CSR equals the atomic scheme to
     accumulation-order rounding, and two CSR runs are bitwise identical."""
