@@ -41,7 +41,10 @@ namespace {
 
 constexpr int kKeyBlock = 128;          // keys per key block (4 waves x 32)
 constexpr int kRowBlock = 128;          // query-head rows per query block
-constexpr int kChunk = 128;             // query blocks per workgroup
+#ifndef SFA_CSR_CHUNK
+#define SFA_CSR_CHUNK 128
+#endif
+constexpr int kChunk = SFA_CSR_CHUNK;   // query blocks per workgroup
 constexpr int kD = 128;                 // head dim (d_qk = d_v)
 constexpr int kCH = kD / 8;             // 16-byte chunks per row
 constexpr int kTB = kRowBlock * kCH;    // slots per Q or dO block buffer
@@ -101,7 +104,9 @@ __global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
   const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
   int* list = p.blist + bgk * p.nqb;
   int* start = p.bstart + bgk * (p.max_chunks + 1);
-  static_assert(2 * kChunk == 256, "one iteration covers two chunks");
+  constexpr int kCPI = 256 / kChunk;  // chunks per iteration
+  constexpr int kWPC = kChunk / 64;   // waves per chunk
+  static_assert(kCPI * kChunk == 256 && kWPC * 64 == kChunk, "an iteration covers whole chunks of whole waves");
   int total = 0;
   for (int q0 = 0; q0 < p.nqb; q0 += 256) {
     const int qb = q0 + tid;
@@ -120,12 +125,17 @@ __global__ __launch_bounds__(256) void csr_blocklist_kernel(Params p) {
     int pos = total + __popcll(m & ((1ull << lane) - 1ull));
     for (int w = 0; w < wave; ++w) pos += s_cnt[w];
     if (any) list[pos] = qb;
-    // chunk starts: query blocks [128 c, 128 (c + 1)) are this iteration's
-    // two halves (waves 0-1 and 2-3)
+    // chunk starts: the kChunk query blocks of chunk c0 + i are those of
+    // waves kWPC i .. kWPC (i + 1) - 1 of this iteration
     const int c0 = q0 / kChunk;
     if (tid == 0) {
-      start[c0] = total;
-      if (c0 + 1 <= p.max_chunks) start[c0 + 1] = total + s_cnt[0] + s_cnt[1];
+      int acc = total;
+#pragma unroll
+      for (int i = 0; i < kCPI; ++i) {
+        if (c0 + i <= p.max_chunks) start[c0 + i] = acc;
+#pragma unroll
+        for (int w = 0; w < kWPC; ++w) acc += s_cnt[kWPC * i + w];
+      }
     }
     total += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
     __syncthreads();

@@ -235,7 +235,18 @@ __global__ __launch_bounds__(256) void bwd_dup_kernel(Params p) {
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
     return x;
   };
+  // skip 1024-slot blocks without a flag with one 16-byte read per lane (the
+  // flag rows are 16-byte aligned when topk is a multiple of 16)
+  const bool vec = p.topk % 16 == 0;
   for (int i0 = 0; i0 < p.topk; i0 += 64) {
+    if (vec && i0 % 1024 == 0) {
+      const int v0 = i0 + 16 * lane;
+      const u32x4 f = v0 < p.topk ? *reinterpret_cast<const u32x4*>(drow + v0) : u32x4{0u, 0u, 0u, 0u};
+      if (__ballot((f.x | f.y | f.z | f.w) != 0u) == 0) {
+        i0 += 1024 - 64;  // (the loop adds the other 64)
+        continue;
+      }
+    }
     const int i = i0 + lane;
     int id = -1;
     if (i < p.topk && drow[i] != 0) id = irow[i];
