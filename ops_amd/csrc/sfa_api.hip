@@ -381,6 +381,8 @@ int mla_chunk_items(const sfa::Params& p, bool det) {
   const int64_t items = (int64_t)p.B * p.Sq * p.Hkv;
   int64_t n = (int64_t)(kMlaChunkBytes / sfa::bwd_mla_bytes_per_item(p, det));
   n = n >= kMlaChunkRound ? n / kMlaChunkRound * kMlaChunkRound : (n / 8 * 8 > 8 ? n / 8 * 8 : 8);
+  const int64_t cap = sfa::bwd_mla_max_chunk_items(det);  // a multiple of kMlaChunkRound
+  if (n > cap) n = cap;
   return (int)(n < items ? n : items);
 }
 

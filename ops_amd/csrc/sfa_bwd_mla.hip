@@ -666,87 +666,103 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   }
 }
 
-// Deterministic reduction of a chunk's contributions: one wave per key (b, g,
-// key), summing the key's rows of the chunk's items in item order into the
-// fp32 accumulator row (each row owned by one wave; chunks run in order).
-// Lane l holds dims 8 l .. 8 l + 7, lanes 0..7 also dims 512 + 8 l ...
-__global__ __launch_bounds__(256) void mla_bwd_reduce_kernel(Params p, int64_t item0, int nitems, int b0, int nb,
-                                                             const bf16* contrib, const uint32_t* kmap,
-                                                             const uint16_t* prefix, int W) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t wi = (int64_t)blockIdx.x * 4 + wave;
-  const int key = (int)(wi % p.Skv);
-  const int64_t r = wi / p.Skv;
+// Deterministic reduction of a chunk's contributions: a workgroup of 16
+// waves owns 16 keys, half of one membership-bitmap word (b, g, word); it
+// stages that word and its prefix count for each of the chunk's items of
+// (b, g) in LDS (one scattered read per item for all 16 keys, instead of one
+// per item and key), then each wave sums the rows of its key in item order
+// into the fp32 accumulator row (each row owned by one wave; chunks run in
+// order).  Lane l holds dims 8 l .. 8 l + 7, lanes 0..7 also dims 512 + 8 l
+// ..; a chunk holds at most kRedItems items (host-side cap).
+constexpr int kRedItems = 1024;
+constexpr int kRedThreads = 1024;
+__global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(Params p, int64_t item0, int nitems, int b0,
+                                                                     int nb, const bf16* contrib,
+                                                                     const uint32_t* kmap, const uint16_t* prefix,
+                                                                     int W) {
+  __shared__ uint32_t s_word[kRedItems];
+  __shared__ uint16_t s_pre[kRedItems];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = (p.Skv + 31) / 32;
+  const int wsel = (int)((blockIdx.x >> 1) % nw);
+  const int half = (int)(blockIdx.x & 1);
+  const int64_t r = (blockIdx.x >> 1) / nw;
   const int g = (int)(r % p.Hkv);
   const int b = b0 + (int)(r / p.Hkv);
-  if (r >= (int64_t)nb * p.Hkv) return;
-  // this (b, g)'s items of the chunk: item = (b Sq + t) Hkv + g
+  if (r >= (int64_t)nb * p.Hkv) return;  // the whole workgroup
+  // this (b, g)'s items of the chunk: item = (b Sq + t) Hkv + g, stride Hkv
   const int64_t first = ((int64_t)b * p.Sq) * p.Hkv + g;
-  int64_t lo = first < item0 ? item0 + ((g - item0 % p.Hkv) + p.Hkv) % p.Hkv : first;
+  const int64_t lo = first < item0 ? item0 + ((g - item0 % p.Hkv) + p.Hkv) % p.Hkv : first;
   const int64_t hi_b = ((int64_t)(b + 1) * p.Sq) * p.Hkv;
   const int64_t hi = hi_b < item0 + nitems ? hi_b : item0 + nitems;
-  const int wsel = key >> 5;
-  const uint32_t bit = 1u << (key & 31);
-  float a0[8] = {}, a1[8] = {};
-  bool any = false;
-  // items in batches of 64 (one per lane); the rows of the batch's hits are
-  // loaded 8 at a time, then added in item order
-  for (int64_t base = lo; base < hi; base += 64 * (int64_t)p.Hkv) {
-    const int64_t it = base + (int64_t)lane * p.Hkv;
-    const int li = (int)(it - item0);
-    uint32_t word = 0;
-    int rank = 0;
-    if (it < hi) {
-      word = kmap[(int64_t)li * W + wsel];
-      rank = prefix[(int64_t)li * W + wsel] + __builtin_popcount(word & (bit - 1u));
-    }
-    uint64_t hits = __ballot((word & bit) != 0u);
-    while (hits) {
-      int n = 0;
-      constexpr int U = 8;
-      int lis[U], rks[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        lis[u] = -1;
-        rks[u] = 0;
-        if (hits) {
-          const int l = __builtin_ctzll(hits);
-          hits &= hits - 1;
-          lis[u] = (int)(base - item0) + l * p.Hkv;
-          rks[u] = __builtin_amdgcn_readlane(rank, l);
-          ++n;
-        }
-      }
-      u32x4 v0[U], v1[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (lis[u] >= 0) {
-          const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)lis[u] * p.topk + rks[u]) * 576);
-          v0[u] = row[lane];
-          v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (lis[u] < 0) continue;
-        const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
-        const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          a0[e] += (float)x0[e];
-          a1[e] += (float)x1[e];
-        }
-      }
-      any = any || n > 0;
-    }
+  const int nit = lo < hi ? (int)((hi - lo + p.Hkv - 1) / p.Hkv) : 0;  // <= kRedItems
+  const int li0 = (int)(lo - item0);
+  for (int i = tid; i < nit; i += kRedThreads) {
+    const int li = li0 + i * p.Hkv;
+    s_word[i] = kmap[(int64_t)li * W + wsel];
+    s_pre[i] = prefix[(int64_t)li * W + wsel];
   }
-  if (!any || key >= bound_of(p, b)) return;
-  float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
+  __syncthreads();
+  const int bound = bound_of(p, b);
+  {
+    const int kbit = 16 * half + wave;
+    const int key = 32 * wsel + kbit;
+    if (key >= p.Skv) return;  // the whole wave
+    const uint32_t bit = 1u << kbit;
+    float a0[8] = {}, a1[8] = {};
+    bool any = false;
+    // items in batches of 64 (one per lane); the rows of the batch's hits are
+    // loaded 8 at a time, then added in item order
+    for (int ib = 0; ib < nit; ib += 64) {
+      const int i = ib + lane;
+      const uint32_t word = i < nit ? s_word[i] : 0u;
+      const int rank = i < nit ? (int)s_pre[i] + __builtin_popcount(word & (bit - 1u)) : 0;
+      uint64_t hits = __ballot((word & bit) != 0u);
+      while (hits) {
+        constexpr int U = 8;
+        int lis[U], rks[U];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
-  if (lane < 8) {
+        for (int u = 0; u < U; ++u) {
+          lis[u] = -1;
+          rks[u] = 0;
+          if (hits) {
+            const int l = __builtin_ctzll(hits);
+            hits &= hits - 1;
+            lis[u] = li0 + (ib + l) * p.Hkv;
+            rks[u] = __builtin_amdgcn_readlane(rank, l);
+          }
+        }
+        u32x4 v0[U], v1[U];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
+        for (int u = 0; u < U; ++u) {
+          if (lis[u] >= 0) {
+            const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)lis[u] * p.topk + rks[u]) * 576);
+            v0[u] = row[lane];
+            v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (lis[u] < 0) continue;
+          const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
+          const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            a0[e] += (float)x0[e];
+            a1[e] += (float)x1[e];
+          }
+        }
+        any = true;
+      }
+    }
+    if (!any || key >= bound) return;
+    float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
+    if (lane < 8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
+    }
   }
 }
 
@@ -760,6 +776,8 @@ bool bwd_mla_supported(const Params& p) {
 }
 
 bool bwd_mla_det_supported(const Params& p) { return p.Skv <= kMaxMapW * 32; }
+
+int bwd_mla_max_chunk_items(bool det) { return det ? kRedItems : 1 << 30; }
 
 int bwd_mla_map_words(const Params& p) { return (p.Skv + 2047) / 2048 * 64; }
 
@@ -799,8 +817,8 @@ hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws,
                        (const uint8_t*)dup, W);
     const int b0 = (int)(item0 / ((int64_t)p.Hkv * p.Sq));
     const int b1 = (int)((item0 + n - 1) / ((int64_t)p.Hkv * p.Sq));
-    const int64_t waves = (int64_t)(b1 - b0 + 1) * p.Hkv * p.Skv;
-    hipLaunchKernelGGL(mla_bwd_reduce_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, item0, n, b0,
+    const int64_t groups = (int64_t)(b1 - b0 + 1) * p.Hkv * ((p.Skv + 31) / 32) * 2;
+    hipLaunchKernelGGL(mla_bwd_reduce_kernel, dim3((unsigned)groups), dim3(kRedThreads), 0, s, p, item0, n, b0,
                        b1 - b0 + 1, (const bf16*)contrib, (const uint32_t*)kmap, (const uint16_t*)prefix, W);
   } else {
     hipLaunchKernelGGL(mla_bwd_dkv_kernel<false>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,

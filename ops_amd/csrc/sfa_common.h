@@ -226,7 +226,8 @@ bool bwd_mfma_supported(const Params& p);
 // of work items (det: plus index maps and the ordered reduction); the chunk's
 // workspace holds bwd_mla_bytes_per_item per item
 bool bwd_mla_supported(const Params& p);
-bool bwd_mla_det_supported(const Params& p);  // deterministic dK/dV: Skv <= 65536
+bool bwd_mla_det_supported(const Params& p);
+int bwd_mla_max_chunk_items(bool det);  // the deterministic reduction stages a chunk's items in LDS  // deterministic dK/dV: Skv <= 65536
 size_t bwd_mla_bytes_per_item(const Params& p, bool det);
 hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
