@@ -41,10 +41,7 @@ namespace {
 
 constexpr int kKeyBlock = 128;          // keys per key block (4 waves x 32)
 constexpr int kRowBlock = 128;          // query-head rows per query block
-#ifndef SFA_CSR_CHUNK
-#define SFA_CSR_CHUNK 128
-#endif
-constexpr int kChunk = SFA_CSR_CHUNK;   // query blocks per workgroup
+constexpr int kChunk = 128;             // query blocks per workgroup (64 measured slower)
 constexpr int kD = 128;                 // head dim (d_qk = d_v)
 constexpr int kCH = kD / 8;             // 16-byte chunks per row
 constexpr int kTB = kRowBlock * kCH;    // slots per Q or dO block buffer
