@@ -72,7 +72,7 @@ def scan(asm: str):
 
 # Kernels whose MFMAs are inline asm (the compiler inserts no wait states for
 # them); kernels built on the MFMA builtins get theirs from the compiler.
-INLINE_ASM_MFMA_KERNELS = ("dkv_keymajor_kernel", "fwd_mfma_kernel")
+INLINE_ASM_MFMA_KERNELS = ("dkv_keymajor_kernel", "fwd_mfma_kernel", "mla_bwd_dq_kernel", "mla_bwd_dkv_kernel")
 DRAIN = 18  # wait states the inline-asm drains provide (at least) after an MFMA before VALU reads
 
 
@@ -249,8 +249,8 @@ def test_no_early_reads_of_inline_asm_mfma_results(tmp_path):
     explicit drains) earlier than the hardware requirement."""
     need = required_read_wait_states(tmp_path)
     assert 8 <= need <= DRAIN, need
-    srcs = [s for s in sfa_build.sources() if Path(s).stem in ("sfa_bwd_csr", "sfa_fwd_mfma")]
-    assert len(srcs) == 2
+    srcs = [s for s in sfa_build.sources() if Path(s).stem in ("sfa_bwd_csr", "sfa_fwd_mfma", "sfa_bwd_mla")]
+    assert len(srcs) == 3
     asms = [_device_asm(Path(s), tmp_path) for s in srcs]
     assert sum(a.count("v_mfma") for a in asms) > 300
     hits = [h for a in asms for h in scan_result_reads(a, drain=need)]
