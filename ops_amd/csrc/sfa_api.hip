@@ -476,15 +476,18 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
   if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
   if (e == hipSuccess && csr) e = sfa::launch_csr_index(p, s);  // before dQ: it reads the repeat flags
-  if (e == hipSuccess) {
-    if (csr)
-      e = sfa::launch_bwd_dq(p, s);
-    else if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
+  if (e == hipSuccess && csr) {
+    e = sfa::launch_bwd_dq(p, s);
+    if (e == hipSuccess) e = sfa::launch_csr_dkv(p, s);
+    // (after the ordered dK/dV reduction, which adds into the same
+    // accumulators without atomics)
+    if (e == hipSuccess) e = sfa::launch_bwd_dup(p, s);
+  } else if (e == hipSuccess) {
+    if (bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p))
       e = sfa::launch_bwd_mfma(p, s);
     else
       e = sfa::launch_bwd_generic(p, f.dtype, s);
   }
-  if (e == hipSuccess && csr) e = sfa::launch_csr_dkv(p, s);
   if (e == hipSuccess) {
     if (merge)
       e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, true, s);

@@ -300,8 +300,11 @@ bool bwd_dq_supported(const Params& p) {
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
   hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dup(const Params& p, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
   hipLaunchKernelGGL(bwd_dup_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p);
   return hipGetLastError();
 }

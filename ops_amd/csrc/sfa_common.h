@@ -232,7 +232,8 @@ size_t bwd_mla_bytes_per_item(const Params& p, bool det);
 hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
 bool bwd_dq_supported(const Params& p);
-hipError_t launch_bwd_dq(const Params& p, hipStream_t s);
+hipError_t launch_bwd_dq(const Params& p, hipStream_t s);   // dQ of the deterministic scheme
+hipError_t launch_bwd_dup(const Params& p, hipStream_t s);  // dK/dV of repeated-key slots (fp32 atomics)
 // deterministic dK/dV
 bool bwd_csr_supported(const Params& p);
 void csr_geometry(Params& p);                 // fills kmap_w, nkb, nqb, lg_g, max_chunks
