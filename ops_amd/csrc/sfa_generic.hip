@@ -301,8 +301,8 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
   const int t = (row / p.Hq) % p.Sq;
   const int b = row / ((int64_t)p.Hq * p.Sq);
   const float ls = lane < p.num_splits ? p.part_lse[lane * nrows + row] : kNegInf;
-  const float m = wave_max(ls);
   const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  const float m = wave_max(ls);
   const float mm = fmaxf(m, sink2);
   const float e = (ls == kNegInf || mm == kNegInf) ? 0.f : exp2f(ls - mm);
   float l = wave_sum(e);
@@ -334,6 +334,44 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
       orow[d] = from_f32<T>(acc);
     }
   }
+  if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
+}
+
+// The same merge for NS splits and d_v = 512 (the MLA decode): a wave
+// issues its NS partial-row loads together with the LSE loads, before the
+// weights that need the LSEs are formed, so it waits for one memory round
+// trip instead of one per split.
+template <typename T, int NS>
+__global__ __launch_bounds__(kThreads) void combine512_kernel(Params p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  if (row >= nrows) return;
+  const int h = row % p.Hq;
+  const int t = (row / p.Hq) % p.Sq;
+  const int b = row / ((int64_t)p.Hq * p.Sq);
+  const float ls = lane < NS ? p.part_lse[lane * nrows + row] : kNegInf;
+  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  bf16x8 pv[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) pv[s] = *reinterpret_cast<const bf16x8*>(p.part_o + (s * nrows + row) * 512 + 8 * lane);
+  const float m = wave_max(ls);
+  const float mm = fmaxf(m, sink2);
+  const float e = (ls == kNegInf || mm == kNegInf) ? 0.f : exp2f(ls - mm);
+  float l = wave_sum(e);
+  if (p.sink && mm != kNegInf) l += exp2f(sink2 - mm);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float wl = e * inv;  // weight of split `lane`
+  float acc[8] = {};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float w = __shfl(wl, s, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += w * (float)pv[s][j];
+  }
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) orow[8 * lane + j] = from_f32<T>(acc[j]);
   if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
 }
 
@@ -458,6 +496,20 @@ hipError_t launch_bwd_finish_merged(const Params& p, int dtype, void* dk, int64_
 hipError_t launch_combine(const Params& p, int dtype, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.Sq * p.Hq;
   const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (p.Dv == 512 && (p.num_splits == 2 || p.num_splits == 4 || p.num_splits == 8)) {
+#define SFA_COMBINE512(NS)                                                              \
+  if (p.num_splits == NS) {                                                               \
+    if (dtype == SFA_DTYPE_F32)                                                           \
+      hipLaunchKernelGGL((combine512_kernel<float, NS>), grid, dim3(kThreads), 0, s, p); \
+    else                                                                                  \
+      hipLaunchKernelGGL((combine512_kernel<bf16, NS>), grid, dim3(kThreads), 0, s, p);  \
+    return hipGetLastError();                                                             \
+  }
+    SFA_COMBINE512(2)
+    SFA_COMBINE512(4)
+    SFA_COMBINE512(8)
+#undef SFA_COMBINE512
+  }
   if (dtype == SFA_DTYPE_F32)
     hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(kThreads), 0, s, p);
   else
