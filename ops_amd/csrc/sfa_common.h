@@ -113,7 +113,9 @@ __device__ __forceinline__ int staged_id(const Params& p, int b, int id, int bou
 // stores each value to LDS as it arrives compiles to one memory round trip
 // per iteration).  load(): thread tid reads slots tid, tid + THREADS, ...
 // (CAP / THREADS coalesced loads, slots past nslots read nothing); store():
-// writes the staged ids (invalid -> -1, padding -1 up to nstage <= CAP).
+// writes the staged ids (invalid -> -1, padding -1 up to nstage <= CAP) and
+// returns 1 + the last of this thread's slots that holds a valid id (0 if
+// none), from which the caller can drop the trailing all-padding tiles.
 template <int CAP, int THREADS>
 struct IdxStage {
   static constexpr int IPT = CAP / THREADS;
@@ -127,16 +129,40 @@ struct IdxStage {
     }
   }
   template <bool PAGED>
-  __device__ __forceinline__ void store(const Params& p, int b, int bound, int nslots, int nstage, int* s_idx,
-                                        int tid) {
+  __device__ __forceinline__ int store(const Params& p, int b, int bound, int nslots, int nstage, int* s_idx,
+                                       int tid) {
     int st[IPT];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_id<PAGED>(p, b, v[j], bound) : -1;
+    int used = 0;
 #pragma unroll
-    for (int j = 0; j < IPT; ++j)
+    for (int j = 0; j < IPT; ++j) {
       if (tid + j * THREADS < nstage) s_idx[tid + j * THREADS] = st[j];
+      if (st[j] >= 0) used = tid + j * THREADS + 1;
+    }
+    return used;
+  }
+  // store() for contiguous rows, staging each slot's row byte offset
+  // id * row_bytes instead of the id (invalid: oob, which has bit 31 set, so
+  // the sign still tells validity); offsets must stay below 2^31.
+  __device__ __forceinline__ int store_offsets(int bound, int nslots, int nstage, int* s_idx, int tid,
+                                               uint32_t row_bytes, uint32_t oob) {
+    int used = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const bool ok = tid + j * THREADS < nslots && v[j] >= 0 && v[j] < bound;
+      if (tid + j * THREADS < nstage) s_idx[tid + j * THREADS] = ok ? (int)__umul24((uint32_t)v[j], row_bytes) : (int)oob;
+      if (ok) used = tid + j * THREADS + 1;
+    }
+    return used;
   }
 };
+
+__device__ __forceinline__ int wave_max_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, 64));
+  return x;
+}
 
 // Byte offset of pool row r from the pool base (paged mode): page r >> shift
 // at page_bytes, row r & mask at row_bytes (64-bit: pools may exceed 4 GiB).

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   int nslots = p.topk - slot0;
   if (nslots > p.split_len) nslots = p.split_len;
   if (nslots < 0) nslots = 0;
-  const int ntiles = (nslots + 31) / 32;
+  int ntiles = (nslots + 31) / 32;  // (trimmed to the last valid slot once the ids are staged)
 
   // ---- index row (invalid -> -1): its loads and Q's are in flight together --
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
@@ -107,8 +107,10 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
 
-  istage.template store<PAGED>(p, b, bound, nslots, ntiles * 32, s_idx, lane);
+  const int used = wave_max_int(istage.template store<PAGED>(p, b, bound, nslots, ntiles * 32, s_idx, lane));
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
+  // tiles past the last valid slot (trailing padding) contribute nothing
+  ntiles = (used + 31) / 32;
 
   // Loads of tile j (keys 32 j .. 32 j + 31): instruction i of a lane loads
   // the 16 bytes at chunk lt of tile row i + 8 hq, for K into kr[i] and for V

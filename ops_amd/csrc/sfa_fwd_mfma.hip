@@ -99,6 +99,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   __shared__ u32x4 s_k0[C::KBUF];
   __shared__ u32x4 s_k1[C::KBUF];
   __shared__ u32x4 s_q[C::QBUF];
+  __shared__ int s_used[C::kWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -138,10 +139,15 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   int nslots = p.topk - slot0;
   if (nslots > p.split_len) nslots = p.split_len;
   if (nslots < 0) nslots = 0;
-  const int ntiles = (nslots + C::NKT - 1) / C::NKT;
+  // (trimmed below to the tiles up to the last valid slot)
+  int ntiles = (nslots + C::NKT - 1) / C::NKT;
 
   // ---- gather setup (V rows are the K rows: one gather) --------------------
-  typedef typename std::conditional<PAGED, PoolRows, BufRows>::type Src;
+  // (contiguous rows: the index row is staged as row byte offsets, so a
+  // row's gather base costs a select; the first tile's rows come from the
+  // global ids)
+  typedef typename std::conditional<PAGED, PoolRows, BufRowsOff>::type Src;
+  typedef typename std::conditional<PAGED, PoolRows, BufRows>::type Src0;
   Src ksrc;
   if constexpr (PAGED) {
     ksrc.base = reinterpret_cast<const char*>(p.k) + 2 * g * p.k_sh;
@@ -157,6 +163,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // The next tile's gather is issued from inside the current tile's S^T MFMA
   // stream instead of in one burst.
   typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src> RG;
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src0> RG0;
+  const Src0& ksrc0 = ksrc;
   static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
   // ---- first tile's gather, then stage indices (invalid -> -1) -----------
   // Each wave reads the ids of its 8 rows of tile 0 straight from global
@@ -170,7 +178,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   IdxStage<kIdxCap, C::kThreads> istage;
   istage.load(irow, nslots, tid);
   {
-    RG rg0;
+    RG0 rg0;
     // (unconditional loads, all in flight together: slots past the split
     // re-read its last slot, whose id is then discarded)
     int raw[RG::RPW];
@@ -178,9 +186,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     for (int r = 0; r < RG::RPW; ++r) raw[r] = irow[min(wave * RG::RPW + r, max(nslots - 1, 0))];
 #pragma unroll
     for (int r = 0; r < RG::RPW; ++r)
-      rg0.set_row(r, (wave * RG::RPW + r < nslots) ? staged_id<PAGED>(p, b, raw[r], bound) : -1, true, ksrc);
+      rg0.set_row(r, (wave * RG::RPW + r < nslots) ? staged_id<PAGED>(p, b, raw[r], bound) : -1, true, ksrc0);
 #pragma unroll
-    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, ksrc, s_k0, wave, lane);
+    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, ksrc0, s_k0, wave, lane);
   }
 
   // ---- Q^T B operands in registers ------------------------------------
@@ -235,39 +243,88 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
   for (int i = 0; i < C::OT; ++i) oacc[i] = acc_t{};
   float m_used = kNegInf;  // running max (base 2) the exponentials are taken against
+  float m_off = 0.f;       // -m_used, or 0 while m_used is -inf (the exponent offset)
   float l_part = 0.f;      // this lane's share of the row sum
 
   const int hq = lane / T;  // lane group: which k-slice of the MFMA operands
   const int lt = lane % T;
+
+  // vmcnt(0) before the barriers that publish a gathered tile, where the
+  // compiler does not see the DMA (PoolRows)
+  auto dma_done = [&]() {
+    if constexpr (Src::kUntrackedDma) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  };
 
   // compute(tile) also issues the gather of the next tile into ndst (rg
   // holds that tile's row offsets), and, inside its O^T MFMA stream (all of
   // that gather has been issued by then), reads the row ids of tile + 2 into
   // rg and the validity mask of tile + 1 into vmask_io (on entry: this
   // tile's), so no LDS round trip sits between the end of one tile's MFMAs
-  // and the next tile's.
-  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, RG& rg, u32x4* ndst, uint32_t& vmask_io) {
+  // and the next tile's.  Its first PDK K operands are in kbuf on entry; after
+  // O^T MFMA kBarAt it runs the barrier that publishes tile + 1 (and ends
+  // every read of this tile's buffer), then reads the first K operands of
+  // tile + 1 into kbuf while its last MFMAs execute.
+  constexpr int PDK = 4;
+  // S^T A operands: step s of lane (key lt, k-slice hq) is chunk 2s + hq = 8 (s >> 2) + v
+  // with v = 2 (s & 3) + hq, at slot 8 (s >> 2) + (v ^ swz(row)): four bases
+  uint32_t kb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    kb[j] = (uint32_t)((ks * 32 + lt) * C::PK + ((2 * j + hq) ^ tile_swz(ks * 32 + lt))) * 16u;
+  auto load_k_at = [&](const u32x4* buf, int s) { return lds_read_b128(buf, kb[s & 3] + (uint32_t)(s >> 2) * 128u); };
+  auto compute = [&](int tile, const u32x4* kt, const u32x4* vt, RG& rg, u32x4* ndst, uint32_t& vmask_io,
+                     bf16x8 (&kbuf)[PDK]) {
     const uint32_t vmask = vmask_io;  // validity of this wave's 32 keys
 
     // S^T = K Q^T
     acc_t sacc[C::MT];
     const uint32_t q_off = (uint32_t)(hl * C::QLP + hq) * 16u;
     // one 32-key M-tile: operands of step s + PDK are loaded before MFMA s
-    // (swizzled tile: step s reads chunk 2s + hq = 8 (s >> 2) + v with
-    // v = 2 (s & 3) + hq at slot 8 (s >> 2) + (v ^ swz(row)): four bases)
-    constexpr int PDK = 4;
-    uint32_t kb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      kb[j] = (uint32_t)((ks * 32 + lt) * C::PK + ((2 * j + hq) ^ tile_swz(ks * 32 + lt))) * 16u;
-    auto load_k = [&](int s) { return lds_read_b128(kt, kb[s & 3] + (uint32_t)(s >> 2) * 128u); };
+    auto load_k = [&](int s) { return load_k_at(kt, s); };
     auto load_q = [&](int s) { return lds_read_b128(s_q, q_off + (uint32_t)((s - C::QREG) * C::LG) * 16u); };
-    bf16x8 kbuf[PDK], qbuf[PDK];
+    bf16x8 qbuf[PDK];
 #pragma unroll
-    for (int i = 0; i < PDK; ++i) {
-      kbuf[i] = load_k(i);
+    for (int i = 0; i < PDK; ++i)
       if (i >= C::QREG) qbuf[i] = load_q(i);
+    // V^T operand reads of the O^T stream (below): the first PD are issued
+    // during the last S^T MFMAs, so they land while the softmax runs
+    // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
+    // of operand i + PD are issued before MFMA i (software pipeline).
+    constexpr int VP = C::PK;  // V rows are the K rows
+    const int gi = lane & 15;         // lane within its 16-lane transpose group
+    const int rr = gi >> 2;           // row within a run of 4 keys this lane loads
+    const int cc = gi & 3;            // 4-dim column piece this lane loads
+    const int mgrp = (lt >> 4) << 4;  // first MFMA row (dim) of the 16-lane group
+    // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
+    const int run0 = 4 * hq;
+    const int run1 = 8 + 4 * hq;
+    // Operand (kk, ot) of a lane: its dims ot*32 + mgrp + 4cc .. +3 are in
+    // chunk 4 ot + cl, cl = mgrp / 8 + cc / 2, i.e. chunk 8 (ot >> 1) + v
+    // with v = 4 (ot & 1) + cl, at slot 8 (ot >> 1) + (v ^ swz(row)) of rows
+    // 16 kk + run + rr; rows r and r + 16 share swz, so each run needs one
+    // base per parity of ot.
+    uint32_t vb[2][2];
+    {
+      const int rows[2] = {ks * 32 + run0 + rr, ks * 32 + run1 + rr};
+      const int cl = mgrp / 8 + cc / 2;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int par = 0; par < 2; ++par)
+          vb[h][par] = (uint32_t)(rows[h] * VP + ((4 * par + cl) ^ tile_swz(rows[h]))) * 16u + (uint32_t)(cc & 1) * 8u;
     }
+    auto load_a = [&](int i) -> bf16x8 {
+      const int kk = i / C::OT, ot = i % C::OT;
+      const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot >> 1) * 128u;
+      const uint32_t o0 = vb[0][ot & 1] + off;
+      const uint32_t o1 = vb[1][ot & 1] + off;
+      const bf16x4 lo = lds_read_tr16(vt, o0);
+      const bf16x4 hi = lds_read_tr16(vt, o1);
+      return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    constexpr int NI = 2 * C::OT;  // O^T MFMAs (two 16-key contraction steps per 32 keys)
+    constexpr int PD = 3;          // V^T operand reads in flight ahead of the O^T MFMAs
+    bf16x8 abuf[PD];
     bf16x8 pa = {}, pq = {};
 #pragma unroll
     for (int s = 0; s < C::QSTEPS; ++s) {
@@ -284,6 +341,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       pa = a;
       pq = bq;
       dma_at(s, rg, ndst);
+      if (s >= C::QSTEPS - PD) abuf[s - (C::QSTEPS - PD)] = load_a(s - (C::QSTEPS - PD));
     }
     M::drain_v(sacc[0], pa, pq);
 
@@ -321,7 +379,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     // run (late_exps, after the max test, so never recomputed).
     constexpr int NE0 = NV < 8 ? NV : 8;
     float ex[NV];
-    float moff = (m_used == kNegInf) ? 0.f : -m_used;
+    float moff = m_off;
     {
 #pragma unroll
       for (int i = 0; i < NE0; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
@@ -331,19 +389,21 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < NE0; ++i) asm volatile("" : "+v"(ex[i]));
     }
-    float tmax = sv[0];
-#pragma unroll
-    for (int i = 1; i < NV; ++i) tmax = fmaxf(tmax, sv[i]);
-    tmax = xor32_max(tmax);
+    static_assert(NV == 16, "the max tree below covers 16 values");
+    const float t0 = max3_raw(sv[0], sv[1], sv[2]), t1 = max3_raw(sv[3], sv[4], sv[5]),
+                t2 = max3_raw(sv[6], sv[7], sv[8]), t3 = max3_raw(sv[9], sv[10], sv[11]),
+                t4 = max3_raw(sv[12], sv[13], sv[14]);
+    float tmax = max_raw(max3_raw(t0, t1, t2), max3_raw(t3, t4, sv[15]));  // depth 3, not a 15-long chain
+    tmax = xor32_max_raw(tmax);
     tmax *= p.scale_log2;
-    const float m_new = fmaxf(m_used, tmax);
+    const float m_new = max_raw(m_used, tmax);
     if (__any(m_new > m_used + kRescaleSlack)) {
       const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_used - m_new);
       l_part *= alpha;
 #pragma unroll
       for (int i = 0; i < C::OT; ++i) M::scale_agpr(oacc[i], alpha);
       m_used = m_new;
-      moff = (m_used == kNegInf) ? 0.f : -m_used;
+      moff = m_off = (m_used == kNegInf) ? 0.f : -m_used;
 #pragma unroll
       for (int i = 0; i < NE0; ++i) ex[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.scale_log2, moff));
     }
@@ -375,45 +435,13 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
         for (int i = 0; i + w < n; i += 2 * w) ex[lo + i] += ex[lo + i + w];
     };
 
-    // O^T += V^T P^T.  Operand i = kk * OT + ot; the two transposed LDS reads
-    // of operand i + PD are issued before MFMA i (software pipeline).
-    constexpr int VP = C::PK;  // V rows are the K rows
-    const int gi = lane & 15;         // lane within its 16-lane transpose group
-    const int rr = gi >> 2;           // row within a run of 4 keys this lane loads
-    const int cc = gi & 3;            // 4-dim column piece this lane loads
-    const int mgrp = (lt >> 4) << 4;  // first MFMA row (dim) of the 16-lane group
-    // the two runs of 4 consecutive keys feeding k = 0..3 and k = 4..7
-    const int run0 = 4 * hq;
-    const int run1 = 8 + 4 * hq;
-    // Operand (kk, ot) of a lane: its dims ot*32 + mgrp + 4cc .. +3 are in
-    // chunk 4 ot + cl, cl = mgrp / 8 + cc / 2, i.e. chunk 8 (ot >> 1) + v
-    // with v = 4 (ot & 1) + cl, at slot 8 (ot >> 1) + (v ^ swz(row)) of rows
-    // 16 kk + run + rr; rows r and r + 16 share swz, so each run needs one
-    // base per parity of ot.
-    uint32_t vb[2][2];
-    {
-      const int rows[2] = {ks * 32 + run0 + rr, ks * 32 + run1 + rr};
-      const int cl = mgrp / 8 + cc / 2;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int par = 0; par < 2; ++par)
-          vb[h][par] = (uint32_t)(rows[h] * VP + ((4 * par + cl) ^ tile_swz(rows[h]))) * 16u + (uint32_t)(cc & 1) * 8u;
-    }
-    auto load_a = [&](int i) -> bf16x8 {
-      const int kk = i / C::OT, ot = i % C::OT;
-      const uint32_t off = (uint32_t)(16 * kk * VP) * 16u + (uint32_t)(ot >> 1) * 128u;
-      const uint32_t o0 = vb[0][ot & 1] + off;
-      const uint32_t o1 = vb[1][ot & 1] + off;
-      const bf16x4 lo = lds_read_tr16(vt, o0);
-      const bf16x4 hi = lds_read_tr16(vt, o1);
-      return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    };
-    constexpr int NI = KSTEPS * C::OT;
+    static_assert(NI == KSTEPS * C::OT, "O^T MFMA count");
     // O^T MFMA after which the ids of tile + 2 are read, and the lag (in
     // MFMAs) after which they are used
     constexpr int kIdsAt = NLATE + 3, kIdsLag = 4;
-    static_assert(kIdsAt + kIdsLag + RG::RPW < NI, "id prefetch fits the O^T stream");
+    // the barrier after the last V^T read has been issued
+    constexpr int kBarAt = NI - PD - 1;
+    static_assert(kIdsAt + kIdsLag + RG::RPW < kBarAt && NLATE + 2 < kBarAt, "id prefetch and softmax pieces precede the barrier");
     static_assert(kDmaFirst + kDmaStride * (RG::NI - 1) < C::QSTEPS + kIdsAt,
                   "the gather of tile + 1 is issued before rg is overwritten");
     int ids_raw[RG::RPW];
@@ -421,10 +449,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
     int vm_raw = 0;
     static_assert(NI >= NLATE + 3 && NLATE <= C::OT && NE0 % 2 == 0 && NLATE % 2 == 0,
                   "late softmax pieces must finish before the MFMAs that use them");
-    constexpr int PD = NI < 3 ? NI : 3;
-    bf16x8 abuf[PD];
-#pragma unroll
-    for (int i = 0; i < PD; ++i) abuf[i] = load_a(i);
     bf16x8 prev_a = {}, prev_b = {};
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -460,35 +484,47 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       if (i == NLATE) sum_range(0, NE0);
       if (NLATE > 0 && i == NLATE + 1) sum_range(NE0, NLATE);
       if (i == NLATE + 2) l_part += (NLATE > 0) ? ex[0] + ex[NE0] : ex[0];
+      if (i == kBarAt) {
+        dma_done();
+        __syncthreads();  // tile + 1 in place in ndst; every read of this tile's buffer done
+#pragma unroll
+        for (int j = 0; j < PDK; ++j) kbuf[j] = load_k_at(ndst, j);
+      }
     }
     M::tail(prev_a, prev_b);
   };
 
-  // vmcnt(0) before the barriers that publish a gathered tile, where the
-  // compiler does not see the DMA (PoolRows)
-  auto dma_done = [&]() {
-    if constexpr (Src::kUntrackedDma) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  };
   load_q();
-  istage.template store<PAGED>(p, b, bound, nslots, ntiles * C::NKT, s_idx, tid);
+  int used;
+  if constexpr (PAGED)
+    used = istage.template store<true>(p, b, bound, nslots, ntiles * C::NKT, s_idx, tid);
+  else
+    used = istage.store_offsets(bound, nslots, ntiles * C::NKT, s_idx, tid, ksrc.row_bytes, kOOBRow);
+  used = wave_max_int(used);
+  if (lane == 0) s_used[wave] = used;
   store_q();
   dma_done();
   __syncthreads();  // indices staged, first tile and the LDS part of Q in place
+  // Tiles past the last valid slot (trailing padding, e.g. a causal row
+  // shorter than top-k) contribute nothing and are skipped.
+  {
+    int u = s_used[0];
+#pragma unroll
+    for (int w = 1; w < C::kWaves; ++w) u = max(u, s_used[w]);
+    ntiles = (u + C::NKT - 1) / C::NKT;
+  }
 
   // row offsets of tile 1 (gathered during tile 0) and the validity mask of
   // tile 0; compute() fetches those of the following tiles itself
   RG rg;
   rg.load_ids(s_idx + (ntiles > 1 ? C::NKT : 0), ntiles > 1, wave, ksrc);
   uint32_t vmask = (uint32_t)__ballot(s_idx[ks * 32 + (lane & 31)] >= 0);
+  bf16x8 kbuf[PDK];
+#pragma unroll
+  for (int j = 0; j < PDK; ++j) kbuf[j] = load_k_at(s_k0, j);
   for (int j = 0; j < ntiles; j += 2) {
-    compute(j, s_k0, s_k0, rg, s_k1, vmask);
-    dma_done();
-    __syncthreads();
-    if (j + 1 < ntiles) {
-      compute(j + 1, s_k1, s_k1, rg, s_k0, vmask);
-      dma_done();
-      __syncthreads();
-    }
+    compute(j, s_k0, s_k0, rg, s_k1, vmask, kbuf);
+    if (j + 1 < ntiles) compute(j + 1, s_k1, s_k1, rg, s_k0, vmask, kbuf);
   }
 
 #pragma unroll

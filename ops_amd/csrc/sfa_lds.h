@@ -18,6 +18,26 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// max of three floats as one v_max3_f32 (fmaxf on values the compiler cannot
+// prove canonical, such as MFMA results from inline asm, adds a quieting
+// v_max x, x per operand; NaN-free inputs here)
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// xor32_max with raw maxes (see max3_raw)
+__device__ __forceinline__ float xor32_max_raw(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // LDS reads go through pointers derived from the __shared__ arrays themselves,
 // so the compiler keeps per-array alias information and does not make reads of
 // one tile buffer wait for the DMA still filling another.
@@ -125,6 +145,12 @@ struct BufRows {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, off, 0, 0, 0);
   }
   static constexpr bool kUntrackedDma = false;  // the compiler tracks the DMA
+};
+// BufRows for staged entries that already are row byte offsets
+// (IdxStage::store_offsets: kOOBRow for an invalid slot), so a row's base
+// costs one select instead of a validity test and a multiply.
+struct BufRowsOff : BufRows {
+  __device__ __forceinline__ base_t row_base(int off, bool valid) const { return valid ? (uint32_t)off : kOOBRow; }
 };
 // Rows of a paged pool (ids are pool rows): 64-bit addresses, since a pool
 // may exceed the 4 GiB a buffer offset reaches; padding rows read kZeroRow.
