@@ -127,6 +127,8 @@ struct FwdPlan {
   int split_len;
   size_t part_o_bytes;
   size_t part_lse_bytes;
+  size_t sched_bytes;  // claim counters of the persistent forward (0 when not persistent)
+  size_t workspace() const { return part_o_bytes + part_lse_bytes + sched_bytes; }
 };
 
 constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
@@ -169,6 +171,11 @@ FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
     pl.part_o_bytes = align_up((size_t)splits * rows * a->Dv * sizeof(__bf16), 256);
     pl.part_lse_bytes = align_up((size_t)splits * rows * sizeof(float), 256);
   }
+  if (pl.mfma) {
+    p.num_splits = pl.num_splits;
+    p.split_len = pl.split_len;
+    if (sfa::fwd_mfma_persistent(p)) pl.sched_bytes = 256;
+  }
   return pl;
 }
 
@@ -189,13 +196,13 @@ int run_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, void* workspace, size
   if (pl.mfma) {
     p.num_splits = pl.num_splits;
     p.split_len = pl.split_len;
+    if (pl.workspace() > 0 && (workspace == nullptr || workspace_bytes < pl.workspace()))
+      return fail(SFA_E_WORKSPACE, "sfa_fwd needs %zu workspace bytes (got %zu)", pl.workspace(), workspace_bytes);
     if (pl.num_splits > 1) {
-      if (workspace == nullptr || workspace_bytes < pl.part_o_bytes + pl.part_lse_bytes)
-        return fail(SFA_E_WORKSPACE, "sfa_fwd needs %zu workspace bytes (got %zu)", pl.part_o_bytes + pl.part_lse_bytes,
-                    workspace_bytes);
       p.part_o = (__bf16*)workspace;
       p.part_lse = (float*)((char*)workspace + pl.part_o_bytes);
     }
+    if (pl.sched_bytes > 0) p.sched = (int*)((char*)workspace + pl.part_o_bytes + pl.part_lse_bytes);
     e = sfa::launch_fwd_mfma(p, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_fwd (mfma)");
     if (pl.num_splits > 1) {
@@ -222,7 +229,7 @@ const char* sfa_last_error(void) { return g_err; }
 size_t sfa_fwd_workspace_size(const sfa_fwd_args* a) {
   if (check_fwd(a) != SFA_OK) return 0;
   const FwdPlan pl = plan_fwd(a, nullptr);
-  return pl.part_o_bytes + pl.part_lse_bytes;
+  return pl.workspace();
 }
 
 int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
@@ -285,7 +292,7 @@ int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream) {
   const int rc = check_fwd(a);
   if (rc != SFA_OK) return rc;
   const FwdPlan pl = plan_fwd(a, nullptr);
-  const size_t need = pl.part_o_bytes + pl.part_lse_bytes;
+  const size_t need = pl.workspace();
   if (need > kNoallocBytes)
     return fail(SFA_E_WORKSPACE,
                 "sfa_fwd_noalloc: the split-k partials need %zu bytes, above its static scratch of %zu bytes "
@@ -302,7 +309,7 @@ int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream) {
 size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages) {
   if (check_fwd(a) != SFA_OK || check_pages(a, pages) != SFA_OK) return 0;
   const FwdPlan pl = plan_fwd(a, pages);
-  return pl.part_o_bytes + pl.part_lse_bytes;
+  return pl.workspace();
 }
 
 int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace, size_t workspace_bytes,

@@ -46,6 +46,7 @@ struct Params {
   int split_len;      // slots per split (multiple of the key tile)
   __bf16* part_o;     // [num_splits][B*Sq*Hq][Dv] bf16, normalised by the split's own sum
   float* part_lse;    // [num_splits][B*Sq*Hq], base-2 log-sum-exp of the split (-inf if empty)
+  int* sched;         // persistent forward: 8 claim counters (one per XCD), zeroed before the launch
   // backward
   const void* dout;
   int64_t do_sb, do_ss, do_sh;
@@ -241,6 +242,7 @@ hipError_t launch_fwd_mfma(const Params& p, hipStream_t s);  // paged when p.blo
 bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
 int fwd_mfma_idx_cap(const Params& p);  // index slots one work item (split) stages
+bool fwd_mfma_persistent(const Params& p);  // needs Params::sched (8 ints of workspace)
 int fwd_d128_idx_cap();
 // d = 128, G <= 16: register-direct gather (sfa_fwd_d128.hip)
 bool fwd_d128_supported(const Params& p);

@@ -89,8 +89,28 @@ struct FwdCfg {
 // LDS reads through pointers derived from the __shared__ arrays themselves, so
 // the compiler keeps per-array alias information and does not make the reads
 // of one tile buffer wait for the DMA still filling the other.
-template <class C, bool PAGED>
-__global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
+// Persistent scheduling (PERSIST): one workgroup per CU claims work items
+// from 8 counters, one per XCD.  Counter x hands out the virtual workgroup
+// ids x, x + 8, x + 16, ... (the ids the hardware would have dispatched to XCD
+// x, so the items keep the L2 locality of the mapping below); a workgroup
+// takes from its own XCD's counter and, once that is exhausted, from the
+// others (XCDs run at different clocks: without this the fastest idle while
+// the slowest finish).  nvb: number of virtual ids.  Called by one thread.
+__device__ __forceinline__ int claim_item(int* ctr, int x, int nvb) {
+  for (int k = 0; k < 8; ++k) {
+    const int y = (x + k) & 7;
+    const int c = atomicAdd(&ctr[y], 1);
+    if (c < (nvb - y + 7) / 8) return y + 8 * c;
+  }
+  return -1;
+}
+
+__global__ void sched_reset_kernel(int* ctr) {
+  if (threadIdx.x < 8) ctr[threadIdx.x] = 0;
+}
+
+template <class C, bool PAGED, bool PERSIST>
+__global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) {
   constexpr int T = C::T;
   using M = Mfma<T>;
   typedef typename M::acc_t acc_t;
@@ -100,12 +120,39 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   __shared__ u32x4 s_k1[C::KBUF];
   __shared__ u32x4 s_q[C::QBUF];
   __shared__ int s_used[C::kWaves];
+  __shared__ int s_claim;
 
-  const int tid = threadIdx.x;
+  const int nvb = (int)((int64_t)p_arg.B * p_arg.Sq * p_arg.Hkv * p_arg.num_splits);  // virtual workgroup ids
+  int vb = blockIdx.x;
+  if constexpr (PERSIST) {
+    if (threadIdx.x == 0) s_claim = claim_item(p_arg.sched, blockIdx.x & 7, nvb);
+    __syncthreads();
+    vb = s_claim;
+  }
+  int next_vb = -1;  // (thread 0) the item claimed for after this one
+  while (vb >= 0) {
+  // The parameters are read through a pointer the compiler cannot see
+  // through, once per item: otherwise it hoists every parameter load out of
+  // the item loop and keeps the values live (and spilled) across it.
+#if __HIP_DEVICE_COMPILE__
+  typedef __attribute__((address_space(4))) const Params* kparams_t;
+  kparams_t pp = (kparams_t)__builtin_amdgcn_kernarg_segment_ptr();
+  if constexpr (PERSIST) asm volatile("" : "+s"(pp));
+  const Params& p = *pp;
+#else
+  const Params& p = p_arg;  // (host pass: the body is only type-checked)
+#endif
+  // (the thread index likewise, so that lane-dependent constants are formed
+  // per item rather than held, and spilled, across the item loop)
+  int tid = threadIdx.x;
+  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int slice = wave % C::NSLICE;
   const int ks = wave / C::NSLICE;
+  if constexpr (PERSIST) {
+    if (tid == 0) next_vb = claim_item(p.sched, blockIdx.x & 7, nvb);  // in flight during this item
+  }
 
   // ---- work item -------------------------------------------------------
   // Work item = (b, t, g) x split.  Workgroups are dispatched to the 8 XCDs
@@ -116,7 +163,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
   // dealt round-robin over the XCDs: the workgroups running together on one
   // XCD then share the keys their queries have in common (e.g. a recency
   // window) in its L2.
-  int wi = blockIdx.x;
+  int wi = vb;
   int split;
   const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
   if (p.num_splits > 1 && nitems % 8 == 0) {
@@ -600,6 +647,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p) {
       *reinterpret_cast<bf16x8*>(wbase + (int64_t)r * orstride + 8 * lane) = v;
     }
   }
+  if constexpr (!PERSIST) break;
+  if (tid == 0) s_claim = next_vb;
+  __syncthreads();  // every wave is done with this item's LDS; the next claim is visible
+  vb = s_claim;
+  }  // items
 }
 
 // The one variant: DeepSeek MLA, G = 128 heads (65..128 accepted), d_qk 576 /
@@ -609,10 +661,24 @@ using CfgMla = FwdCfg<32, 576, 512, 4, 1, true, MLA_QREG, true>;
 template <class C>
 hipError_t launch(const Params& p, hipStream_t s) {
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
+  if (p.sched) {
+    // persistent: one workgroup per CU (the LDS use allows one)
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    const unsigned grid = (unsigned)(n < cus ? n : cus);
+    hipLaunchKernelGGL(sched_reset_kernel, dim3(1), dim3(64), 0, s, p.sched);
+    if (p.block_table)
+      hipLaunchKernelGGL((fwd_mfma_kernel<C, true, true>), dim3(grid), dim3(C::kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((fwd_mfma_kernel<C, false, true>), dim3(grid), dim3(C::kThreads), 0, s, p);
+    return hipGetLastError();
+  }
   if (p.block_table)
-    hipLaunchKernelGGL((fwd_mfma_kernel<C, true>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<C, true, false>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((fwd_mfma_kernel<C, false>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
+    hipLaunchKernelGGL((fwd_mfma_kernel<C, false, false>), dim3((unsigned)n), dim3(C::kThreads), 0, s, p);
   return hipGetLastError();
 }
 
@@ -643,6 +709,13 @@ int fwd_mfma_tile_keys(const Params& p) {
 }
 
 int fwd_mfma_idx_cap(const Params& p) { return mla_supported(p) ? kIdxCap : fwd_d128_idx_cap(); }
+
+// Whether the forward of p runs persistent (its Params then need sched, 8
+// zeroed ints): the MLA kernel without split-k over enough items to keep
+// every CU busy for many rounds.
+bool fwd_mfma_persistent(const Params& p) {
+  return mla_supported(p) && p.num_splits == 1 && (int64_t)p.B * p.Sq * p.Hkv >= 4096;
+}
 
 bool fwd_mfma_supported(const Params& p) { return mla_supported(p) || fwd_d128_supported(p); }
 

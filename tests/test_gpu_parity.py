@@ -309,6 +309,28 @@ def test_mla_prefill_full_sampled():
     _check_fwd(out[:, rows], lse[:, rows], o_ref, l_ref)
 
 
+def test_mla_prefill_persistent_schedule():
+    """S = 4100 queries (>= 4096 work items: one workgroup per CU claims them
+    from per-XCD counters; 4100 is not a multiple of 8 or 256, so the XCD
+    queues differ in length and the plain item mapping is used), with fully
+    masked rows and rows whose valid slots end early: sampled rows match the
+    oracle, and a second run is bitwise identical (the claim order varies, a
+    row's arithmetic does not)."""
+    _say("mla_prefill bf16 persistent S=4100 K=256 Hq=128 (sampled rows vs oracle, run-to-run bitwise)")
+    w = make_workload("mla_prefill", device=DEV, S=4100, K=256)
+    idx = w.idx.clone()
+    idx[:, 4000] = -1                 # no valid slot
+    idx[:, 4001, :, 40:] = -1         # valid slots end in the second tile
+    out1, lse1 = ops_amd.sfa_forward(w.q, w.k, w.v, idx, w.scale)
+    out2, lse2 = ops_amd.sfa_forward(w.q, w.k, w.v, idx, w.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2) and torch.equal(lse1, lse2)
+    assert torch.all(out1[:, 4000] == 0) and torch.all(lse1[:, 4000] == float("-inf"))
+    rows = torch.tensor([0, 1, 255, 256, 1000, 2047, 3333, 4001, 4095, 4096, 4099])
+    o_ref, l_ref = ref_forward(w.q[:, rows].cpu(), w.k.cpu(), w.v.cpu(), idx[:, rows].cpu(), w.scale)
+    _check_fwd(out1[:, rows], lse1[:, rows], o_ref, l_ref)
+
+
 def _decode_compact(w):
     """Gather the referenced rows on the GPU so the oracle sees a small KV."""
     B, K = w.idx.shape[0], w.idx.shape[3]
