@@ -129,6 +129,13 @@ struct IdxStage {
       v[j] = i < nslots ? irow[i] : -1;
     }
   }
+  // load() through a buffer resource over the row's nslots ids: slots past it
+  // read 0 instead of being selected to -1 (store() and store_offsets() test
+  // the slot index), so no instruction waits for the loads here
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t rs, int tid) {
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) v[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (uint32_t)(tid + j * THREADS), 0, 0);
+  }
   template <bool PAGED>
   __device__ __forceinline__ int store(const Params& p, int b, int bound, int nslots, int nstage, int* s_idx,
                                        int tid) {

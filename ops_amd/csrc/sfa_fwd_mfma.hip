@@ -92,15 +92,27 @@ struct FwdCfg {
 // Persistent scheduling (PERSIST): one workgroup per CU claims work items
 // from 8 counters, one per XCD.  Counter x hands out the virtual workgroup
 // ids x, x + 8, x + 16, ... (the ids the hardware would have dispatched to XCD
-// x, so the items keep the L2 locality of the mapping below); a workgroup
+// x, so the items keep the L2 locality of item_of's mapping); a workgroup
 // takes from its own XCD's counter and, once that is exhausted, from the
 // others (XCDs run at different clocks: without this the fastest idle while
 // the slowest finish).  nvb: number of virtual ids.  Called by one thread.
-__device__ __forceinline__ int claim_item(int* ctr, int x, int nvb) {
-  for (int k = 0; k < 8; ++k) {
+// claim_start only issues the own-counter atomic; claim_finish reads its
+// result later (so the atomic's latency overlaps other work) and steals when
+// the own counter is exhausted.
+__device__ __forceinline__ int claim_start(int* ctr, int x) {
+  // (an offset the compiler cannot prove uniform: for a uniform address it
+  // rewrites the atomic into a wave reduction that needs the returned value
+  // at once, i.e. waits for every load in flight right here)
+  int o = 0;
+  asm volatile("" : "+v"(o));
+  return atomicAdd(ctr + x + o, 1);
+}
+__device__ __forceinline__ int claim_finish(int* ctr, int x, int nvb, int c) {
+  if (c < (nvb - x + 7) / 8) return x + 8 * c;
+  for (int k = 1; k < 8; ++k) {
     const int y = (x + k) & 7;
-    const int c = atomicAdd(&ctr[y], 1);
-    if (c < (nvb - y + 7) / 8) return y + 8 * c;
+    const int cy = atomicAdd(&ctr[y], 1);
+    if (cy < (nvb - y + 7) / 8) return y + 8 * cy;
   }
   return -1;
 }
@@ -109,27 +121,228 @@ __global__ void sched_reset_kernel(int* ctr) {
   if (threadIdx.x < 8) ctr[threadIdx.x] = 0;
 }
 
+// A work item: (batch, query, kv head) and its split of the top-k slots.
+struct ItemPos {
+  int b, t, g, split, nslots;
+};
+
+// Virtual workgroup id -> work item.  Workgroups are dispatched to the 8 XCDs
+// round-robin (id % 8); with splits, the splits of one item are placed on
+// the same XCD (so its L2 serves the item's Q rows to all of them) whenever
+// the item count allows a bijective mapping.  Without splits, XCD x gets
+// runs of 32 consecutive items (queries), runs dealt round-robin over the
+// XCDs: the workgroups running together on one XCD then share the keys their
+// queries have in common (e.g. a recency window) in its L2.
+__device__ __forceinline__ ItemPos item_of(const Params& p, int vb) {
+  ItemPos it;
+  int wi = vb;
+  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
+  if (p.num_splits > 1 && nitems % 8 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    it.split = r % p.num_splits;
+    wi = (r / p.num_splits) * 8 + x;
+  } else if (p.num_splits == 1 && nitems % 256 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    it.split = 0;
+    wi = ((r / 32) * 8 + x) * 32 + r % 32;
+  } else {
+    it.split = wi % p.num_splits;
+    wi /= p.num_splits;
+  }
+  it.g = wi % p.Hkv;
+  wi /= p.Hkv;
+  it.t = wi % p.Sq;
+  it.b = wi / p.Sq;
+  int nslots = p.topk - it.split * p.split_len;
+  if (nslots > p.split_len) nslots = p.split_len;
+  if (nslots < 0) nslots = 0;
+  it.nslots = nslots;
+  return it;
+}
+
+// LDS-only workgroup barrier: waits for this wave's LDS operations (and for
+// all but its last VM vector-memory operations, VM an immediate), not for the
+// global stores a __syncthreads fence would also wait for.
+#define SFA_LDS_BARRIER(VM) asm volatile("s_waitcnt vmcnt(" #VM ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+// LDS reads go through pointers derived from the __shared__ arrays themselves,
+// so the compiler keeps per-array alias information and does not make the reads
+// of one tile buffer wait for the DMA still filling the other.
+//
+// Per work item: a prologue (the index row, tile 0's gather, Q), the tile
+// loop, the output.  The persistent kernel (PERSIST) overlaps the next
+// item's prologue with this item's output: its loads are issued right after
+// the tile loop, its tile 0 is gathered between the two rounds of the output
+// staging (which then uses the Q area only), and its ids and Q are staged
+// behind one barrier after the output.
 template <class C, bool PAGED, bool PERSIST>
 __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) {
   constexpr int T = C::T;
   using M = Mfma<T>;
   typedef typename M::acc_t acc_t;
+  // (contiguous rows: the index row is staged as row byte offsets, so a
+  // row's gather base costs a select; tile 0's rows come from the global ids)
+  // (the prologue gathers -- tile 0 and Q -- are untracked, so the output
+  // staging's LDS reads that overlap them in the persistent kernel do not
+  // wait for them; item_stage waits for them before its barrier)
+  typedef typename std::conditional<PAGED, PoolRows, BufRowsOff>::type Src;
+  typedef typename std::conditional<PAGED, PoolRows, BufRowsUT>::type Src0;
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src> RG;
+  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src0> RG0;
+  static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
 
   __shared__ int s_idx[kIdxCap];
   __shared__ u32x4 s_k0[C::KBUF];
   __shared__ u32x4 s_k1[C::KBUF];
   __shared__ u32x4 s_q[C::QBUF];
   __shared__ int s_used[C::kWaves];
-  __shared__ int s_claim;
+  // claimed virtual ids, by item parity: item i's successor is published in
+  // slot (i + 1) & 1 before item i's staging barrier and read after item i's
+  // tile loop; the slot is rewritten two items later, behind barriers
+  __shared__ int s_claim[2];
 
   const int nvb = (int)((int64_t)p_arg.B * p_arg.Sq * p_arg.Hkv * p_arg.num_splits);  // virtual workgroup ids
+  constexpr bool kUntracked = Src::kUntrackedDma;
+
+  // ---- prologue pieces ------------------------------------------------
+  // Loop-carried: the item and its Q^T B operands in VGPRs (QREG steps; the
+  // rest are gathered into s_q).
+  ItemPos it{};
+  bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
+  IdxStage<kIdxCap, C::kThreads> istage;
+  int raw[RG::RPW];
+  int claim_c = 0;  // (thread 0) the pending claim's raw count
+  // the gather source of an item: the (batch, kv head) slice's rows
+  auto make_src = [&](const Params& p, const ItemPos& q) {
+    Src s;
+    if constexpr (PAGED) {
+      s.base = reinterpret_cast<const char*>(p.k) + 2 * q.g * p.k_sh;
+      s.page_bytes = (uint64_t)(2 * p.k_sb);
+      s.row_bytes = (uint32_t)(2 * p.k_ss);
+      s.shift = p.page_shift;
+    } else {
+      const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (q.b * p.k_sb + q.g * p.k_sh);
+      s.rs = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
+      s.row_bytes = (uint32_t)(2 * p.k_ss);
+    }
+    return s;
+  };
+  // (1) the item's loads, all in flight together: the claim of the item
+  // after it, its index row (coalesced), the ids of the wave's 8 rows of
+  // tile 0 (uniform addresses; slots past the split re-read its last slot,
+  // whose id is then discarded), the register steps of Q.  Loads complete in
+  // order, so each later wait covers only what was issued before it.
+  // (Buffer loads whose out-of-range lanes read zeros: a select on loaded
+  // data would make the wave wait for each load right here.)
+  auto item_loads = [&](const Params& p, const ItemPos& q, int tid, int wave, int lane) {
+    if constexpr (PERSIST) {
+      if (tid == 0) claim_c = claim_start(p.sched, blockIdx.x & 7);
+    }
+    const int32_t* irow = p.idx + q.b * p.i_sb + q.t * p.i_ss + q.g * p.i_sh + q.split * p.split_len;
+    istage.load_buf(make_rsrc(irow, 4u * (uint32_t)q.nslots), tid);
+#pragma unroll
+    for (int r = 0; r < RG::RPW; ++r) raw[r] = irow[min(wave * RG::RPW + r, max(q.nslots - 1, 0))];
+    const int hl = (wave % C::NSLICE) * T + (lane % T);
+    const char* qbase = reinterpret_cast<const char*>(p.q) + 2 * (q.b * p.q_sb + q.t * p.q_ss + (int64_t)q.g * p.G * p.q_sh);
+    const uint32_t hbytes = (uint32_t)(2 * p.q_sh);
+    // (heads past G: offsets >= G * hbytes, past the range, read zeros)
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, (uint32_t)(p.G - 1) * hbytes + 2u * C::DQK);
+    const uint32_t qoff = (uint32_t)hl * hbytes + 16u * (uint32_t)(lane / T);
+#pragma unroll
+    for (int s = 0; s < C::QREG; ++s) {
+      typedef int i32x4 __attribute__((ext_vector_type(4)));
+      const i32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 2u * (uint32_t)(s * C::KD), 0, 0);
+      qb[s] = __builtin_bit_cast(bf16x8, x);
+    }
+  };
+  // (1b) the LDS-resident steps of Q straight into s_q (buffer_load ... lds,
+  // no VGPRs): head h's steps QREG.. are its dims [16 QREG, DQK), contiguous
+  // in memory, and go to slots h * QLP .. h * QLP + 2 QL - 1 (chunk (s - QREG)
+  // * LG + j = dims 16 s + 8 j); the slot after them is padding (it re-reads
+  // the last chunk).  Instruction k of the workgroup writes slots [64 k, 64 k
+  // + 64); heads past G read zeros (out of range).
+  auto item_qdma = [&](const Params& p, const ItemPos& q, int wave, int lane) {
+    const char* qbase = reinterpret_cast<const char*>(p.q) + 2 * (q.b * p.q_sb + q.t * p.q_ss + (int64_t)q.g * p.G * p.q_sh);
+    const uint32_t hbytes = (uint32_t)(2 * p.q_sh);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, (uint32_t)(p.G - 1) * hbytes + 2u * C::DQK);
+    constexpr int NSLOT = C::QBUF, NINST = (NSLOT + 63) / 64;
+#pragma unroll
+    for (int k0 = 0; k0 < NINST; k0 += C::kWaves) {
+      const int k = k0 + wave;
+      const int u = 64 * k + lane;
+      const int h = u / C::QLP;
+      const int c = min(u - h * C::QLP, 2 * C::QL - 1);
+      const uint32_t off = h < p.G ? (uint32_t)h * hbytes + 32u * C::QREG + 16u * (uint32_t)c : kOOB;
+      static_assert(NSLOT % 64 == 0, "whole instructions");
+      if (k < NINST) dma_lds16_untracked(rq, s_q + 64 * k, off);
+    }
+  };
+  // (2) tile 0's gather into s_k0, from the ids of (1)
+  auto item_gather0 = [&](const Params& p, const ItemPos& q, int wave, int lane) {
+    const Src s = make_src(p, q);
+    Src0 s0;
+    if constexpr (PAGED) {
+      s0 = s;
+    } else {
+      s0.rs = s.rs;
+      s0.row_bytes = s.row_bytes;
+    }
+    const int bound = bound_of(p, q.b);
+    RG0 rg0;
+#pragma unroll
+    for (int r = 0; r < RG::RPW; ++r)
+      rg0.set_row(r, (wave * RG::RPW + r < q.nslots) ? staged_id<PAGED>(p, q.b, raw[r], bound) : -1, true, s0);
+#pragma unroll
+    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, s0, s_k0, wave, lane);
+  };
+  // (3) stage the index row, publish the next claim, wait for this wave's
+  // gathers (tile 0 and Q; VM: the vector-memory operations issued after
+  // them, which need not complete), barrier.  Returns
+  // the item's tile count, trimmed to the last valid slot (tiles of trailing
+  // padding, e.g. a causal row shorter than top-k, contribute nothing).
+  int ipar = 0;  // parity of the current item
+  auto item_stage = [&](const Params& p, const ItemPos& q, int tid, int wave, int lane, bool vm24) -> int {
+    const int ntiles0 = (q.nslots + C::NKT - 1) / C::NKT;
+    const int bound = bound_of(p, q.b);
+    int used;
+    if constexpr (PAGED)
+      used = istage.template store<true>(p, q.b, bound, q.nslots, ntiles0 * C::NKT, s_idx, tid);
+    else
+      used = istage.store_offsets(bound, q.nslots, ntiles0 * C::NKT, s_idx, tid, (uint32_t)(2 * p.k_ss), kOOBRow);
+    used = wave_max_int(used);
+    if (lane == 0) s_used[wave] = used;
+    if constexpr (PERSIST) {
+      if (tid == 0) s_claim[ipar ^ 1] = claim_finish(p.sched, blockIdx.x & 7, nvb, claim_c);
+    }
+    // (the gathers are untracked: this wait and the barrier are what make the
+    // other waves' rows and Q chunks visible)
+    if (vm24)
+      SFA_LDS_BARRIER(24);
+    else
+      SFA_LDS_BARRIER(0);
+    int u = s_used[0];
+#pragma unroll
+    for (int w = 1; w < C::kWaves; ++w) u = max(u, s_used[w]);
+    return (u + C::NKT - 1) / C::NKT;
+  };
+
   int vb = blockIdx.x;
   if constexpr (PERSIST) {
-    if (threadIdx.x == 0) s_claim = claim_item(p_arg.sched, blockIdx.x & 7, nvb);
+    if (threadIdx.x == 0) s_claim[0] = claim_finish(p_arg.sched, blockIdx.x & 7, nvb, claim_start(p_arg.sched, blockIdx.x & 7));
     __syncthreads();
-    vb = s_claim;
+    vb = s_claim[0];
   }
-  int next_vb = -1;  // (thread 0) the item claimed for after this one
+  int ntiles = 0;
+  if (vb >= 0) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    it = item_of(p_arg, vb);
+    item_loads(p_arg, it, tid, wave, lane);
+    item_qdma(p_arg, it, wave, lane);
+    item_gather0(p_arg, it, wave, lane);
+    ntiles = item_stage(p_arg, it, tid, wave, lane, false);
+  }
+
   while (vb >= 0) {
   // The parameters are read through a pointer the compiler cannot see
   // through, once per item: otherwise it hoists every parameter load out of
@@ -150,121 +363,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int slice = wave % C::NSLICE;
   const int ks = wave / C::NSLICE;
-  if constexpr (PERSIST) {
-    if (tid == 0) next_vb = claim_item(p.sched, blockIdx.x & 7, nvb);  // in flight during this item
-  }
-
-  // ---- work item -------------------------------------------------------
-  // Work item = (b, t, g) x split.  Workgroups are dispatched to the 8 XCDs
-  // round-robin (blockIdx % 8); with splits, the splits of one item are
-  // placed on the same XCD (so its L2 serves the item's Q rows to all of
-  // them) whenever the item count allows a bijective mapping.
-  // Without splits, XCD x gets runs of 32 consecutive items (queries), runs
-  // dealt round-robin over the XCDs: the workgroups running together on one
-  // XCD then share the keys their queries have in common (e.g. a recency
-  // window) in its L2.
-  int wi = vb;
-  int split;
-  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
-  if (p.num_splits > 1 && nitems % 8 == 0) {
-    const int x = wi % 8, r = wi / 8;
-    split = r % p.num_splits;
-    wi = (r / p.num_splits) * 8 + x;
-  } else if (p.num_splits == 1 && nitems % 256 == 0) {
-    const int x = wi % 8, r = wi / 8;
-    split = 0;
-    wi = ((r / 32) * 8 + x) * 32 + r % 32;
-  } else {
-    split = wi % p.num_splits;
-    wi /= p.num_splits;
-  }
-  const int g = wi % p.Hkv;
-  wi /= p.Hkv;
-  const int t = wi % p.Sq;
-  const int b = wi / p.Sq;
-  const int slot0 = split * p.split_len;
-  int nslots = p.topk - slot0;
-  if (nslots > p.split_len) nslots = p.split_len;
-  if (nslots < 0) nslots = 0;
-  // (trimmed below to the tiles up to the last valid slot)
-  int ntiles = (nslots + C::NKT - 1) / C::NKT;
-
-  // ---- gather setup (V rows are the K rows: one gather) --------------------
-  // (contiguous rows: the index row is staged as row byte offsets, so a
-  // row's gather base costs a select; the first tile's rows come from the
-  // global ids)
-  typedef typename std::conditional<PAGED, PoolRows, BufRowsOff>::type Src;
-  typedef typename std::conditional<PAGED, PoolRows, BufRows>::type Src0;
-  Src ksrc;
-  if constexpr (PAGED) {
-    ksrc.base = reinterpret_cast<const char*>(p.k) + 2 * g * p.k_sh;
-    ksrc.page_bytes = (uint64_t)(2 * p.k_sb);
-    ksrc.row_bytes = (uint32_t)(2 * p.k_ss);
-    ksrc.shift = p.page_shift;
-  } else {
-    const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
-    ksrc.rs = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
-    ksrc.row_bytes = (uint32_t)(2 * p.k_ss);
-  }
-
-  // The next tile's gather is issued from inside the current tile's S^T MFMA
-  // stream instead of in one burst.
-  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src> RG;
-  typedef RowGather<C::NKT, C::CHK, C::kWaves, C::SWZ, Src0> RG0;
-  const Src0& ksrc0 = ksrc;
-  static_assert(RG::PITCH == C::PK, "gather and readers agree on the pitch");
-  // ---- first tile's gather, then stage indices (invalid -> -1) -----------
-  // Each wave reads the ids of its 8 rows of tile 0 straight from global
-  // memory (uniform addresses), so the first gather is in flight while the
-  // index row is staged and Q is loaded, instead of waiting for both.
-  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh + slot0;
-  const int bound = bound_of(p, b);
-  // The item's index row is requested first (coalesced, all loads in
-  // flight), then the first tile's gather and Q: loads complete in order, so
-  // the wait for the index row covers nothing issued after it.
-  IdxStage<kIdxCap, C::kThreads> istage;
-  istage.load(irow, nslots, tid);
-  {
-    RG0 rg0;
-    // (unconditional loads, all in flight together: slots past the split
-    // re-read its last slot, whose id is then discarded)
-    int raw[RG::RPW];
-#pragma unroll
-    for (int r = 0; r < RG::RPW; ++r) raw[r] = irow[min(wave * RG::RPW + r, max(nslots - 1, 0))];
-#pragma unroll
-    for (int r = 0; r < RG::RPW; ++r)
-      rg0.set_row(r, (wave * RG::RPW + r < nslots) ? staged_id<PAGED>(p, b, raw[r], bound) : -1, true, ksrc0);
-#pragma unroll
-    for (int k = 0; k < RG::NI; ++k) rg0.issue(k, ksrc0, s_k0, wave, lane);
-  }
-
-  // ---- Q^T B operands in registers ------------------------------------
+  const int b = it.b, t = it.t, g = it.g, split = it.split;
+  const Src ksrc = make_src(p, it);
   const int hl = slice * T + (lane % T);  // head within the group
   const bool hvalid = hl < p.G;
-  bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
-  // (issued after the first tile's gather, so the two latencies overlap;
-  // the LDS-resident steps are written once the index row is staged)
-  bf16x8 ql[C::QL > 0 ? C::QL : 1];
-  auto load_q = [&]() {
-    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
-                       (int64_t)(g * p.G + (hvalid ? hl : 0)) * p.q_sh + 8 * (lane / T);
-#pragma unroll
-    for (int s = 0; s < C::QSTEPS; ++s) {
-      bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + s * C::KD);
-      if (!hvalid) x = bf16x8{};
-      if (s < C::QREG)
-        qb[s < C::QREG ? s : 0] = x;
-      else
-        ql[s >= C::QREG ? s - C::QREG : 0] = x;
-    }
-  };
-  // the LDS-resident steps: head hl's row holds its chunks (step s, lane
-  // group j) at slot (s - QREG) * LG + j
-  auto store_q = [&]() {
-#pragma unroll
-    for (int s = C::QREG; s < C::QSTEPS; ++s)
-      *reinterpret_cast<bf16x8*>(&s_q[hl * C::QLP + (s - C::QREG) * C::LG + lane / T]) = ql[s - C::QREG];
-  };
 
   // DMA instruction k follows MFMA number kDmaFirst + kDmaStride * k of the
   // tile's MFMA sequence (QSTEPS S^T MFMAs, then the O^T MFMAs)
@@ -299,7 +401,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   // vmcnt(0) before the barriers that publish a gathered tile, where the
   // compiler does not see the DMA (PoolRows)
   auto dma_done = [&]() {
-    if constexpr (Src::kUntrackedDma) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if constexpr (kUntracked) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   };
 
   // compute(tile) also issues the gather of the next tile into ndst (rg
@@ -541,26 +643,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     M::tail(prev_a, prev_b);
   };
 
-  load_q();
-  int used;
-  if constexpr (PAGED)
-    used = istage.template store<true>(p, b, bound, nslots, ntiles * C::NKT, s_idx, tid);
-  else
-    used = istage.store_offsets(bound, nslots, ntiles * C::NKT, s_idx, tid, ksrc.row_bytes, kOOBRow);
-  used = wave_max_int(used);
-  if (lane == 0) s_used[wave] = used;
-  store_q();
-  dma_done();
-  __syncthreads();  // indices staged, first tile and the LDS part of Q in place
-  // Tiles past the last valid slot (trailing padding, e.g. a causal row
-  // shorter than top-k) contribute nothing and are skipped.
-  {
-    int u = s_used[0];
-#pragma unroll
-    for (int w = 1; w < C::kWaves; ++w) u = max(u, s_used[w]);
-    ntiles = (u + C::NKT - 1) / C::NKT;
-  }
-
   // row offsets of tile 1 (gathered during tile 0) and the validity mask of
   // tile 0; compute() fetches those of the following tiles itself
   RG rg;
@@ -580,12 +662,6 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   // ---- finish: row sums over the lane groups sharing a head -------------------
   const float l_sum = xor32_sum(l_part);
   const float m_fin = m_used;
-
-  // final output staged through LDS (every lane of the wave takes part in the
-  // row stores, so lanes of absent heads stay until then and only skip their
-  // own writes)
-  static_assert(T * (C::DV + 8) * 2 <= C::KBUF * 16 && T * (C::DV + 8) * 2 <= C::QBUF * 8,
-                "a wave's output block fits an idle tile buffer");
   const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
   // Split partials: normalised O of this split in bf16 plus its base-2 LSE
@@ -615,18 +691,36 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   bf16* const obase = partial ? p.part_o + ((int64_t)split * nrows + row0) * C::DV
                               : reinterpret_cast<bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)(g * p.G) * p.o_sh;
   const int64_t orstride = partial ? C::DV : p.o_sh;
-  {
-    // The accumulator layout gives each lane 4-dim pieces of one head, i.e.
-    // stores that touch 32 rows per instruction.  Each wave instead writes
-    // its T x DV bf16 block into a private LDS area (row pitch DV + 8, so the
-    // 8-byte writes of the 32 heads fall in distinct banks), then streams it
-    // out row by row with 16-byte stores (one 1 KB row per instruction).  The
-    // tile buffers are idle here: the last barrier of the tile loop ended
-    // every read of them and every DMA into them.
+
+  // the next item (persistent): its loads go out now, under this output
+  const int vb2 = PERSIST ? s_claim[ipar ^ 1] : -1;
+  ItemPos it2{};
+  if (vb2 >= 0) {
+    it2 = item_of(p, vb2);
+    item_loads(p, it2, tid, wave, lane);
+    item_qdma(p, it2, wave, lane);  // (the Q area is idle: the last S^T has run)
+  }
+
+  // ---- output, staged through LDS ---------------------------------------
+  // The accumulator layout gives each lane 4-dim pieces of one head, i.e.
+  // stores that touch 32 rows per instruction.  Each wave instead writes its
+  // heads' bf16 values into a private LDS area, then streams them out with
+  // 16-byte stores that each cover whole row segments; every lane takes part
+  // in the stores (lanes of absent heads only skip their own writes).
+  //  * one pass (not persistent): all DV dims of the wave's 32 heads (row
+  //    pitch DV + 8, so the 8-byte writes of the heads fall in distinct banks)
+  //    in the tile buffers and the Q area, idle after the tile loop's last
+  //    barrier; one 1 KB row per store instruction;
+  //  * persistent: four rounds of DV / 4 dims (4 accumulators each, row pitch
+  //    DV / 4 + 4) in s_k1 alone, while the next item's Q is gathered into the
+  //    Q area and, after the first round, its tile 0 into s_k0; four 256-byte
+  //    row segments per store instruction.
+  if constexpr (!PERSIST) {
     constexpr int SP = C::DV + 8;
-    char* stg = wave == 0 ? reinterpret_cast<char*>(s_k0)
-              : wave == 1 ? reinterpret_cast<char*>(s_k1)
-                          : reinterpret_cast<char*>(s_q) + (wave - 2) * (C::QBUF * 8);
+    static_assert(T * SP * 2 <= C::KBUF * 16 && T * SP * 2 <= C::QBUF * 8, "a wave's output block fits an idle buffer");
+    char* const stg = wave == 0 ? reinterpret_cast<char*>(s_k0)
+                    : wave == 1 ? reinterpret_cast<char*>(s_k1)
+                                : reinterpret_cast<char*>(s_q) + (wave - 2) * (C::QBUF * 8);
     bf16* srow = reinterpret_cast<bf16*>(stg) + lt * SP;
 #pragma unroll
     for (int ot = 0; ot < C::OT; ++ot) {
@@ -637,6 +731,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
                      (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
         *reinterpret_cast<bf16x4*>(srow + dim) = v4;
       }
+      // one accumulator at a time (see the persistent rounds below)
+      if (ot + 1 < C::OT) asm volatile("" : "+a"(oacc[ot + 1 < C::OT ? ot + 1 : 0])::"memory");
     }
     const bf16* sbase = reinterpret_cast<const bf16*>(stg);
     bf16* const wbase = obase + (int64_t)(slice * T) * orstride;
@@ -646,11 +742,56 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(sbase + r * SP + 8 * lane);
       *reinterpret_cast<bf16x8*>(wbase + (int64_t)r * orstride + 8 * lane) = v;
     }
+  } else {
+    constexpr int NR = 4;                  // rounds
+    constexpr int OTR = C::OT / NR;        // accumulators (32-dim tiles) per round
+    constexpr int DR = OTR * T;            // dims per round
+    constexpr int SPR = DR + 4;            // row pitch (bf16): 66 dwords, so the 32 rows' 8-byte writes fall in distinct banks
+    constexpr int LPR = DR / 8;            // lanes per row segment (16 bytes each)
+    constexpr int RPI = 64 / LPR;          // row segments per store instruction
+    static_assert(C::OT % NR == 0 && 64 % LPR == 0 && T % RPI == 0, "round geometry");
+    static_assert(C::kWaves * T * SPR * 2 <= C::KBUF * 16, "the rounds fit one tile buffer");
+    bf16* const stg = reinterpret_cast<bf16*>(s_k1) + wave * (T * SPR);
+    const int sr = lane / LPR, sc = lane % LPR;  // row within an instruction's group, 16-byte chunk
+#pragma unroll
+    for (int rd = 0; rd < NR; ++rd) {
+#pragma unroll
+      for (int o = 0; o < OTR; ++o) {
+        const int ot = rd * OTR + o;
+#pragma unroll
+        for (int q4 = 0; q4 < C::CPL / 4; ++q4) {
+          const int dim = o * T + 4 * C::LG * q4 + 4 * hq;
+          bf16x4 v4 = {(bf16)(oacc[ot][4 * q4 + 0] * scale_o), (bf16)(oacc[ot][4 * q4 + 1] * scale_o),
+                       (bf16)(oacc[ot][4 * q4 + 2] * scale_o), (bf16)(oacc[ot][4 * q4 + 3] * scale_o)};
+          *reinterpret_cast<bf16x4*>(stg + lt * SPR + dim) = v4;
+        }
+        // one accumulator at a time: its writes are issued before the next
+        // one's values are read (else the compiler reads all 256 up front)
+        if (ot + 1 < C::OT) asm volatile("" : "+a"(oacc[ot + 1 < C::OT ? ot + 1 : 0])::"memory");
+      }
+#pragma unroll
+      for (int j = 0; j < T / RPI; ++j) {
+        const int r = j * RPI + sr;  // head within the wave's slice
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(stg + r * SPR + 8 * sc);
+        if (slice * T + r < p.G)
+          *reinterpret_cast<bf16x8*>(obase + (int64_t)(slice * T + r) * orstride + rd * DR + 8 * sc) = v;
+      }
+      if (rd == 0 && vb2 >= 0) item_gather0(p, it2, wave, lane);
+    }
   }
   if constexpr (!PERSIST) break;
-  if (tid == 0) s_claim = next_vb;
-  __syncthreads();  // every wave is done with this item's LDS; the next claim is visible
-  vb = s_claim;
+  if (vb2 >= 0) {
+    // the wave's last three rounds issued 24 stores after its gathers unless
+    // its head slice is partly absent (then some lanes' stores are skipped and
+    // the count is not known here): then wait for everything.  (The barrier
+    // also ends every staging read of s_k1, which the next item's tile 1
+    // overwrites.)
+    const bool vm24 = p.G - slice * T >= T;
+    ipar ^= 1;
+    ntiles = item_stage(p, it2, tid, wave, lane, vm24);
+  }
+  it = it2;
+  vb = vb2;
   }  // items
 }
 

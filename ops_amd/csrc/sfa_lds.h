@@ -152,6 +152,21 @@ struct BufRows {
 struct BufRowsOff : BufRows {
   __device__ __forceinline__ base_t row_base(int off, bool valid) const { return valid ? (uint32_t)off : kOOBRow; }
 };
+// One buffer_load_dwordx4 ... lds (M0 = the wave's LDS destination, lane l
+// writes 16 bytes at M0 + 16 l) as inline asm: the compiler neither sees nor
+// waits for it (its builtin form makes every later LDS read that the
+// compiler cannot tell apart wait for vmcnt(0)).  The caller waits for
+// vmcnt itself before the barrier that publishes the data.
+__device__ __forceinline__ void dma_lds16_untracked(__amdgpu_buffer_rsrc_t rs, u32x4* dst, uint32_t off) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(rs)
+               : "memory", "m0");
+}
+// BufRows with untracked DMA (dma_lds16_untracked)
+struct BufRowsUT : BufRows {
+  __device__ __forceinline__ void load_lds16(u32x4* dst, base_t off) const { dma_lds16_untracked(rs, dst, off); }
+  static constexpr bool kUntrackedDma = true;
+};
 // Rows of a paged pool (ids are pool rows): 64-bit addresses, since a pool
 // may exceed the 4 GiB a buffer offset reaches; padding rows read kZeroRow.
 // The DMA (global_load_lds_dwordx4: M0 = the wave's LDS destination, lane l
