@@ -171,8 +171,9 @@ SFA_API int sfa_abi_version(void);
 SFA_API const char* sfa_last_error(void);
 
 /* Bytes of device workspace sfa_fwd needs for `a` (0 when none).
- * Replaces the per-launch workspaces of SFA.py:117-120; only the split-k
- * partial results of the decode shape remain. */
+ * Replaces the per-launch workspaces of SFA.py:117-120; what remains: the
+ * split-k partial results of the decode shape, and 256 bytes of work-claim
+ * counters for the persistent MLA prefill (>= 4096 work items). */
 SFA_API size_t sfa_fwd_workspace_size(const sfa_fwd_args* a);
 
 /* Forward: out = softmax(scale * q k[idx]^T) v[idx], lse = log-sum-exp.
@@ -185,8 +186,9 @@ SFA_API int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_byt
 /* Forward that allocates nothing and takes no workspace: the same arguments,
  * kernels and results as sfa_fwd.  No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP-graph capture,
- * tight serving loops, harnesses that forbid hipMalloc).  The split-k partials
- * of the decode shape (sfa_fwd_workspace_size(a) bytes) go to a static device
+ * tight serving loops, harnesses that forbid hipMalloc).  The workspace of
+ * sfa_fwd (sfa_fwd_workspace_size(a) bytes: decode split-k partials, prefill
+ * claim counters) goes to a static device
  * buffer of SFA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
  * until the process ends; a plan that needs more returns SFA_E_WORKSPACE
  * before any device work.  `stream` must belong to the current device; the

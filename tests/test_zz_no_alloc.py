@@ -1,9 +1,10 @@
 """GPU test of sfa_fwd_noalloc, the forward entry point that allocates
-nothing (split-k partials in the library's static per-GPU scratch), called
-through the C ABI: its results must be bitwise those of sfa_fwd (same
-kernels, same split plan, caller workspace) and within the oracle's bars,
-on two calls in a row, the second with a smaller input (a different kernel
-family), and again on the first input afterwards."""
+nothing (split-k partials and the persistent prefill's claim counters in the
+library's static per-GPU scratch), called through the C ABI: its results
+must be bitwise those of sfa_fwd (same kernels, same split plan, caller
+workspace) and within the oracle's bars, on two calls in a row, the second
+with a smaller input (a different kernel family), and again on the first
+input afterwards."""
 import ctypes
 import math
 import sys
@@ -13,6 +14,7 @@ import torch
 
 from ops_amd import _lib
 from ops_amd import sfa as sfa_mod
+from ops_amd.workloads import make_workload
 from oracle.sfa_oracle import sfa_forward as ref_forward
 
 pytestmark = pytest.mark.gpu
@@ -90,3 +92,30 @@ def test_noalloc_matches_sfa_fwd_on_consecutive_calls():
         assert torch.equal(o_na, o_ws) and torch.equal(l_na, l_ws), name
         _check_oracle(o_na, l_na, q.float(), k.float(), v.float(), idx, kv_lens, scale)
     assert sizes[1] < sizes[0]
+
+
+def test_noalloc_persistent_prefill_after_decode():
+    """MLA prefill at S = 4100 (>= 4096 items: the persistent schedule, whose
+    per-XCD claim counters sit in the static scratch and are cleared by a fill
+    kernel on every call) right after a decode call that left split-k partials
+    there, then a smaller prefill (S = 1000, plain grid): bitwise equal to
+    sfa_fwd, sampled rows within the oracle's bars."""
+    dec = dict(B=2, Skv=1024, Hq=32, Hkv=2, Dqk=128, Dv=128, K=256, seed=3, shared_kv=False)
+    q, k, v, idx, kv_lens = (t.to(DEV) for t in _decode_case(**dec))
+    _run("noalloc", q, k, v, idx, kv_lens, 1.0 / math.sqrt(128))
+    sizes = []
+    for S in (4100, 1000):
+        _say(f"sfa_fwd_noalloc vs sfa_fwd: mla prefill S={S} K=256 Hq=128")
+        w = make_workload("mla_prefill", device=DEV, S=S, K=256)
+        o_na, l_na, ws = _run("noalloc", w.q, w.k, w.v, w.idx, None, w.scale)
+        o_ws, l_ws, _ = _run("workspace", w.q, w.k, w.v, w.idx, None, w.scale)
+        sizes.append(ws)
+        assert ws <= _lib.SFA_NOALLOC_SCRATCH_BYTES
+        assert torch.equal(o_na, o_ws) and torch.equal(l_na, l_ws), S
+        rows = torch.tensor([0, 1, 255, 256, S // 2, S - 2, S - 1])
+        o_ref, l_ref = ref_forward(w.q[:, rows].float().cpu(), w.k.float().cpu(), w.v.float().cpu(),
+                                   w.idx[:, rows].cpu(), w.scale)
+        err_o = float((o_na[:, rows].float().cpu() - o_ref).abs().max())
+        err_l = float((l_na[:, rows].cpu() - l_ref).abs().max())
+        assert err_o <= 2e-2 and err_l <= 1e-3, (S, err_o, err_l)
+    assert sizes[0] > 0 and sizes[1] == 0
