@@ -17,11 +17,12 @@
 //     least one of its keys (`blist`, a per-key-block CSR at block
 //     granularity), with `bstart` marking where each chunk of kChunk
 //     consecutive query blocks (an absolute query range) begins in it.
-//  2. Key-major recompute.  One workgroup owns a key block (each wave 32
-//     keys, K and V rows kept in registers) and one chunk: the listed query
-//     blocks in one absolute range of kChunk query blocks, so the workgroups
-//     of neighbouring key blocks that run together read the same query
-//     blocks.  Per query block it recomputes, for every (row, key)
+//  2. Key-major recompute.  A work unit is a key block (each wave 32 keys, K
+//     and V rows kept in registers) and one chunk: the listed query blocks in
+//     one absolute range of kChunk query blocks.  One persistent workgroup
+//     per CU claims units from a counter, longest first and otherwise in
+//     chunk-descending order, so the units that run together are key blocks
+//     of the same query range and read the same query blocks.  Per query block it recomputes, for every (row, key)
 //     pair of the block, S = Q K^T and dP = dO V^T (32x32x16 MFMA, rows as
 //     M, keys as N), P = 2^(S scale log2e - lse2) and dS = P (dP - δ) masked
 //     by the bitmap, and accumulates dV^T += dO^T P and dK^T += Q^T dS in
@@ -56,6 +57,16 @@ static_assert(kTB % 64 == 0 && kCH == 16, "block buffers: 4 rows per DMA instruc
 //    (dV / dK A operands): blk_swz(4m + i) = 4 i + (m & 3) sends the group of
 //    each of the 4 rows to a different group.
 __device__ __forceinline__ int blk_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// A pointer that is the same in every lane, read from the first lane (a
+// buffer descriptor built from it then stays scalar)
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
 
 // ---- 1a. membership bitmap and repeated-slot flags ------------------------
 // One workgroup per index row (b, t, g): the row's bitmap is built with LDS
@@ -176,12 +187,85 @@ __global__ __launch_bounds__(256) void csr_scatter_wave_kernel(Params p) {
     *reinterpret_cast<u32x4*>(mrow + w) = *reinterpret_cast<const u32x4*>(map + w);
 }
 
+// ---- 1c. the key-major kernel's claim order --------------------------------
+// Units u = (chunk, key block, (b, g)) in base order: chunk-descending, then
+// key block, then (b, g).  The non-empty units are listed longest first, in
+// classes of 16 query blocks (a unit of n listed query blocks is in class
+// (kChunk - n) / 16), each class in base order: the full units keep their
+// grouping by query range (the units that run together share their query
+// blocks in L2), and the short ones, claimed last, fill the end of the
+// key-major kernel.  One workgroup: a unit's position is its class's start
+// plus the count of earlier units of its class (ballots, then a prefix over
+// the waves of the tile and the tiles before it).
+constexpr int kClasses = kChunk / 16;
+__global__ __launch_bounds__(1024) void unit_order_kernel(Params p) {
+  __shared__ int s_cnt[16][kClasses];
+  __shared__ int s_start[kClasses];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbg = p.B * p.Hkv, per_chunk = nbg * p.nkb, nunits = per_chunk * p.max_chunks;
+  auto cls = [&](int u) -> int {  // class of unit u, -1 if it has no query block
+    const int c = p.max_chunks - 1 - u / per_chunk;
+    const int kb = (u % per_chunk) / nbg, bg = (u % per_chunk) % nbg;
+    const int* start = p.bstart + ((int64_t)bg * p.nkb + kb) * (p.max_chunks + 1);
+    const int n = start[c + 1] - start[c];
+    return n > 0 ? (kChunk - n) / 16 : -1;
+  };
+  // class sizes
+  int cnt[kClasses] = {};
+  for (int u = tid; u < nunits; u += 1024) {
+    const int k = cls(u);
+#pragma unroll
+    for (int j = 0; j < kClasses; ++j) cnt[j] += k == j;
+  }
+#pragma unroll
+  for (int j = 0; j < kClasses; ++j) {
+    const int w = wave_sum_int(cnt[j]);
+    if (lane == 0) s_cnt[wave][j] = w;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int j = 0; j < kClasses; ++j) {
+      s_start[j] = acc;
+      for (int w = 0; w < 16; ++w) acc += s_cnt[w][j];
+    }
+    p.kctr[0] = 0;
+    p.kctr[1] = acc;
+  }
+  __syncthreads();
+  // positions, tile by tile in base order
+  for (int u0 = 0; u0 < nunits; u0 += 1024) {
+    const int u = u0 + tid;
+    const int k = u < nunits ? cls(u) : -1;
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < kClasses; ++j) {
+      const uint64_t m = __ballot(k == j);
+      if (lane == 0) s_cnt[wave][j] = __popcll(m);
+      if (k == j) rank = __popcll(m & ((1ull << lane) - 1ull));
+    }
+    __syncthreads();
+    if (k >= 0) {
+      int pos = s_start[k] + rank;
+      for (int w = 0; w < wave; ++w) pos += s_cnt[w][k];
+      p.uorder[pos] = u;
+    }
+    __syncthreads();
+    if (tid < kClasses) {
+      int t = 0;
+      for (int w = 0; w < 16; ++w) t += s_cnt[w][tid];
+      s_start[tid] += t;
+    }
+    __syncthreads();
+  }
+}
+
 // ---- 2. key-major dK / dV ---------------------------------------------------
 // LDS: Q and dO blocks double buffered (row r = query (r >> lg_g), head
 // (r & (G - 1)); swizzled, see blk_swz), each row's lse and δ, and per wave the
 // bitmap word of its 32 keys for each row.  Buffers are separate arrays so
 // reads of one are not made to wait for DMA into the other.
-__global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
+__global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p_arg) {
   typedef Mfma<32> M;
   typedef M::acc_t acc_t;
   __shared__ u32x4 s_q0[kTB];
@@ -195,38 +279,54 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint32_t s_msk0[4][kRowBlock];
   __shared__ __attribute__((aligned(16))) uint32_t s_msk1[4][kRowBlock];
   __shared__ int s_list[kChunk];
+  // claimed units by parity: unit i's successor is claimed during unit i and
+  // published in the other slot behind unit i's barriers
+  __shared__ int s_unit[2];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  // Units are claimed from one counter in the order unit_order_kernel lists
+  // them (the full ones first, grouped by query range; the short ones last).
+  // Claiming balances the CUs however unequal the units are (a fixed unit ->
+  // workgroup mapping leaves CUs idle: workgroups are dispatched to the XCDs
+  // in turn, so an XCD whose units are longer holds back the dispatch to the
+  // others).  A claim is published as the unit itself, or -1 past the list.
+  const int nbg = p_arg.B * p_arg.Hkv;
+  const int per_chunk = nbg * p_arg.nkb;
+  // (an offset the compiler cannot prove uniform keeps the atomic a single
+  // lane's: for a uniform address it is rewritten into a wave reduction that
+  // waits for every load in flight)
+  auto claim = [](const Params& q) {
+    int o = 0;
+    asm volatile("" : "+v"(o));
+    const int i = atomicAdd(q.kctr + o, 1);
+    return i < q.kctr[1] ? q.uorder[i] : -1;
+  };
+  if (threadIdx.x == 0) s_unit[0] = claim(p_arg);
+  __syncthreads();
+  int par = 0;
+  for (;;) {
+  const Params& p = p_arg;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Workgroup = (b, g, key block kb, chunk c): the entries of kb's list that
-  // fall in query blocks [128 c, 128 (c + 1)).  Workgroups are dispatched to
-  // the 8 XCDs round-robin; when the key-block count allows, XCD x gets the
-  // key blocks kb = x (mod 8) in chunk-major order, so the workgroups that run
-  // together on one XCD share query blocks (its L2 serves them once loaded).
-  // Within an XCD the order is chunk-descending across all (b, g): the long
-  // workgroups (late chunks see the most key blocks) start first, the short
-  // diagonal ones fill the tail.
-  const int nbg = p.B * p.Hkv;
-  int bg, kb, c;
-  if (p.nkb % 8 == 0) {
-    const int x = blockIdx.x % 8, r = blockIdx.x / 8, per = p.nkb / 8;
-    kb = x + 8 * (r % per);
-    bg = (r / per) % nbg;
-    c = p.max_chunks - 1 - r / (per * nbg);
-  } else {
-    const int per_bg = p.nkb * p.max_chunks;
-    bg = blockIdx.x / per_bg;
-    const int l = blockIdx.x % per_bg;
-    kb = l / p.max_chunks;
-    c = l % p.max_chunks;
-  }
+  // (read as uniform: a value loaded from LDS is a per-lane value to the
+  // compiler, and every address derived from it would be built per lane)
+  const int u = __builtin_amdgcn_readfirstlane(s_unit[par]);
+  if (u < 0) break;
+  if (tid == 0) s_unit[par ^ 1] = claim(p);
+  par ^= 1;
+  const int c = p.max_chunks - 1 - u / per_chunk;
+  const int kb = (u % per_chunk) / nbg;
+  const int bg = (u % per_chunk) % nbg;
   const int g = bg % p.Hkv;
   const int b = bg / p.Hkv;
   const int64_t bgk = ((int64_t)b * p.Hkv + g) * p.nkb + kb;
   const int* start = p.bstart + bgk * (p.max_chunks + 1);
-  const int e0 = start[c];
-  const int nblk = start[c + 1] - e0;
-  if (nblk <= 0) return;  // the whole workgroup: no query block in this chunk
+  const int e0 = __builtin_amdgcn_readfirstlane(start[c]);
+  const int nblk = __builtin_amdgcn_readfirstlane(start[c + 1]) - e0;
+  if (nblk <= 0) {  // no query block of this chunk selects the key block
+    __syncthreads();
+    continue;
+  }
   for (int i = tid; i < nblk; i += 256) s_list[i] = p.blist[bgk * p.nqb + e0 + i];
 
   const int G = p.G, lg = p.lg_g;
@@ -250,20 +350,22 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
     }
   }
 
-  // buffer resources (ranges checked on the host to fit 31 bits)
+  // buffer resources (ranges checked on the host to fit 31 bits; the bases
+  // are the unit's, the same in every lane, and are read as such so that no
+  // load waits on a loop over distinct descriptors)
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-      reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + (int64_t)(g * G) * p.q_sh,
+      uniform_ptr(reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + (int64_t)(g * G) * p.q_sh),
       (uint32_t)(2 * ((int64_t)(p.Sq - 1) * p.q_ss + (int64_t)(G - 1) * p.q_sh + kD)));
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(
-      reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + (int64_t)(g * G) * p.do_sh,
+      uniform_ptr(reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + (int64_t)(g * G) * p.do_sh),
       (uint32_t)(2 * ((int64_t)(p.Sq - 1) * p.do_ss + (int64_t)(G - 1) * p.do_sh + kD)));
   // per-row start values of the S and dP accumulators (-lse / scale, -δ)
   const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
   const uint32_t rc_bytes = (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.Hq + G));
-  const __amdgpu_buffer_rsrc_t rl = make_rsrc(p.rowc + (int64_t)b * p.Sq * p.Hq + g * G, rc_bytes);
-  const __amdgpu_buffer_rsrc_t rdl = make_rsrc(p.rowc + nrows + (int64_t)b * p.Sq * p.Hq + g * G, rc_bytes);
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(uniform_ptr(p.rowc + (int64_t)b * p.Sq * p.Hq + g * G), rc_bytes);
+  const __amdgpu_buffer_rsrc_t rdl = make_rsrc(uniform_ptr(p.rowc + nrows + (int64_t)b * p.Sq * p.Hq + g * G), rc_bytes);
   const __amdgpu_buffer_rsrc_t rm = make_rsrc(
-      p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4,
+      uniform_ptr(p.kmap + ((int64_t)b * p.Hkv + g) * p.Sq * p.kmap_w + kb * 4),
       (uint32_t)(4 * ((int64_t)(p.Sq - 1) * p.kmap_w + 4)));
 
   // Query block qb into one set of buffers: Q / dO rows (32 instructions
@@ -532,6 +634,8 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p) {
       *reinterpret_cast<f32x4*>(part + kD + dim) = v4;
     }
   }
+  __syncthreads();  // the next unit's list and blocks overwrite the LDS; its claim is published
+  }  // units
 }
 
 // ---- 3. chunk partials -> per-key accumulators (chunk order) --------------
@@ -595,7 +699,8 @@ size_t csr_workspace_bytes(const Params& p) {
   const size_t bg = (size_t)p.B * p.Hkv;
   return al256(bg * p.Sq * p.kmap_w * 4) + al256((size_t)p.B * p.Sq * p.Hkv * p.topk) +
          al256(bg * p.nkb * p.nqb * 4) + al256(bg * p.nkb * (p.max_chunks + 1) * 4) +
-         al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4) + al256((size_t)2 * p.B * p.Sq * p.Hq * 4);
+         al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4) + al256((size_t)2 * p.B * p.Sq * p.Hq * 4) + 256 +
+         al256(bg * p.nkb * p.max_chunks * 4);
 }
 
 void csr_bind_workspace(Params& p, void* ws) {
@@ -612,6 +717,10 @@ void csr_bind_workspace(Params& p, void* ws) {
   p.dkv_part = reinterpret_cast<float*>(c);
   c += al256(bg * p.nkb * p.max_chunks * kKeyBlock * 2 * kD * 4);
   p.rowc = reinterpret_cast<float*>(c);
+  c += al256((size_t)2 * p.B * p.Sq * p.Hq * 4);
+  p.kctr = reinterpret_cast<int*>(c);
+  c += 256;
+  p.uorder = reinterpret_cast<int*>(c);
 }
 
 hipError_t launch_csr_index(const Params& p, hipStream_t s) {
@@ -621,11 +730,18 @@ hipError_t launch_csr_index(const Params& p, hipStream_t s) {
   else
     hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)rows), dim3(256), 0, s, p);
   hipLaunchKernelGGL(csr_blocklist_kernel, dim3((unsigned)((int64_t)p.B * p.Hkv * p.nkb)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(unit_order_kernel, dim3(1), dim3(1024), 0, s, p);
   return hipGetLastError();
 }
 
 hipError_t launch_csr_dkv(const Params& p, hipStream_t s) {
-  const int64_t wgs = (int64_t)p.B * p.Hkv * p.nkb * p.max_chunks;
+  // persistent: one workgroup per CU (its LDS use allows one)
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int64_t units = (int64_t)p.B * p.Hkv * p.nkb * p.max_chunks;
+  const int64_t wgs = units < cus ? units : cus;
   hipLaunchKernelGGL(dkv_keymajor_kernel, dim3((unsigned)wgs), dim3(256), 0, s, p);
   const int64_t n4 = (int64_t)p.B * p.Skv * p.Hkv * (2 * kD / 4);
   hipLaunchKernelGGL(dkv_reduce_kernel, dim3(grid_stride_blocks(n4)), dim3(256), 0, s, p);

@@ -65,6 +65,8 @@ struct Params {
   int* bstart;        // [B][Hkv][nkb][max_chunks + 1] blist index of each 128-query-block chunk's first entry
   float* dkv_part;    // [B][Hkv][nkb][max_chunks][128][2 D] fp32 partial dK | dV per chunk
   float* rowc;        // [2][B*Sq*Hq] per row: -lse / scale, then -δ (written by the δ pass)
+  int* kctr;          // key-major claims: [0] counter, [1] listed units (both set by unit_order_kernel)
+  int* uorder;        // [B*Hkv*nkb*max_chunks] key-major units in claim order (non-empty ones only)
   int nkb, nqb;       // key blocks (128 keys), query blocks (128 / G queries)
   int lg_g;           // log2(G)
   int max_chunks;     // chunks per key block (query blocks / chunk, rounded up)
@@ -169,6 +171,11 @@ struct IdxStage {
 __device__ __forceinline__ int wave_max_int(int x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ int wave_sum_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
   return x;
 }
 

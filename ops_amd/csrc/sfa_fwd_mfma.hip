@@ -330,7 +330,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   if constexpr (PERSIST) {
     if (threadIdx.x == 0) s_claim[0] = claim_finish(p_arg.sched, blockIdx.x & 7, nvb, claim_start(p_arg.sched, blockIdx.x & 7));
     __syncthreads();
-    vb = s_claim[0];
+    // (read as uniform: a value loaded from LDS is a per-lane value to the
+    // compiler, and every address derived from it would be built per lane)
+    vb = __builtin_amdgcn_readfirstlane(s_claim[0]);
   }
   int ntiles = 0;
   if (vb >= 0) {
@@ -693,7 +695,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   const int64_t orstride = partial ? C::DV : p.o_sh;
 
   // the next item (persistent): its loads go out now, under this output
-  const int vb2 = PERSIST ? s_claim[ipar ^ 1] : -1;
+  const int vb2 = PERSIST ? __builtin_amdgcn_readfirstlane(s_claim[ipar ^ 1]) : -1;
   ItemPos it2{};
   if (vb2 >= 0) {
     it2 = item_of(p, vb2);
