@@ -81,6 +81,7 @@ sfa::Params to_params(const sfa_fwd_args* a, const sfa_kv_pages* pg = nullptr) {
     p.bt_sb = pg->bt_sb;
     p.page_shift = __builtin_ctz((unsigned)pg->page_size);
     p.num_pages = pg->num_pages;
+    p.pool_shift = sfa::pool_unit_shift(2 * a->k_sb, 2 * a->k_ss);
   }
   p.q = a->q; p.k = a->k; p.v = a->v; p.idx = a->idx; p.kv_lens = a->kv_lens; p.sink = a->sink;
   p.out = a->out; p.lse = a->lse;

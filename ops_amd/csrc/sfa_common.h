@@ -39,6 +39,7 @@ struct Params {
   int64_t bt_sb;
   int page_shift;
   int num_pages;
+  int pool_shift;     // paged MLA gathers: staged pool offsets are in units of 2^pool_shift bytes
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e): scores in base-2 units
   // split-k partial results (forward, num_splits > 1)
@@ -103,12 +104,33 @@ __device__ __forceinline__ int paged_row(const Params& p, int b, int id, int bou
   return (pg << p.page_shift) | (id & ((1 << p.page_shift) - 1));
 }
 
+// Unit (log2 bytes) of the pool offsets the paged MLA gathers stage: the
+// largest power of two up to 2^7 that divides both the page and the row
+// stride, so an offset of a pool up to 2^(31 + shift) bytes fits 31 bits.
+__host__ __device__ inline int pool_unit_shift(int64_t page_bytes, int64_t row_bytes) {
+  const uint64_t m = (uint64_t)(page_bytes | row_bytes);
+  int sh = 0;
+  while (sh < 7 && ((m >> sh) & 1u) == 0) ++sh;
+  return sh;
+}
+
 // The staged id of a slot: the key row itself (contiguous k / v) or its pool
 // row (paged), -1 for an invalid slot.
 template <bool PAGED>
 __device__ __forceinline__ int staged_id(const Params& p, int b, int id, int bound) {
   if (PAGED) return paged_row(p, b, id, bound);
   return (id >= 0 && id < bound) ? id : -1;
+}
+
+// The staged form of a slot for the paged MLA gathers: the byte offset of its
+// pool row from the (kv head's) pool base in units of 2^pool_shift bytes, -1
+// for an invalid slot (the tile loop then forms a row's 64-bit address with
+// one shift and one add instead of the page arithmetic).
+__device__ __forceinline__ uint64_t pool_row_offset(uint32_t r, int shift, uint64_t page_bytes, uint32_t row_bytes);
+__device__ __forceinline__ int staged_pool_off(const Params& p, int b, int id, int bound) {
+  const int r = paged_row(p, b, id, bound);
+  if (r < 0) return -1;
+  return (int)(pool_row_offset((uint32_t)r, p.page_shift, (uint64_t)(2 * p.k_sb), (uint32_t)(2 * p.k_ss)) >> p.pool_shift);
 }
 
 // Index row of a work item, in two phases so that its global loads are in
@@ -144,6 +166,21 @@ struct IdxStage {
     int st[IPT];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_id<PAGED>(p, b, v[j], bound) : -1;
+    int used = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      if (tid + j * THREADS < nstage) s_idx[tid + j * THREADS] = st[j];
+      if (st[j] >= 0) used = tid + j * THREADS + 1;
+    }
+    return used;
+  }
+  // store() for the paged MLA gathers: each slot's scaled pool offset
+  // (staged_pool_off)
+  __device__ __forceinline__ int store_pool_offsets(const Params& p, int b, int bound, int nslots, int nstage,
+                                                    int* s_idx, int tid) {
+    int st[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_pool_off(p, b, v[j], bound) : -1;
     int used = 0;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {

@@ -217,9 +217,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     Src s;
     if constexpr (PAGED) {
       s.base = reinterpret_cast<const char*>(p.k) + 2 * q.g * p.k_sh;
-      s.page_bytes = (uint64_t)(2 * p.k_sb);
-      s.row_bytes = (uint32_t)(2 * p.k_ss);
-      s.shift = p.page_shift;
+      s.shift = p.pool_shift;
     } else {
       const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (q.b * p.k_sb + q.g * p.k_sh);
       s.rs = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + C::DQK)));
@@ -291,7 +289,10 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     RG0 rg0;
 #pragma unroll
     for (int r = 0; r < RG::RPW; ++r)
-      rg0.set_row(r, (wave * RG::RPW + r < q.nslots) ? staged_id<PAGED>(p, q.b, raw[r], bound) : -1, true, s0);
+      rg0.set_row(r, (wave * RG::RPW + r < q.nslots) ? (PAGED ? staged_pool_off(p, q.b, raw[r], bound)
+                                                              : staged_id<false>(p, q.b, raw[r], bound))
+                                                    : -1,
+                  true, s0);
 #pragma unroll
     for (int k = 0; k < RG::NI; ++k) rg0.issue(k, s0, s_k0, wave, lane);
   };
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     const int bound = bound_of(p, q.b);
     int used;
     if constexpr (PAGED)
-      used = istage.template store<true>(p, q.b, bound, q.nslots, ntiles0 * C::NKT, s_idx, tid);
+      used = istage.store_pool_offsets(p, q.b, bound, q.nslots, ntiles0 * C::NKT, s_idx, tid);
     else
       used = istage.store_offsets(bound, q.nslots, ntiles0 * C::NKT, s_idx, tid, (uint32_t)(2 * p.k_ss), kOOBRow);
     used = wave_max_int(used);
@@ -832,7 +833,13 @@ bool v_is_k_prefix(const Params& p) {
 // contiguous rows are addressed by 32-bit buffer offsets; paged pools by
 // 64-bit addresses (pool rows fit an int by the API's check)
 bool rows_fit_32bit(const Params& p) {
-  if (p.block_table) return true;
+  if (p.block_table) {
+    // the staged pool offsets (units of 2^pool_shift bytes) must fit 31 bits
+    const int64_t page_bytes = 2 * p.k_sb, row_bytes = 2 * p.k_ss;
+    const int64_t rows_per_page = (int64_t)1 << p.page_shift;
+    const int64_t last = (int64_t)(p.num_pages - 1) * page_bytes + (rows_per_page - 1) * row_bytes;
+    return p.pool_shift == pool_unit_shift(page_bytes, row_bytes) && (last >> p.pool_shift) < ((int64_t)1 << 31);
+  }
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
   return kb < (int64_t)kOOB && vb < (int64_t)kOOB && fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss);

@@ -167,8 +167,9 @@ struct BufRowsUT : BufRows {
   __device__ __forceinline__ void load_lds16(u32x4* dst, base_t off) const { dma_lds16_untracked(rs, dst, off); }
   static constexpr bool kUntrackedDma = true;
 };
-// Rows of a paged pool (ids are pool rows): 64-bit addresses, since a pool
-// may exceed the 4 GiB a buffer offset reaches; padding rows read kZeroRow.
+// Rows of a paged pool (ids are the scaled pool offsets of staged_pool_off):
+// 64-bit addresses, since a pool may exceed the 4 GiB a buffer offset
+// reaches; padding rows read kZeroRow.
 // The DMA (global_load_lds_dwordx4: M0 = the wave's LDS destination, lane l
 // writes 16 bytes at M0 + 16 l) is issued as inline asm: the compiler counts
 // its builtin form against the LDS counter too, which turns every later
@@ -177,14 +178,12 @@ struct BufRowsUT : BufRows {
 // the kernel waits for vmcnt(0) itself before the barrier that publishes a
 // tile (waits the compiler inserts for other loads only get stricter).
 struct PoolRows {
-  const char* base;      // pool base + the kv head's offset
-  uint64_t page_bytes;   // page stride
-  uint32_t row_bytes;    // row stride within a page
-  int shift;             // log2(rows per page)
+  const char* base;  // pool base + the kv head's offset
+  int shift;         // staged offsets are in units of 2^shift bytes
   typedef uint64_t base_t;
-  __device__ __forceinline__ base_t row_base(int id, bool valid) const {
-    return (valid && id >= 0) ? (uint64_t)(uintptr_t)base + pool_row_offset((uint32_t)id, shift, page_bytes, row_bytes)
-                              : (uint64_t)(uintptr_t)kZeroRow;
+  __device__ __forceinline__ base_t row_base(int off, bool valid) const {
+    return (valid && off >= 0) ? (uint64_t)(uintptr_t)base + ((uint64_t)(uint32_t)off << shift)
+                               : (uint64_t)(uintptr_t)kZeroRow;
   }
   __device__ __forceinline__ void load_lds16(u32x4* dst, base_t addr) const {
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
