@@ -136,3 +136,31 @@ def test_csr_matches_atomic_and_is_deterministic():
         assert torch.equal(a, b), f"{name} differs between two CSR runs"
         e = _rel_l2(a, c)
         assert e <= 2e-3, f"{name} CSR vs atomic rel-L2 {e}"
+
+
+def test_csr_empty_and_unequal_units():
+    """An index set whose (key block, chunk) units are full, empty or short:
+    queries t < 2048 select 64 keys uniformly from [0, 4096) (key blocks 0-31
+    dense in query chunks 0-1, empty in chunks 2-3), later queries 64 keys
+    from a band of 256 around 4 t (short units of key blocks 63-127); key
+    blocks 32-62 are never selected.  2 x 2 (b, kv head) x 128 key blocks x 4
+    chunks = 2048 units, so the claim-order list spans two of its kernel's
+    1024-unit tiles.  dQ/dK/dV against the oracle, and bitwise run to run."""
+    _say("csr backward: empty / full / short units, B=2 Sq=4096 Skv=16384 Hq=32 Hkv=2 K=64")
+    B, Sq, Skv, Hq, Hkv, K = 2, 4096, 16384, 32, 2, 64
+    g = torch.Generator(device="cpu").manual_seed(11)
+    q = torch.randn(B, Sq, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    do = torch.randn(B, Sq, Hq, 128, generator=g).to(torch.bfloat16)
+    early = torch.rand(B, 2048, Hkv, 4096, generator=g).argsort(-1)[..., :K]
+    t = torch.arange(2048, Sq)
+    band = torch.rand(B, Sq - 2048, Hkv, 256, generator=g).argsort(-1)[..., :K]
+    late = band + (4 * t - 128).clamp(max=Skv - 256).view(1, -1, 1, 1)
+    idx = torch.cat([early, late], dim=1).to(torch.int32)
+    assert int(idx.min()) >= 0 and int(idx.max()) < Skv
+    res = _run(q, k, v, do, idx, "csr")
+    _check_vs_oracle(q, k, v, do, idx, res)
+    res2 = _run(q, k, v, do, idx, "csr")
+    for a, b in zip(res[2:5], res2[2:5]):
+        assert torch.equal(a, b)
