@@ -341,11 +341,25 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(Params p) {
 // issues its NS partial-row loads together with the LSE loads, before the
 // weights that need the LSEs are formed, so it waits for one memory round
 // trip instead of one per split.
+//
+// Placement: the forward puts the splits of work item i (a (b, t) row group,
+// Hkv = 1) on XCD i % 8; when the item count and head count allow, the
+// workgroups merging item i's rows are dispatched to the same XCD (workgroup
+// w goes to XCD w % 8), whose L2 may still hold the partial rows just
+// written.
 template <typename T, int NS>
 __global__ __launch_bounds__(kThreads) void combine512_kernel(Params p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + wave;
-  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  const int64_t nitems = (int64_t)p.B * p.Sq;
+  int64_t row;
+  if (nitems % 8 == 0 && p.Hq % kWaves == 0) {
+    const int per = p.Hq / kWaves;  // workgroups per item
+    const int x = blockIdx.x % 8, r = blockIdx.x / 8;
+    row = ((int64_t)(r / per) * 8 + x) * p.Hq + (r % per) * kWaves + wave;
+  } else {
+    row = (int64_t)blockIdx.x * kWaves + wave;
+  }
+  const int64_t nrows = nitems * p.Hq;
   if (row >= nrows) return;
   const int h = row % p.Hq;
   const int t = (row / p.Hq) % p.Sq;
