@@ -130,3 +130,24 @@ def test_single_row_pages_and_padded_table():
     assert torch.equal(o_p, o_c)
     assert torch.equal(l_p, l_c)
 
+
+
+def test_paged_persistent_mla_prefill():
+    """MLA prefill at S = 4160 (>= 4096 work items: the persistent kernel,
+    which stages scaled pool offsets for its paged gathers) with 64-row
+    pages shuffled over the pool and a sink: bitwise equal to the contiguous
+    forward; sampled rows within the oracle's bars."""
+    _say("paged mla_prefill persistent S=4160 K=256 page=64 sink")
+    w = make_workload("mla_prefill", device=DEV, S=4160, K=256)
+    Hq = w.q.shape[2]
+    sink = torch.linspace(-1.0, 2.0, Hq, device=DEV)
+    kp, vp, bt = page_kv(w.k, w.v, 64, seed=5, spare_pages=3)
+    o_c, l_c = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, None, sink)
+    o_p, l_p = ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, None, sink)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_c)
+    assert torch.equal(l_p, l_c)
+    rows = torch.tensor([0, 1, 255, 1000, 2047, 2048, 4095, 4159])
+    k2, v2, i2 = paged_to_contiguous(kp.cpu(), vp.cpu(), bt.cpu(), w.idx[:, rows].cpu())
+    o_r, l_r = ref_forward(w.q[:, rows].cpu().float(), k2.float(), v2.float(), i2, w.scale, None, sink.cpu())
+    _check_oracle(o_p[:, rows], l_p[:, rows], o_r, l_r)
