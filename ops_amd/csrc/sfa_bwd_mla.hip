@@ -682,6 +682,7 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(Params p, i
                                                                      int W) {
   __shared__ uint32_t s_word[kRedItems];
   __shared__ uint16_t s_pre[kRedItems];
+  __shared__ int2 s_hits[kRedThreads / 64][8];  // per wave: queued hits (item, rank)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nw = (p.Skv + 31) / 32;
   const int wsel = (int)((blockIdx.x >> 1) % nw);
@@ -711,50 +712,60 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(Params p, i
     const uint32_t bit = 1u << kbit;
     float a0[8] = {}, a1[8] = {};
     bool any = false;
-    // items in batches of 64 (one per lane); the rows of the batch's hits are
-    // loaded 8 at a time, then added in item order
+    // Items in batches of 64 (one per lane).  A key has only a few hits per
+    // batch, so the hits are queued across batches (item and rank, in item
+    // order, in the wave's LDS list) and their rows are loaded U at a time,
+    // then added in item order: full rounds of loads in flight instead of
+    // one short round per batch.
+    constexpr int U = 8;
+    int2* q = s_hits[wave];
+    int nq = 0;  // queued hits (wave-uniform)
+    auto flush = [&](int n) {
+      u32x4 v0[U], v1[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u < n) {
+          const int2 h = q[u];
+          const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
+          v0[u] = row[lane];
+          v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= n) continue;
+        const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
+        const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a0[e] += (float)x0[e];
+          a1[e] += (float)x1[e];
+        }
+      }
+      any = true;
+    };
     for (int ib = 0; ib < nit; ib += 64) {
       const int i = ib + lane;
       const uint32_t word = i < nit ? s_word[i] : 0u;
       const int rank = i < nit ? (int)s_pre[i] + __builtin_popcount(word & (bit - 1u)) : 0;
       uint64_t hits = __ballot((word & bit) != 0u);
       while (hits) {
-        constexpr int U = 8;
-        int lis[U], rks[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          lis[u] = -1;
-          rks[u] = 0;
-          if (hits) {
-            const int l = __builtin_ctzll(hits);
-            hits &= hits - 1;
-            lis[u] = li0 + (ib + l) * p.Hkv;
-            rks[u] = __builtin_amdgcn_readlane(rank, l);
-          }
+        // queue up to U - nq of this batch's hits (lane order = item order)
+        const int take = min(__popcll(hits), U - nq);
+        const uint64_t below = ((1ull << lane) - 1ull);
+        const bool mine = ((hits >> lane) & 1ull) && __popcll(hits & below) < take;
+        if (mine) q[nq + __popcll(hits & below)] = int2{li0 + i * p.Hkv, rank};
+        for (int t = 0; t < take; ++t) hits &= hits - 1;
+        nq += take;
+        __builtin_amdgcn_wave_barrier();
+        if (nq == U) {
+          flush(U);
+          nq = 0;
+          __builtin_amdgcn_wave_barrier();
         }
-        u32x4 v0[U], v1[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (lis[u] >= 0) {
-            const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)lis[u] * p.topk + rks[u]) * 576);
-            v0[u] = row[lane];
-            v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (lis[u] < 0) continue;
-          const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
-          const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            a0[e] += (float)x0[e];
-            a1[e] += (float)x1[e];
-          }
-        }
-        any = true;
       }
     }
+    if (nq > 0) flush(nq);
     if (!any || key >= bound) return;
     float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
 #pragma unroll
