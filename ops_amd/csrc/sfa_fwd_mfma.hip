@@ -211,6 +211,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   bf16x8 qb[C::QREG > 0 ? C::QREG : 1];
   IdxStage<kIdxCap, C::kThreads> istage;
   int raw[RG::RPW];
+  int klen = 0;     // the item's kv_lens entry as loaded (0 without kv_lens); see item_bound
   int claim_c = 0;  // (thread 0) the pending claim's raw count
   // the gather source of an item: the (batch, kv head) slice's rows
   auto make_src = [&](const Params& p, const ItemPos& q) {
@@ -236,6 +237,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     if constexpr (PERSIST) {
       if (tid == 0) claim_c = claim_start(p.sched, blockIdx.x & 7);
     }
+    // (one work item per workgroup, e.g. a decode step with kv_lens) the key
+    // bound first, as a buffer load (no kv_lens: an empty range, which reads
+    // 0) whose value is only used at the staging: a load used at once makes
+    // the wave wait there for every load issued before it, the Q loads
+    // included, and used late it is waited for alone
+    if constexpr (!PERSIST)
+      klen = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p.kv_lens, p.kv_lens ? 4u * (uint32_t)p.B : 0u),
+                                                  4u * (uint32_t)q.b, 0, 0);
     const int32_t* irow = p.idx + q.b * p.i_sb + q.t * p.i_ss + q.g * p.i_sh + q.split * p.split_len;
     istage.load_buf(make_rsrc(irow, 4u * (uint32_t)q.nslots), tid);
 #pragma unroll
@@ -252,6 +261,11 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
       const i32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 2u * (uint32_t)(s * C::KD), 0, 0);
       qb[s] = __builtin_bit_cast(bf16x8, x);
     }
+  };
+  // the item's key bound: kv_lens[b] (at most Skv), or Skv without kv_lens
+  auto item_bound = [&](const Params& p, const ItemPos& q) {
+    if constexpr (PERSIST) return bound_of(p, q.b);
+    return p.kv_lens ? min(klen, p.Skv) : p.Skv;
   };
   // (1b) the LDS-resident steps of Q straight into s_q (buffer_load ... lds,
   // no VGPRs): head h's steps QREG.. are its dims [16 QREG, DQK), contiguous
@@ -285,7 +299,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
       s0.rs = s.rs;
       s0.row_bytes = s.row_bytes;
     }
-    const int bound = bound_of(p, q.b);
+    const int bound = item_bound(p, q);
     RG0 rg0;
 #pragma unroll
     for (int r = 0; r < RG::RPW; ++r)
@@ -304,7 +318,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
   int ipar = 0;  // parity of the current item
   auto item_stage = [&](const Params& p, const ItemPos& q, int tid, int wave, int lane, bool vm24) -> int {
     const int ntiles0 = (q.nslots + C::NKT - 1) / C::NKT;
-    const int bound = bound_of(p, q.b);
+    const int bound = item_bound(p, q);
     int used;
     if constexpr (PAGED)
       used = istage.store_pool_offsets(p, q.b, bound, q.nslots, ntiles0 * C::NKT, s_idx, tid);
