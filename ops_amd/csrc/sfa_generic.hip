@@ -364,11 +364,22 @@ __global__ __launch_bounds__(kThreads) void combine512_kernel(Params p) {
   const int h = row % p.Hq;
   const int t = (row / p.Hq) % p.Sq;
   const int b = row / ((int64_t)p.Hq * p.Sq);
-  const float ls = lane < NS ? p.part_lse[lane * nrows + row] : kNegInf;
-  const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
+  // The LSE and sink loads are buffer loads that read 0 out of range (lanes
+  // >= NS, no sink) and whose values are selected only after the row loads
+  // are issued: a conditional load or a value used at once makes the wave
+  // wait for it before issuing the rows, a second memory round trip.
+  const uint32_t lse_bytes = (uint32_t)((int64_t)NS * nrows * 4);
+  const float ls_raw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(p.part_lse, lse_bytes), lane < NS ? (uint32_t)((lane * nrows + row) * 4) : lse_bytes, 0, 0));
+  const float sink_raw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(p.sink, p.sink ? 4u * (uint32_t)p.Hq : 0u), 4u * (uint32_t)h, 0, 0));
   bf16x8 pv[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) pv[s] = *reinterpret_cast<const bf16x8*>(p.part_o + (s * nrows + row) * 512 + 8 * lane);
+  // (keeps the row loads ahead of the selects below)
+  __builtin_amdgcn_sched_barrier(0);
+  const float ls = lane < NS ? ls_raw : kNegInf;
+  const float sink2 = p.sink ? sink_raw * kLog2e : kNegInf;
   const float m = wave_max(ls);
   const float mm = fmaxf(m, sink2);
   const float e = (ls == kNegInf || mm == kNegInf) ? 0.f : exp2f(ls - mm);

@@ -494,3 +494,17 @@ def test_mla_shared_kv_backward_autograd():
     assert _rel_l2(q.grad.float().cpu(), dq) <= GRAD_RL2
     assert _rel_l2(kv.grad.float().cpu(), dkv) <= GRAD_RL2
     assert _rel_l2(sink.grad.cpu(), ds) <= GRAD_RL2
+
+
+@pytest.mark.parametrize("splits", [2, 4, 8])
+def test_mla_decode_splits_sink(splits):
+    """The d_v = 512 split merge (2, 4 or 8 splits) with an attention sink and
+    per-sequence kv_lens, against the oracle."""
+    _say(f"mla_decode bf16 B=4 Skv=2048 Hq=128 K=512 num_splits={splits} sink")
+    w = make_workload("mla_decode", device=DEV, B=4, Skv=2048, K=512, ctx_lo=300)
+    sink = torch.linspace(-1.0, 2.0, w.q.shape[2], device=DEV)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens, attn_sink=sink,
+                                   num_splits=splits)
+    o_ref, l_ref = ref_forward(w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), w.scale, kv_lens=w.kv_lens.cpu(),
+                               sink=sink.cpu())
+    _check_fwd(out, lse, o_ref, l_ref)
