@@ -70,6 +70,8 @@ int check_pages(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
                 pg->max_pages);
   if ((int64_t)a->Skv > (int64_t)pg->max_pages * pg->page_size)
     return fail(SFA_E_INVALID, "Skv %d exceeds max_pages * page_size", a->Skv);
+  if (4 * ((int64_t)(a->B - 1) * pg->bt_sb + pg->max_pages) >= ((int64_t)1 << 32))
+    return fail(SFA_E_INVALID, "block table spans 4 GiB or more");
   return SFA_OK;
 }
 

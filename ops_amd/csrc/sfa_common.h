@@ -133,6 +133,37 @@ __device__ __forceinline__ int staged_pool_off(const Params& p, int b, int id, i
   return (int)(pool_row_offset((uint32_t)r, p.page_shift, (uint64_t)(2 * p.k_sb), (uint32_t)(2 * p.k_ss)) >> p.pool_shift);
 }
 
+// paged_row() of N slots at once: the N block-table loads are issued before
+// any of them is used (buffer loads over the table's rows up to the last page
+// any valid key can use; invalid slots read out of range, i.e. 0, and are
+// dropped), so they cost one memory round trip, not N.  OFFS: return
+// staged_pool_off() values instead of pool rows.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes);
+template <int N, bool OFFS>
+__device__ __forceinline__ void paged_rows(const Params& p, int b, const int (&id)[N], int bound, int (&out)[N]) {
+  const int64_t pages = ((int64_t)p.Skv + (1 << p.page_shift) - 1) >> p.page_shift;
+  const uint32_t tbytes = (uint32_t)(4 * ((int64_t)(p.B - 1) * p.bt_sb + pages));
+  const __amdgpu_buffer_rsrc_t rt = make_rsrc(p.block_table, tbytes);
+  int pg[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const bool ok = id[i] >= 0 && id[i] < bound;
+    const uint32_t off = ok ? 4u * (uint32_t)((int64_t)b * p.bt_sb + (id[i] >> p.page_shift)) : tbytes;
+    pg[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(rt, off, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const bool ok = id[i] >= 0 && id[i] < bound && pg[i] >= 0 && pg[i] < p.num_pages;
+    const int r = (pg[i] << p.page_shift) | (id[i] & ((1 << p.page_shift) - 1));
+    if constexpr (OFFS)
+      out[i] = ok ? (int)(pool_row_offset((uint32_t)r, p.page_shift, (uint64_t)(2 * p.k_sb), (uint32_t)(2 * p.k_ss)) >>
+                          p.pool_shift)
+                  : -1;
+    else
+      out[i] = ok ? r : -1;
+  }
+}
+
 // Index row of a work item, in two phases so that its global loads are in
 // flight together with whatever the caller issues in between (a loop that
 // stores each value to LDS as it arrives compiles to one memory round trip
@@ -164,8 +195,15 @@ struct IdxStage {
   __device__ __forceinline__ int store(const Params& p, int b, int bound, int nslots, int nstage, int* s_idx,
                                        int tid) {
     int st[IPT];
+    if constexpr (PAGED) {
+      int id[IPT];
 #pragma unroll
-    for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_id<PAGED>(p, b, v[j], bound) : -1;
+      for (int j = 0; j < IPT; ++j) id[j] = tid + j * THREADS < nslots ? v[j] : -1;
+      paged_rows<IPT, false>(p, b, id, bound, st);
+    } else {
+#pragma unroll
+      for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_id<false>(p, b, v[j], bound) : -1;
+    }
     int used = 0;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
@@ -178,9 +216,10 @@ struct IdxStage {
   // (staged_pool_off)
   __device__ __forceinline__ int store_pool_offsets(const Params& p, int b, int bound, int nslots, int nstage,
                                                     int* s_idx, int tid) {
-    int st[IPT];
+    int st[IPT], id[IPT];
 #pragma unroll
-    for (int j = 0; j < IPT; ++j) st[j] = tid + j * THREADS < nslots ? staged_pool_off(p, b, v[j], bound) : -1;
+    for (int j = 0; j < IPT; ++j) id[j] = tid + j * THREADS < nslots ? v[j] : -1;
+    paged_rows<IPT, true>(p, b, id, bound, st);
     int used = 0;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {

@@ -301,12 +301,19 @@ __global__ __launch_bounds__(C::kThreads, 1) void fwd_mfma_kernel(Params p_arg) 
     }
     const int bound = item_bound(p, q);
     RG0 rg0;
+    if constexpr (PAGED) {
+      // (all 8 block-table loads in flight together)
+      int id[RG::RPW], st[RG::RPW];
 #pragma unroll
-    for (int r = 0; r < RG::RPW; ++r)
-      rg0.set_row(r, (wave * RG::RPW + r < q.nslots) ? (PAGED ? staged_pool_off(p, q.b, raw[r], bound)
-                                                              : staged_id<false>(p, q.b, raw[r], bound))
-                                                    : -1,
-                  true, s0);
+      for (int r = 0; r < RG::RPW; ++r) id[r] = wave * RG::RPW + r < q.nslots ? raw[r] : -1;
+      paged_rows<RG::RPW, true>(p, q.b, id, bound, st);
+#pragma unroll
+      for (int r = 0; r < RG::RPW; ++r) rg0.set_row(r, st[r], true, s0);
+    } else {
+#pragma unroll
+      for (int r = 0; r < RG::RPW; ++r)
+        rg0.set_row(r, (wave * RG::RPW + r < q.nslots) ? staged_id<false>(p, q.b, raw[r], bound) : -1, true, s0);
+    }
 #pragma unroll
     for (int k = 0; k < RG::NI; ++k) rg0.issue(k, s0, s_k0, wave, lane);
   };
