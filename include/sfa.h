@@ -128,7 +128,9 @@ typedef struct sfa_bwd_args {
  * [0, num_pages); an unmapped page (e.g. -1) makes the slot invalid. */
 typedef struct sfa_kv_pages {
   const int32_t* block_table;    /* [B, max_pages] int32 page ids                     */
-  int64_t bt_sb;                 /* block-table row stride (elements)                 */
+  int64_t bt_sb;                 /* block-table row stride (elements); the table's
+                                    extent, ((B - 1) * bt_sb + max_pages) * 4 bytes,
+                                    must stay below 4 GiB                            */
   int32_t max_pages;             /* block-table columns                               */
   int32_t page_size;             /* rows per page, a power of two                     */
   int32_t num_pages;             /* pages in each pool; num_pages * page_size < 2^31  */
