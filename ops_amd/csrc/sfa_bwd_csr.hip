@@ -312,8 +312,15 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p_arg) {
   // compiler, and every address derived from it would be built per lane)
   const int u = __builtin_amdgcn_readfirstlane(s_unit[par]);
   if (u < 0) break;
-  if (tid == 0) s_unit[par ^ 1] = claim(p);
-  par ^= 1;
+  // the successor's claim: the atomic goes out now and its result is read at
+  // the end of the unit (waiting for it here would also wait for this
+  // workgroup's partial stores of the previous unit, still in flight)
+  int claim_i = 0;
+  if (tid == 0) {
+    int o = 0;
+    asm volatile("" : "+v"(o));
+    claim_i = atomicAdd(p.kctr + o, 1);
+  }
   const int c = p.max_chunks - 1 - u / per_chunk;
   const int kb = (u % per_chunk) / nbg;
   const int bg = (u % per_chunk) % nbg;
@@ -324,6 +331,8 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p_arg) {
   const int e0 = __builtin_amdgcn_readfirstlane(start[c]);
   const int nblk = __builtin_amdgcn_readfirstlane(start[c + 1]) - e0;
   if (nblk <= 0) {  // no query block of this chunk selects the key block
+    if (tid == 0) s_unit[par ^ 1] = claim_i < p.kctr[1] ? p.uorder[claim_i] : -1;
+    par ^= 1;
     __syncthreads();
     continue;
   }
@@ -634,6 +643,8 @@ __global__ __launch_bounds__(256, 1) void dkv_keymajor_kernel(Params p_arg) {
       *reinterpret_cast<f32x4*>(part + kD + dim) = v4;
     }
   }
+  if (tid == 0) s_unit[par ^ 1] = claim_i < p.kctr[1] ? p.uorder[claim_i] : -1;
+  par ^= 1;
   __syncthreads();  // the next unit's list and blocks overwrite the LDS; its claim is published
   }  // units
 }
