@@ -347,13 +347,23 @@ __global__ __launch_bounds__(256) void mla_map_kernel(Params p, int64_t item0, i
   for (int w = lane; w < W; w += 64) map[w] = 0u;
   __builtin_amdgcn_wave_barrier();
   uint8_t* drow = dup + (int64_t)li * p.topk;
-  for (int s0 = 0; s0 < p.topk; s0 += 64) {
-    const int s = s0 + lane;
-    const int id = s < p.topk ? irow[s] : -1;
+  // the lane's slots s = 64 j + lane are loaded first, all in flight together
+  // (buffer loads over the row's topk ids: slots past it read 0 and are
+  // dropped by the slot test below; a load used where it is issued would
+  // cost one memory round trip per 64 slots)
+  constexpr int J = kMIdxCap / 64;
+  const __amdgpu_buffer_rsrc_t rrow = make_rsrc(irow, 4u * (uint32_t)p.topk);
+  int ids[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) ids[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(rrow, 4u * (uint32_t)(64 * j + lane), 0, 0);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int s = 64 * j + lane;
+    const int id = ids[j];
     // exactly one slot of each distinct key finds its bit clear (the first
     // atomicOr to set it); every other slot of that key is a repeat
     uint8_t rep = 0;
-    if (id >= 0 && id < bound) {
+    if (s < p.topk && id >= 0 && id < bound) {
       const uint32_t bit = 1u << (id & 31);
       rep = (atomicOr(&map[id >> 5], bit) & bit) ? 1 : 0;
     }
