@@ -507,6 +507,10 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
     uint32_t words[IPT];
     int pre[IPT];
     uint8_t rep[IPT];
+    // the repeat flags by buffer loads (slots >= nslots read 0): a load under
+    // the slot test would be waited for where it is issued, one memory round
+    // trip per j
+    const __amdgpu_buffer_rsrc_t rdup = make_rsrc(drow, (uint32_t)nslots);
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int sl = tid + j * kMThreads;
@@ -517,7 +521,7 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
       const int id = ids[j] >= 0 ? ids[j] : 0;
       words[j] = mrow[id >> 5];
       pre[j] = prow[id >> 5];
-      rep[j] = (tid + j * kMThreads < nslots) ? drow[tid + j * kMThreads] : 0;
+      rep[j] = __builtin_amdgcn_raw_buffer_load_b8(rdup, (uint32_t)(tid + j * kMThreads), 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
