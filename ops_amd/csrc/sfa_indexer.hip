@@ -112,6 +112,7 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   // 16 s + 8 (l / 32) .. + 7, fp8: dims 64 s + 32 (l / 32) .. + 31) and weights
   const int hl = lane & 31, lg = lane >> 5;
   op_t qa[4][O::kSteps];
+  float wv[4];  // weights of heads 32 hg + hl (both lane halves load them)
   int tq[QPW];
   bool qok[QPW];
 #pragma unroll
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
       }
     }
     const float* wrow = p.w + b * p.w_sb + t * p.w_ss + hg * 32;
-    if (lg == 0) s_w[(wave * 4 + mt) * 32 + hl] = wrow[hl];
+    wv[mt] = wrow[hl];
   }
   // weight of accumulator element e of M-tile mt: head 8 (e / 4) + 4 lg + e % 4
   // of the tile, read as 4 consecutive floats per group of 4 elements
@@ -247,6 +248,12 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   };
 
   if (ntiles > 0) load_tile(0, s_k0);
+  // the weights go to LDS once tile 0 is in flight (a load under the lane
+  // test would be waited for where issued, before the tile's DMA)
+  if (lg == 0) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) s_w[(wave * 4 + mt) * 32 + hl] = wv[mt];
+  }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();                     // tile 0 and the weights are in place
   for (int kt = 0; kt < ntiles; kt += 2) {
