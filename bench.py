@@ -35,6 +35,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -341,8 +342,11 @@ def bench_mla_decode(args):
     times, _ = time_steps(fn, args.steps * 4, args.warmup, before=flush)
     us = sum(times) / len(times) * 1e3
     gbs = nbytes / (us * 1e-6) / 1e9
+    # "us" is the mean over the timed steps; the median and the slowest step
+    # beside it show whether one stalled step moved the mean
     res = {"metric": "decode GB/s (algorithmic bytes, cache flushed)", "value": gbs, "unit": "GB/s", "us": us,
-           "bytes": nbytes, "frac_of_peak": gbs / PEAK_HBM_GBS, "tflops": fwd_flops(w, pairs) / (us * 1e-6) / 1e12,
+           "us_median": statistics.median(times) * 1e3, "us_max": max(times) * 1e3, "bytes": nbytes,
+           "frac_of_peak": gbs / PEAK_HBM_GBS, "tflops": fwd_flops(w, pairs) / (us * 1e-6) / 1e12,
            "config": {"B": 64, "Skv": 65536, "Hq": 128, "d_qk": 576, "d_v": 512, "topk": 2048}}
     # the same step over a paged cache (block table of 64-row pages)
     from ops_amd.workloads import page_kv
@@ -351,7 +355,8 @@ def bench_mla_decode(args):
     fnp = lambda: ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
     times, _ = time_steps(fnp, args.steps * 4, args.warmup, before=flush)
     pus = sum(times) / len(times) * 1e3
-    res["paged"] = {"value": pbytes / (pus * 1e-6) / 1e9, "unit": "GB/s", "us": pus, "bytes": pbytes,
+    res["paged"] = {"value": pbytes / (pus * 1e-6) / 1e9, "unit": "GB/s", "us": pus,
+                    "us_median": statistics.median(times) * 1e3, "us_max": max(times) * 1e3, "bytes": pbytes,
                     "frac_of_peak": pbytes / (pus * 1e-6) / 1e9 / PEAK_HBM_GBS, "page_size": 64,
                     "pool_bytes": kp.numel() * kp.element_size()}
     del kp, vp
