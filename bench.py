@@ -194,6 +194,12 @@ def cpu_fwd_bwd(w, rows=None, bwd=True):
     return t_fwd, t_bwd, pairs
 
 
+# per-workload CPU rates wait until every GPU timing is done: the oracle's
+# threads busy the host cores, and a launching thread that loses its core
+# for a few ms in a timed step moves a short step's mean (the decode step)
+_CPU_PENDING = []
+
+
 def cpu_rate(name, w):
     """CPU (oracle, PyTorch eager fp32) rate of workload ``name`` on this
     host's cores: full runs where they take seconds, a bounded sample of query
@@ -266,7 +272,7 @@ def bench_tiny(args):
            ((fms + bms) * 1e-3) / 1e12, "unit": "TFLOP/s", "fwd_ms": fms, "bwd_ms": bms, "valid_pairs": pairs,
            "dtype": "f32", "config": {"B": 1, "S": 256, "Hq": 4, "Hkv": 1, "d": 64, "topk": 64}}
     if not args.no_cpu:
-        res["cpu"] = cpu_rate("tiny", w)
+        _CPU_PENDING.append((res, "tiny", w))
     return res
 
 
@@ -283,7 +289,7 @@ def bench_prefill(args):
            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
            "config": {"B": 1, "S": 4096, "Hq": 16, "Hkv": 1, "d": 128, "topk": 512}}
     if not args.no_cpu:
-        res["cpu"] = cpu_rate("prefill", w)
+        _CPU_PENDING.append((res, "prefill", w))
     return res
 
 
@@ -313,7 +319,7 @@ def bench_train_gqa(args):
         res["bwd"]["note"] = ("TFLOP/s over valid pairs (pairs * G * 2 (3 d_qk + 2 d_v)); 'csr' = deterministic "
                               "dK/dV (the default), 'atomic' = fp32 atomics")
     if not args.no_cpu:
-        res["cpu"] = cpu_rate("train_gqa", w)
+        _CPU_PENDING.append((res, "train_gqa", w))
     return res
 
 
@@ -361,7 +367,7 @@ def bench_mla_decode(args):
                     "pool_bytes": kp.numel() * kp.element_size()}
     del kp, vp
     if not args.no_cpu:
-        res["cpu"] = cpu_rate("mla_decode", w)
+        _CPU_PENDING.append((res, "mla_decode", w))
     return res
 
 
@@ -744,6 +750,9 @@ def main():
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
+        for res, name, wl in _CPU_PENDING:
+            res["cpu"] = cpu_rate(name, wl)
+        _CPU_PENDING.clear()
         log("cpu baseline (oracle) on a bounded sample")
         cpu = cpu_baseline_mla(w, args.cpu_seconds)
         cpu["cpu_model"] = cpu_model()
