@@ -218,8 +218,15 @@ SFA_API size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a);
 SFA_API int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace sfa_bwd needs for `a` (fp32 dK/dV accumulators,
- * delta, the CSR arrays in SFA_DKV_CSR mode, and for the MLA backward the
- * bf16 P / dS of a chunk of about 512 MiB of queries).
+ * delta, the CSR arrays in SFA_DKV_CSR mode).  The MLA backward
+ * (SFA_BWD_MERGE_KV at its shape) needs fp32 accumulators of the shared rows
+ * (B * Skv * Hkv * Dqk * 4 bytes), delta (B * Sq * Hq * 4 bytes) and one
+ * chunk of queries: per query the bf16 P / dS of its slots (about 1 MiB at
+ * top-k 2048, G = 128) and, in the deterministic mode, its per-slot bf16
+ * gradient rows (top-k * Dqk * 2 bytes) and index maps; a chunk stays within
+ * 2 GiB (whole rounds of 256 queries when that many fit, else multiples of 8,
+ * at least 8 queries), so the total is about 2 GiB plus the accumulators at
+ * the full-size shapes.
  * Replaces the workspaces of SFA.py:184-194 and SFA.py:253-261. */
 SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
 

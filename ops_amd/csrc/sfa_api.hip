@@ -447,12 +447,13 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
     void* pd = (char*)p.delta + align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
     p.dsink = a->dsink;
     p.dlse = a->dlse;
-    hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
-    if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
-    if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
+    // (refused before any device work is queued)
     const bool det = mla_det(a, p);
     if (a->dkv_mode == SFA_DKV_CSR && !det)
       return fail(SFA_E_UNSUPPORTED, "the deterministic MLA backward supports Skv <= 65536 (got %d)", f.Skv);
+    hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
     const int64_t items = (int64_t)f.B * f.Sq * f.Hkv;
     const int chunk = mla_chunk_items(p, det);
     for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk)

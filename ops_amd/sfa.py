@@ -215,10 +215,26 @@ def _is_prefix_view(k: torch.Tensor, v: torch.Tensor) -> bool:
             and v.shape[:3] == k.shape[:3] and v.shape[3] <= k.shape[3] and v.stride(-1) == k.stride(-1))
 
 
+def _merge_in_autograd(k: torch.Tensor, v: torch.Tensor, needs_k: bool, needs_v: bool) -> bool:
+    """Whether the backward may return dK + dV as k's gradient and None for v.
+
+    That is exact only when autograd itself would add v's gradient into the
+    rows of k: v is k, or a view of k (or of k's own base) that autograd
+    tracks, its memory is the first Dv dims of k's rows, and both inputs
+    want a gradient.  An alias that autograd does not see (a detached view,
+    a second leaf over the same storage) shares memory but not gradients."""
+    if not (needs_k and needs_v and _is_prefix_view(k, v)):
+        return False
+    return v is k or v._base is k or (v._base is not None and v._base is k._base)
+
+
 def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None, attn_sink=None,
-                 dlse: Optional[torch.Tensor] = None, dkv_mode: Optional[str] = None, merge_kv: bool = False):
+                 dlse: Optional[torch.Tensor] = None, dkv_mode: Optional[str] = None, merge_kv: bool = False,
+                 dq: Optional[torch.Tensor] = None, dk: Optional[torch.Tensor] = None,
+                 dv: Optional[torch.Tensor] = None):
     """Backward only (no autograd): ``(dq, dk, dv, dsink)``; ``dsink`` is None
-    without a sink.
+    without a sink.  ``dq`` / ``dk`` / ``dv`` may be preallocated (q's / k's
+    / v's shape and dtype, unit feature stride); they are fully overwritten.
 
     ``merge_kv=True`` (``v`` must be the first ``Dv`` dims of ``k``'s rows,
     e.g. MLA's ``kv[..., :512]``): ``dk`` is the gradient of the shared rows,
@@ -247,9 +263,16 @@ def sfa_backward(q, k, v, topk_idxs, out, lse, dout, sm_scale=None, kv_lens=None
     mode = dkv_mode or os.environ.get("SFA_DKV_MODE", "auto")
     if mode not in _DKV_MODES:
         raise ValueError(f"dkv_mode must be one of {sorted(_DKV_MODES)}")
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = torch.empty((B, Skv, Hkv, Dqk), dtype=q.dtype, device=q.device)
-    dv = None if merge_kv else torch.empty((B, Skv, Hkv, Dv), dtype=q.dtype, device=q.device)
+    def _out(t, shape, name):
+        if t is None:
+            return torch.empty(shape, dtype=q.dtype, device=q.device)
+        if tuple(t.shape) != shape or t.dtype != q.dtype or t.device != q.device or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be a {list(shape)} {q.dtype} tensor on {q.device} with a unit feature stride")
+        return t
+
+    dq = _out(dq, (B, Sq, Hq, Dqk), "dq")
+    dk = _out(dk, (B, Skv, Hkv, Dqk), "dk")
+    dv = None if merge_kv else _out(dv, (B, Skv, Hkv, Dv), "dv")
     dsink = torch.empty((Hq,), dtype=torch.float32, device=q.device) if sink is not None else None
     if dlse is not None:
         dlse = dlse.to(torch.float32).contiguous()
@@ -286,6 +309,8 @@ class SparseFlashAttention(torch.autograd.Function):
         out, lse = sfa_forward(q, k, v, topk_idxs, sm_scale, kv_lens, attn_sink)
         ctx.save_for_backward(q, k, v, topk_idxs, out, lse, kv_lens, attn_sink)
         ctx.sm_scale = sm_scale
+        # decided here, where the inputs' autograd identity is still known
+        ctx.merge_kv = _merge_in_autograd(k, v, ctx.needs_input_grad[1], ctx.needs_input_grad[2])
         ctx.mark_non_differentiable()
         ctx.set_materialize_grads(False)
         return out, lse
@@ -295,11 +320,11 @@ class SparseFlashAttention(torch.autograd.Function):
         q, k, v, idx, out, lse, kv_lens, sink = ctx.saved_tensors
         if grad_out is None:
             grad_out = torch.zeros_like(out)
-        # v a prefix view of k (MLA's shared kv): the merged gradient of the
-        # shared rows goes to k, nothing to v (autograd sums both into the
-        # same storage anyway)
+        # v an autograd view of k's first Dv dims (MLA's shared kv): the
+        # merged gradient of the shared rows goes to k, nothing to v (autograd
+        # would add v's gradient into the same rows of k)
         dq, dk, dv, dsink = sfa_backward(q, k, v, idx, out, lse, grad_out, ctx.sm_scale, kv_lens, sink,
-                                         dlse=grad_lse, merge_kv=_is_prefix_view(k, v))
+                                         dlse=grad_lse, merge_kv=ctx.merge_kv)
         if dsink is not None and sink is not None:
             dsink = dsink.to(sink.dtype)
         return dq, dk, dv, None, None, None, dsink

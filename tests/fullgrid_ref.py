@@ -148,3 +148,45 @@ def rowwise_rel_err(a: torch.Tensor, ref: torch.Tensor, floor: float = 1e-3) -> 
     keep = rn > floor * rn.median().clamp_min(1e-30)
     err = (a - ref).norm(dim=1)[keep] / rn[keep]
     return float(err.max()) if err.numel() else 0.0
+
+
+def key_grads(q, k, v, idx, out, lse, dout, scale, keys, b: int = 0, g: int = 0, kv_lens=None, dlse=None,
+              chunk: int = 512):
+    """``(dk, dv)`` float32 ``[len(keys), Dqk]`` / ``[len(keys), Dv]``: the
+    gradients of key rows ``keys`` of batch ``b``, KV head ``g``, summed over
+    every (query, slot) pair that references them (SFA.py:831-853), each pair
+    with its own query's P and dS from ``lse`` and ``delta = Σ out·dout -
+    dlse``.  This checks a key's gradient at full workload sizes without the
+    whole backward: only the queries that select the key are visited."""
+    Sq, Hq, Dqk = q.shape[1], q.shape[2], q.shape[3]
+    Skv, Hkv, Dv = k.shape[1], k.shape[2], v.shape[3]
+    G = Hq // Hkv
+    dev = q.device
+    hs = slice(g * G, (g + 1) * G)
+    bound = int(_bounds(q.shape[0], Skv, kv_lens, dev)[b])
+    ib = idx[b, :, g].long()
+    vm = (ib >= 0) & (ib < bound)
+    dk = torch.zeros(len(keys), Dqk, dtype=torch.float32, device=dev)
+    dv = torch.zeros(len(keys), Dv, dtype=torch.float32, device=dev)
+    for n, j in enumerate(keys):
+        j = int(j)
+        if not 0 <= j < bound:
+            continue
+        ts = ((ib == j) & vm).nonzero(as_tuple=True)[0]  # one entry per referencing slot
+        kj = k[b, j, g].float()
+        vj = v[b, j, g].float()
+        for c0 in range(0, ts.numel(), chunk):
+            t = ts[c0:c0 + chunk]
+            qg = q[b, t][:, hs].float()                           # [n, G, Dqk]
+            dog = dout[b, t][:, hs].float()                       # [n, G, Dv]
+            lg = lse[b, t][:, hs].float()
+            delta = (out[b, t][:, hs].float() * dog).sum(-1)
+            if dlse is not None:
+                delta = delta - dlse[b, t][:, hs].float()
+            lfin = torch.where(torch.isfinite(lg), lg, torch.zeros_like(lg))
+            p = torch.exp(qg @ kj * scale - lfin)
+            p = torch.where(torch.isfinite(lg), p, torch.zeros_like(p))
+            ds = p * (dog @ vj - delta)
+            dk[n] += scale * (ds[..., None] * qg).sum((0, 1))
+            dv[n] += (p[..., None] * dog).sum((0, 1))
+    return dk, dv

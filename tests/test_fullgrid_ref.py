@@ -68,3 +68,28 @@ def test_rowwise_error_flags_an_unwritten_row():
     assert fr.rowwise_rel_err(a, ref) < 1e-3
     a[13, 2] = 0
     assert fr.rowwise_rel_err(a, ref) > 0.99
+
+
+def test_key_grads_match_the_full_backward():
+    """The per-key gradient helper against the full backward's rows (which
+    the test above pins to the oracle), for referenced, unreferenced,
+    out-of-range and past-kv_lens keys, with a gradient into LSE."""
+    q, k, v, dout, idx, kv_lens, sink = _inputs(4)
+    scale = 0.3
+    o, l = sfa_forward(q, k, v, idx, scale, kv_lens=kv_lens, sink=sink)
+    dlse = torch.randn(l.shape, generator=torch.Generator().manual_seed(9))
+    _, rk, rv, _ = fr.backward(q, k, v, idx, o, l, dout, scale, kv_lens, sink, dlse=dlse)
+    keys = [0, 3, 20, 21, 32, 40]
+    for b in range(2):
+        for g in range(2):
+            dk, dv = fr.key_grads(q, k, v, idx, o, l, dout, scale, keys, b=b, g=g, kv_lens=kv_lens, dlse=dlse,
+                                  chunk=3)
+            for n, j in enumerate(keys):
+                if j < 33:
+                    assert float((dk[n] - rk[b, j, g]).abs().max()) < 1e-4, (b, g, j)
+                    assert float((dv[n] - rv[b, j, g]).abs().max()) < 1e-4, (b, g, j)
+                else:
+                    assert bool((dk[n] == 0).all() and (dv[n] == 0).all())
+    # a planted mistake (delta without the LSE gradient) is caught
+    dk_bad, _ = fr.key_grads(q, k, v, idx, o, l, dout, scale, [3], b=0, g=0, kv_lens=kv_lens)
+    assert float((dk_bad[0] - rk[0, 3, 0]).abs().max()) > 1e-3

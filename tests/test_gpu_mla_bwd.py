@@ -167,3 +167,46 @@ def test_mla_bwd_separate_dk_dv_generic():
     merged[..., :512] += dv_s.float()
     assert _rel_l2(dq_m.float(), dq_s.float()) <= GRAD_RL2
     assert _rel_l2(dkv_m.float(), merged) <= GRAD_RL2
+
+
+def test_autograd_merges_only_views_autograd_tracks():
+    """The autograd Function returns dK + dV as k's gradient only when v is
+    a view of k that autograd tracks.  An alias autograd does not see (a
+    detached prefix view, or a view of a second leaf over the same storage)
+    shares memory but not gradients: k then gets dK alone and v's own leaf
+    dV (the unmerged path), against the CPU oracle."""
+    _say("MLA autograd: detached / second-leaf aliases of v vs an autograd view")
+    w = _inputs(1, 48, 128, 24, seed=13)
+    qc, kc = w.q.float().cpu(), w.k.float().cpu()
+    out_ref, lse_ref = ref_forward(qc, kc, kc[..., :512], w.idx.cpu(), w.scale)
+    rdq, rdk, rdv, _ = ref_backward(qc, kc, kc[..., :512], w.idx.cpu(), out_ref, lse_ref, w.dout.float().cpu(),
+                                    w.scale)
+    merged = rdk.clone()
+    merged[..., :512] += rdv
+
+    def run(make_v):
+        q = w.q.clone().requires_grad_(True)
+        kv = w.k.clone().requires_grad_(True)
+        v, v_leaf = make_v(kv)
+        out, _ = ops_amd.sparse_flash_attention(q, kv, v, w.idx, w.scale)
+        (out.float() * w.dout.float()).sum().backward()
+        torch.cuda.synchronize()
+        return q.grad, kv.grad, (v_leaf.grad if v_leaf is not None else None)
+
+    # an autograd view: k's gradient is dK + dV
+    dq, dkv, _ = run(lambda kv: (kv[..., :512], None))
+    assert _rel_l2(dq.float().cpu(), rdq) <= GRAD_RL2
+    assert _rel_l2(dkv.float().cpu(), merged) <= GRAD_RL2
+    # a detached alias: dK alone
+    dq, dk, _ = run(lambda kv: (kv[..., :512].detach(), None))
+    assert _rel_l2(dq.float().cpu(), rdq) <= GRAD_RL2
+    assert _rel_l2(dk.float().cpu(), rdk) <= GRAD_RL2
+    # a view of a second leaf over the same storage: dK to k, dV to that leaf
+    def second_leaf(kv):
+        other = kv.detach().requires_grad_(True)
+        return other[..., :512], other
+
+    dq, dk, dother = run(second_leaf)
+    assert _rel_l2(dk.float().cpu(), rdk) <= GRAD_RL2
+    assert dother is not None and _rel_l2(dother[..., :512].float().cpu(), rdv) <= GRAD_RL2
+    assert bool((dother[..., 512:] == 0).all())

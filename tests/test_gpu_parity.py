@@ -440,20 +440,26 @@ def test_autograd_function_and_dlse():
         assert _rel_l2(a.grad.cpu(), b.grad) <= GRAD_RL2
 
 
-def test_reference_signature_shim():
+@pytest.mark.parametrize("H,D,dtypes", [(16, 128, (torch.float32, torch.bfloat16)), (64, 128, (torch.bfloat16,)),
+                                         (32, 576, (torch.bfloat16,))])
+def test_reference_signature_shim(H, D, dtypes):
     """SparseFlashAttentionTriton.apply(q[S,B,H,D], kv[S_kv,B,D], sink[H],
     idx[S,B,K], scale) -> out, with grads (q, kv, sink), against the oracle
-    (K = V = kv, one KV head)."""
-    _say("reference-signature SBHD shim, bf16 and fp32")
-    for dtype in (torch.float32, torch.bfloat16):
-        g = torch.Generator(device=DEV).manual_seed(11)
-        S, B, H, D, K = 96, 2, 16, 128, 48
+    (K = V = the whole kv row, one KV head, so out is D wide as
+    torch.empty_like(q) makes it, SFA.py:104, 456), at the reference's own
+    head tiling (BLOCK_H = 32 and multiples, SFA.py:35-48) and at the MLA
+    row width D = 576."""
+    _say(f"reference-signature SBHD shim H={H} D={D} {[str(d) for d in dtypes]}")
+    for dtype in dtypes:
+        g = torch.Generator(device=DEV).manual_seed(11 + H + D)
+        S, B, K = 96, 2, 48
         q = torch.randn(S, B, H, D, device=DEV, generator=g).to(dtype).requires_grad_(True)
         kv = torch.randn(S, B, D, device=DEV, generator=g).to(dtype).requires_grad_(True)
         sink = torch.randn(H, device=DEV, generator=g).requires_grad_(True)
         idx = torch.randint(-1, S, (S, B, K), device=DEV, generator=g, dtype=torch.int32)
         dout = torch.randn(S, B, H, D, device=DEV, generator=g).to(dtype)
         out = ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, 0.1)
+        assert tuple(out.shape) == (S, B, H, D)
         out.backward(dout)
         qb = q.detach().permute(1, 0, 2, 3).cpu()
         kb = kv.detach().permute(1, 0, 2).unsqueeze(2).cpu()
