@@ -23,6 +23,8 @@ measured in the same run and reported under ``workloads``:
 * ``mla_bwd``     shared-KV (MLA) backward at the full prefill shape (S=32768,
                   128 heads, d_qk 576 / d_v 512, top-k 2048; TFLOP/s over valid
                   pairs): dQ and the merged dK + dV of the shared rows
+* ``shim``        the reference's own signature (SBHD q, one shared kv, sink):
+                  S=4096, H=64, D=128, top-k 2048, fwd and bwd
 
 Inputs are resident in HBM before timing.  Timing uses HIP events on the
 stream the kernels run on (torch's current stream).  ``cpu_baseline`` times
@@ -381,13 +383,65 @@ def bench_mla_bwd(args):
     w = make_workload("mla_prefill", device="cuda", with_dout=True)
     pairs = valid_pairs(w)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
-    fn = lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True)
-    bt, _ = time_steps(fn, max(2, args.steps // 4), 1)
-    ms = sum(bt) / len(bt)
-    tf = bwd_flops(w, pairs) / (ms * 1e-3) / 1e12
-    return {"metric": "bwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
-            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "kernels": "mla_map_kernel + mla_bwd_dq_kernel + mla_bwd_dkv_kernel<true> + mla_bwd_reduce_kernel (deterministic: per-slot bf16 rows summed per key in slot order)",
-            "config": {"B": 1, "S": 32768, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
+    res = {"metric": "bwd effective TFLOP/s", "valid_pairs": pairs, "unit": "TFLOP/s",
+           "config": {"B": 1, "S": 32768, "Hq": 128, "Hkv": 1, "d_qk": 576, "d_v": 512, "topk": 2048}}
+    for mode in ("auto", "atomic"):
+        fn = lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True,
+                                          dkv_mode=mode)
+        bt, _ = time_steps(fn, max(2, args.steps // 4), 1)
+        ms = sum(bt) / len(bt)
+        tf = bwd_flops(w, pairs) / (ms * 1e-3) / 1e12
+        if mode == "auto":
+            res.update({"value": tf, "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+                        "kernels": "mla_map_kernel + mla_bwd_dq_kernel + mla_bwd_dkv_kernel<true> + "
+                                   "mla_bwd_reduce_kernel (deterministic: per-slot bf16 rows summed per key "
+                                   "in query order)"})
+        else:
+            res["atomic"] = {"value": tf, "ms": ms, "frac_of_peak": tf / PEAK_BF16_TFLOPS,
+                             "kernels": "mla_bwd_dq_kernel + mla_bwd_dkv_kernel<false> (fp32 atomic adds of "
+                                        "every slot's row, SFA.py:853's scheme)"}
+    return res
+
+
+def bench_shim(args):
+    """The reference's own operator signature and shape class:
+    ``SparseFlashAttentionTriton.apply(q [S, B, H, D], kv [S_kv, B, D],
+    attn_sink [H], topk_idxs [S, B, K], sm_scale)`` (SFA.py:69-164) with one
+    kv row serving as K and V, at S = 4096, B = 1, H = 64, D = 128, top-k 2048
+    (the query, the 255 before it and uniform draws from the rest of the
+    causal prefix), bf16, a sink: forward, then backward (dQ, kv's gradient
+    dK + dV, dsink) through the shim's strided views.  G = 64 query heads per
+    kv row: the d = 128 MFMA kernels in head groups of 16, the deterministic
+    dK/dV."""
+    import torch
+    import ops_amd
+    from ops_amd.workloads import make_workload
+    w = make_workload("prefill", device="cuda", S=4096, Hq=64, K=2048, with_dout=True)
+    q = w.q.permute(1, 0, 2, 3).detach().requires_grad_(True)   # [S, B, H, D]
+    kv = w.k[:, :, 0].permute(1, 0, 2).detach().requires_grad_(True)  # [S_kv, B, D]
+    idx = w.idx[:, :, 0].permute(1, 0, 2)                          # [S, B, K]
+    sink = torch.linspace(-1.0, 1.0, 64, device="cuda").requires_grad_(True)
+    dout = w.dout.permute(1, 0, 2, 3)
+    pairs = valid_pairs(w)
+    G = 64
+    ff = pairs * G * 2.0 * (128 + 128)
+    bf = pairs * G * 2.0 * (3 * 128 + 2 * 128)
+    with torch.no_grad():
+        ft, _ = time_steps(lambda: ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, w.scale),
+                           args.steps, args.warmup)
+    out = ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, w.scale)
+    bt, _ = time_steps(lambda: torch.autograd.grad(out, (q, kv, sink), dout, retain_graph=True),
+                       max(2, args.steps // 2), 1)
+    fms, bms = sum(ft) / len(ft), sum(bt) / len(bt)
+    return {"metric": "fwd / bwd effective TFLOP/s (reference signature)", "value": ff / (fms * 1e-3) / 1e12,
+            "unit": "TFLOP/s", "fwd_ms": fms, "frac_of_peak": ff / (fms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "gather_gbs": pairs * 2 * 128 * 2 * 4 / (fms * 1e-3) / 1e9,
+            "bwd": {"value": bf / (bms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": bms,
+                    "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+            "valid_pairs": pairs,
+            "note": "gather_gbs: K and V row bytes per valid pair and 16-head group (4 groups re-gather a row)",
+            "config": {"api": "SparseFlashAttentionTriton.apply (SBHD, shared kv, sink)", "B": 1, "S": 4096,
+                       "H": 64, "D": 128, "topk": 2048}}
 
 
 def bench_indexer(args, mla=None):
@@ -678,7 +732,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--extra", default="tiny,prefill,train_gqa,mla_decode,indexer,mla_bwd",
+    ap.add_argument("--extra", default="tiny,prefill,train_gqa,mla_decode,indexer,mla_bwd,shim",
                     help="comma list of additional workloads to measure ('' for none)")
     ap.add_argument("--no-bwd", action="store_true", help="skip the train_gqa backward timing")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -746,7 +800,8 @@ def main():
             extra[name] = bench_indexer(args, w)
         else:
             extra[name] = {"tiny": bench_tiny, "prefill": bench_prefill, "train_gqa": bench_train_gqa,
-                           "mla_decode": bench_mla_decode, "mla_bwd": bench_mla_bwd}[name](args)
+                           "mla_decode": bench_mla_decode, "mla_bwd": bench_mla_bwd,
+                           "shim": bench_shim}[name](args)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:

@@ -146,7 +146,8 @@ FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
   int splits = 1;
   if (pl.mfma) {
     const int nk = sfa::fwd_mfma_tile_keys(p);
-    const int64_t items = (int64_t)a->B * a->Sq * a->Hkv;
+    // workgroups before the split: work items times head groups
+    const int64_t items = (int64_t)a->B * a->Sq * a->Hkv * sfa::fwd_mfma_head_groups(p);
     if (a->num_splits > 0) {
       splits = a->num_splits;
     } else if (items < kTargetWorkgroups / 2) {

@@ -1,6 +1,6 @@
 // Deterministic dK/dV for the gfx950 sparse flash attention backward
-// (SFA_DKV_CSR), d_qk = d_v = 128 and G = 1, 2, 4, 8 or 16 query heads per
-// KV head.
+// (SFA_DKV_CSR), d_qk = d_v = 128 and G = 1, 2, 4, ..., 128 query heads per
+// KV head (a power of two).
 //
 // Reference: `_attn_bwd_dk_dv` / `_inner_dkv` (SFA.py:1005-1145, 719-853)
 // gathers, per query tile, the selected K/V rows and scatters dK/dV with
@@ -685,7 +685,7 @@ bool fits31(int64_t bytes) { return bytes > 0 && bytes < (int64_t)kOOB; }
 bool bwd_csr_supported(const Params& p) {
   if (!bwd_mfma_supported(p)) return false;  // the query-major dQ kernel
   if (p.Dqk != kD || p.Dv != kD) return false;
-  if (p.G != 1 && p.G != 2 && p.G != 4 && p.G != 8 && p.G != 16) return false;
+  if (p.G < 1 || p.G > kRowBlock || (p.G & (p.G - 1)) != 0) return false;  // a query block holds whole queries
   const int nkb = (p.Skv + kKeyBlock - 1) / kKeyBlock;
   const int64_t w = 4 * (int64_t)nkb;
   if (w > kMaxMapWords) return false;
@@ -698,7 +698,8 @@ bool bwd_csr_supported(const Params& p) {
 void csr_geometry(Params& p) {
   p.nkb = (p.Skv + kKeyBlock - 1) / kKeyBlock;
   p.kmap_w = 4 * p.nkb;
-  p.lg_g = p.G <= 1 ? 0 : p.G <= 2 ? 1 : p.G <= 4 ? 2 : p.G <= 8 ? 3 : 4;
+  p.lg_g = 0;
+  while ((1 << p.lg_g) < p.G) ++p.lg_g;  // G is a power of two <= 128
   const int nq = kRowBlock >> p.lg_g;
   p.nqb = (p.Sq + nq - 1) / nq;
   p.max_chunks = (p.nqb + kChunk - 1) / kChunk;

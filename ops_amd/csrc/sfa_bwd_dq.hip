@@ -1,5 +1,6 @@
 // gfx950 dQ (and dsink) kernel of the deterministic backward for d_qk = d_v =
-// 128 and G <= 16 query heads per KV head: register-direct gather.
+// 128: register-direct gather, 16 query heads per wave (G > 16 is split into
+// head groups of 16, each its own workgroup).
 //
 // Reference: `_attn_bwd_dq_dsink` / `_inner_dq` (SFA.py:856-1002, 613-716).
 // With the deterministic dK/dV scheme (sfa_bwd_csr.hip) the query-major pass
@@ -33,6 +34,7 @@ constexpr int kIdxWin = 512;    // slots staged in LDS at a time (a window of th
 constexpr int kQS = 4;          // 128 / 32 contraction steps over the head dim
 constexpr int kDT = 8;          // 128 / 16 dim tiles
 constexpr int kPK = 17;         // K staging row pitch in 16-byte slots (odd: conflict-free reads)
+constexpr int kMaxGroupQ = 256; // query heads per KV head (16 groups of 16)
 __device__ __forceinline__ f32x4 mma16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -46,7 +48,20 @@ __global__ __launch_bounds__(64, 2) void bwd_dq_kernel(Params p) {
   const int lt = lane & 15;  // head column / key row within a 16-row M-tile
   const int hq = lane >> 4;  // lane group
 
+  // work item and head group; the head groups of an item go to one XCD (its
+  // L2 then serves the re-gathered rows)
   int wi = blockIdx.x;
+  const int nhs = (p.G + 15) >> 4;
+  int hs;
+  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
+  if (nhs > 1 && nitems % 8 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    hs = r % nhs;
+    wi = (r / nhs) * 8 + x;
+  } else {
+    hs = wi % nhs;
+    wi /= nhs;
+  }
   const int g = wi % p.Hkv;
   wi /= p.Hkv;
   const int t = wi % p.Sq;
@@ -55,8 +70,9 @@ __global__ __launch_bounds__(64, 2) void bwd_dq_kernel(Params p) {
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
   const int bound = bound_of(p, b);
 
-  const bool hvalid = lt < p.G;
-  const int h = g * p.G + (hvalid ? lt : 0);
+  const int hl = 16 * hs + lt;  // head within the kv group
+  const bool hvalid = hl < p.G;
+  const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
   const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
   // rows with no valid slot (lse = -inf) and padding heads contribute nothing
@@ -291,14 +307,14 @@ __global__ __launch_bounds__(256) void bwd_dup_kernel(Params p) {
 
 bool bwd_dq_supported(const Params& p) {
   if (p.Dqk != 128 || p.Dv != 128) return false;
-  if (p.G > 16 || p.G < 1 || p.topk > kIdxCapQ) return false;
+  if (p.G > kMaxGroupQ || p.G < 1 || p.topk > kIdxCapQ) return false;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128);
   return kb < (int64_t)kOOB && vb < (int64_t)kOOB && fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss);
 }
 
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s) {
-  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * ((p.G + 15) / 16);
   hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
   return hipGetLastError();
 }

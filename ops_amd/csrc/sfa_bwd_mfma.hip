@@ -1,6 +1,6 @@
 // gfx950 MFMA backward of top-k sparse flash attention (bf16 in, fp32
-// accumulate), for head dims D = d_qk = d_v that are multiples of 32 and up
-// to 16 query heads per KV head.
+// accumulate), for head dims D = d_qk = d_v that are multiples of 32; up to
+// 16 query heads per workgroup (G > 16 is split into head groups of 16).
 //
 // Reference: `_attn_bwd_dq_dsink` / `_inner_dq` (SFA.py:856-1002, 613-716) and
 // `_attn_bwd_dk_dv` / `_inner_dkv` (SFA.py:1005-1145, 719-853).  The reference
@@ -34,6 +34,7 @@ namespace sfa {
 namespace {
 
 constexpr int kBwdIdxCap = 2048;  // slots staged in LDS per work item
+constexpr int kMaxGroupB = 256;   // query heads per KV head (16 groups of 16)
 
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
 
@@ -76,13 +77,26 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
   const int lt = lane & 15;     // head column / MFMA row within 16
   const int hq = lane >> 4;     // lane group
 
+  // work item and head group (the head groups of an item on one XCD)
   int wi = blockIdx.x;
+  const int nhs = (p.G + 15) >> 4;
+  int hs;
+  const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
+  if (nhs > 1 && nitems % 8 == 0) {
+    const int x = wi % 8, r = wi / 8;
+    hs = r % nhs;
+    wi = (r / nhs) * 8 + x;
+  } else {
+    hs = wi % nhs;
+    wi /= nhs;
+  }
   const int g = wi % p.Hkv;
   wi /= p.Hkv;
   const int t = wi % p.Sq;
   const int b = wi / p.Sq;
   const int nslots = p.topk;
   const int ntiles = (nslots + C::NKT - 1) / C::NKT;
+  const int hg0 = 16 * hs;  // first head (within the kv group) of this workgroup
 
   {
     const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
@@ -93,8 +107,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
     }
   }
 
-  // per-lane head: hl = lt
-  const int hl = lt;
+  // per-lane head: hl = hg0 + lt
+  const int hl = hg0 + lt;
   const bool hvalid = hl < p.G;
   const int h = g * p.G + (hvalid ? hl : 0);
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
@@ -119,7 +133,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
     qb[s] = x;
     dob[s] = y;
   }
-  // B operands over heads (16x16x16): lane holds heads 4hq .. 4hq+3 of dim 16nd + lt
+  // B operands over heads (16x16x16): lane holds heads hg0 + 4hq .. +3 of dim 16nd + lt
   bf16x4_t qh[C::DT], doh[C::DT];
   {
     const bf16* q0 = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)(g * p.G) * p.q_sh;
@@ -129,7 +143,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
       bf16x4_t x, y;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int hh = 4 * hq + j;
+        const int hh = hg0 + 4 * hq + j;
         const bool ok = hh < p.G;
         x[j] = ok ? q0[(int64_t)hh * p.q_sh + 16 * nd + lt] : (bf16)0.f;
         y[j] = ok ? d0[(int64_t)hh * p.do_sh + 16 * nd + lt] : (bf16)0.f;
@@ -193,8 +207,8 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
         dv[e] = (bf16)ds;
         dsb[4 * mt + e] = dv[e];
       }
-      *reinterpret_cast<bf16x4_t*>(patch_p + hl * C::PSTRIDE + mt * 16 + 4 * hq) = pv;
-      *reinterpret_cast<bf16x4_t*>(patch_s + hl * C::PSTRIDE + mt * 16 + 4 * hq) = dv;
+      *reinterpret_cast<bf16x4_t*>(patch_p + lt * C::PSTRIDE + mt * 16 + 4 * hq) = pv;
+      *reinterpret_cast<bf16x4_t*>(patch_s + lt * C::PSTRIDE + mt * 16 + 4 * hq) = dv;
     }
     // dQ^T += K^T dS^T: A = K^T from the k tile (transposing reads)
     {
@@ -278,7 +292,7 @@ using CfgBwdD128 = BwdCfg<128>;
 
 bool bwd_mfma_supported(const Params& p) {
   if (p.Dqk != 128 || p.Dv != 128) return false;
-  if (p.G > 16 || p.topk > kBwdIdxCap) return false;
+  if (p.G > kMaxGroupB || p.topk > kBwdIdxCap) return false;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
   return kb < (int64_t)kOOB && vb < (int64_t)kOOB && fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss);
@@ -286,7 +300,7 @@ bool bwd_mfma_supported(const Params& p) {
 
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s) {
   if (p.Dqk == 128 && p.Dv == 128) {
-    const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
+    const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * ((p.G + 15) / 16);
     hipLaunchKernelGGL(bwd_mfma_kernel<CfgBwdD128>, dim3((unsigned)n), dim3(CfgBwdD128::kThreads), 0, s, p);
     return hipGetLastError();
   }

@@ -1,12 +1,15 @@
-// gfx950 forward for d_qk = d_v = 128 with G <= 16 query heads per KV head
-// (the MQA prefill and GQA training shapes): register gather of whole rows.
+// gfx950 forward for d_qk = d_v = 128 (the MQA prefill and GQA training
+// shapes, and the reference's own single shared kv with G = 32, 64, 128 query
+// heads): register gather of whole rows.
 //
 // Reference: `_attn_fwd` / `_inner_fwd` (SFA.py:309-587); the math is the one
 // of the MLA kernel in sfa_fwd_mfma.hip (masked base-2 online softmax with a
 // lazy rescale, P V, sink, LSE, split-k partials).  The schedule follows from
-// the shape: one wave holds all G <= 16 heads of a work item, so a gathered K
-// or V row is used by exactly one wave and its load pattern, not reuse,
-// decides the gather rate.
+// the shape: one wave holds up to 16 heads of a work item (G <= 16: all of
+// them; larger G is split into head groups of 16, each its own workgroup,
+// the groups of one item placed on one XCD so the re-gathered rows come from
+// its L2), so a gathered K or V row is used by exactly one wave and its load
+// pattern, not reuse, decides the gather rate.
 //  * K and V rows of a 32-key tile are loaded one tile ahead into VGPRs as
 //    whole 256-byte rows: each load instruction moves 4 rows (16 lanes per
 //    row, 16 bytes each).  Loading them straight in the MFMA operand layout
@@ -39,6 +42,7 @@ constexpr int kT = 16;          // heads per wave (MFMA N)
 constexpr int kQSteps = 4;      // 128 / 32 contraction steps of S^T
 constexpr int kOT = 8;          // 128 / 16 O^T dim tiles
 constexpr int kPV = 17;         // V staging row pitch in 16-byte slots (odd: conflict-free reads)
+constexpr int kMaxGroupD = 256; // query heads per KV head (16 groups of 16)
 
 template <bool PAGED>
 __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
@@ -53,21 +57,27 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   const int hq = lane >> 4;  // lane group: 8-element slice of the contraction
 
   // ---- work item (same placement as the MLA kernel) ----------------------
+  // A sub-item is (split, head group): the sub-items of one item go to the
+  // same XCD, so its L2 serves them the item's rows.
   int wi = blockIdx.x;
-  int split;
+  const int nhs = (p.G + kT - 1) / kT;  // head groups of 16
+  const int nsub = p.num_splits * nhs;
+  int sub;
   const int64_t nitems = (int64_t)p.B * p.Sq * p.Hkv;
-  if (p.num_splits > 1 && nitems % 8 == 0) {
+  if (nsub > 1 && nitems % 8 == 0) {
     const int x = wi % 8, r = wi / 8;
-    split = r % p.num_splits;
-    wi = (r / p.num_splits) * 8 + x;
-  } else if (p.num_splits == 1 && nitems % 256 == 0) {
+    sub = r % nsub;
+    wi = (r / nsub) * 8 + x;
+  } else if (nsub == 1 && nitems % 256 == 0) {
     const int x = wi % 8, r = wi / 8;
-    split = 0;
+    sub = 0;
     wi = ((r / 32) * 8 + x) * 32 + r % 32;
   } else {
-    split = wi % p.num_splits;
-    wi /= p.num_splits;
+    sub = wi % nsub;
+    wi /= nsub;
   }
+  const int split = sub / nhs;
+  const int hg0 = (sub % nhs) * kT;  // first head (within the kv group) of this wave
   const int g = wi % p.Hkv;
   wi /= p.Hkv;
   const int t = wi % p.Sq;
@@ -84,12 +94,13 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   IdxStage<kIdxCapD, 64> istage;
   istage.load(irow, nslots, lane);
 
-  // ---- Q^T B operands (16x16x32: lane holds head lt, dims 32 s + 8 hq ..) ---
-  const bool hvalid = lt < p.G;
+  // ---- Q^T B operands (16x16x32: lane holds head hg0 + lt, dims 32 s + 8 hq ..) ---
+  const int hl = hg0 + lt;
+  const bool hvalid = hl < p.G;
   bf16x8 qb[kQSteps];
   {
     const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss +
-                       (int64_t)(g * p.G + (hvalid ? lt : 0)) * p.q_sh + 8 * hq;
+                       (int64_t)(g * p.G + (hvalid ? hl : 0)) * p.q_sh + 8 * hq;
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s) {
       bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
@@ -250,7 +261,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   const float m_fin = m_used;
 
   if (!hvalid) return;
-  const int h = g * p.G + lt;
+  const int h = g * p.G + hl;
   const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
   // Split partials: normalised O of this split in bf16 plus its base-2 LSE
   // (no sink: the merge adds it once).  Final output: the sink joins the
@@ -290,13 +301,15 @@ bool fwd_d128_supported(const Params& p) {
   // contiguous rows use 32-bit buffer offsets, paged pools 64-bit addresses
   const bool addressable = p.block_table != nullptr || (kb < (int64_t)kOOB && vb < (int64_t)kOOB &&
                                                         fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss));
-  return p.Dqk == 128 && p.Dv == 128 && p.G <= kT && p.G > 0 && addressable;
+  return p.Dqk == 128 && p.Dv == 128 && p.G <= kMaxGroupD && p.G > 0 && addressable;
 }
+
+int fwd_d128_head_groups(const Params& p) { return (p.G + kT - 1) / kT; }
 
 int fwd_d128_idx_cap() { return kIdxCapD; }
 
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
-  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits * fwd_d128_head_groups(p);
   if (p.block_table)
     hipLaunchKernelGGL(fwd_d128_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, p);
   else

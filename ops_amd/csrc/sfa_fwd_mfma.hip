@@ -1,7 +1,7 @@
 // gfx950 MFMA forward of top-k sparse flash attention for DeepSeek MLA
 // (G = 128 query heads share one latent KV head, d_qk = 576, d_v = 512, V the
-// first 512 dims of the K rows); bf16 in, fp32 accumulate.  The d = 128,
-// G <= 16 shapes have their own kernel (sfa_fwd_d128.hip).
+// first 512 dims of the K rows); bf16 in, fp32 accumulate.  The d = 128
+// shapes have their own kernel (sfa_fwd_d128.hip).
 //
 // Reference: `_attn_fwd` / `_inner_fwd` (lilac-me/ops SFA.py:309-587).  The
 // math is the same (gather the top-k rows, masked base-2 online softmax, P·V,
@@ -889,6 +889,10 @@ bool fwd_mfma_persistent(const Params& p) {
 }
 
 bool fwd_mfma_supported(const Params& p) { return mla_supported(p) || fwd_d128_supported(p); }
+
+// The MLA kernel holds all G heads of an item in one workgroup; the d = 128
+// kernel one head group of 16.
+int fwd_mfma_head_groups(const Params& p) { return mla_supported(p) ? 1 : fwd_d128_head_groups(p); }
 
 hipError_t launch_fwd_mfma(const Params& p, hipStream_t s) {
   if (mla_supported(p)) return launch<CfgMla>(p, s);

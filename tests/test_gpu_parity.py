@@ -275,6 +275,68 @@ def test_d128_non_power_of_two_groups(G, mode):
         assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
 
 
+@pytest.mark.parametrize("G,Hkv,mode", [(32, 1, "auto"), (32, 2, "atomic"), (64, 1, "auto"), (64, 1, "csr"),
+                                         (64, 1, "atomic"), (48, 1, "auto"), (128, 1, "csr")])
+def test_d128_large_groups(G, Hkv, mode):
+    """d=128 with more than 16 query heads per KV head, the reference's own
+    shape class (one shared kv, query heads tiled by 32, SFA.py:35-48, 88):
+    the MFMA kernels split the heads into groups of 16.  Forward and backward
+    with interior padding, ids past Skv and past kv_lens, a fully masked row,
+    a sink and a gradient into LSE; S = 320 spans several key blocks and, at
+    G = 64, several 128-query-block chunks of the deterministic scheme (G = 48
+    is not a power of two: 'auto' then takes the atomic scheme)."""
+    _say(f"d=128 G={G} Hkv={Hkv} B=2 S=320 Skv=384 K=96 fwd+bwd, dkv_mode={mode}")
+    g = torch.Generator(device="cpu").manual_seed(300 + G + Hkv)
+    B, S, Skv, K = 2, 320, 384, 96
+    Hq = G * Hkv
+    q = torch.randn(B, S, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Skv, Hkv, 128, generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, S, Hq, 128, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(Skv + 40, generator=g)[:K] - 20 for _ in range(B * S * Hkv)])
+    idx = idx.view(B, S, Hkv, K).to(torch.int32)
+    idx[:, :, :, K - 9:] = -1   # trailing padding
+    idx[1, 5] = -1              # a fully masked row
+    kv_lens = torch.tensor([Skv, 301], dtype=torch.int32)
+    sink = torch.linspace(-1.0, 2.0, Hq)
+    dlse = torch.randn(B, S, Hq, generator=g)
+    scale = 1.0 / math.sqrt(128)
+    o_ref, l_ref = ref_forward(q, k, v, idx, scale, kv_lens=kv_lens, sink=sink)
+    qd, kd, vd, idd, kld, sd = (t.to(DEV) for t in (q, k, v, idx, kv_lens, sink))
+    out, lse = ops_amd.sfa_forward(qd, kd, vd, idd, scale, kv_lens=kld, attn_sink=sd)
+    _check_fwd(out, lse, o_ref, l_ref)
+    dq, dk, dv, ds = ops_amd.sfa_backward(qd, kd, vd, idd, out, lse, dout.to(DEV), scale, kv_lens=kld,
+                                          attn_sink=sd, dlse=dlse.to(DEV), dkv_mode=mode)
+    g_ref = _bwd_with_dlse_ref(q.float(), k.float(), v.float(), idx, dout.float(), dlse, scale, kv_lens, sink)
+    for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
+        e = _rel_l2(a.cpu(), b)
+        assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+    assert torch.all(dq[1, 5] == 0)
+    assert torch.all(dk[1, 301:] == 0) and torch.all(dv[1, 301:] == 0)
+
+
+def test_d128_large_group_decode_splits():
+    """Decode with G = 64 (one shared kv, 4 head groups of 16 per sequence
+    and split-k over the top-k set): against the oracle at 1, 2 and 4
+    splits, with kv_lens and a sink."""
+    _say("d=128 decode G=64 B=4 Skv=4096 K=1024, splits 1/2/4")
+    g = torch.Generator(device="cpu").manual_seed(77)
+    B, Skv, H, K = 4, 4096, 64, 1024
+    q = torch.randn(B, 1, H, 128, generator=g).to(torch.bfloat16)
+    kv = torch.randn(B, Skv, 1, 128, generator=g).to(torch.bfloat16)
+    kv_lens = torch.tensor([4096, 3000, 1500, 700], dtype=torch.int32)
+    idx = torch.stack([torch.randperm(int(n), generator=g)[:K] if n >= K else
+                       torch.cat([torch.randperm(int(n), generator=g), torch.full((K - int(n),), -1)])
+                       for n in kv_lens]).view(B, 1, 1, K).to(torch.int32)
+    sink = torch.linspace(-0.5, 1.0, H)
+    scale = 1.0 / math.sqrt(128)
+    o_ref, l_ref = ref_forward(q, kv, kv, idx, scale, kv_lens=kv_lens, sink=sink)
+    qd, kd, idd, kld, sd = (t.to(DEV) for t in (q, kv, idx, kv_lens, sink))
+    for splits in (1, 2, 4):
+        out, lse = ops_amd.sfa_forward(qd, kd, kd, idd, scale, kv_lens=kld, attn_sink=sd, num_splits=splits)
+        _check_fwd(out, lse, o_ref, l_ref)
+
+
 @pytest.mark.parametrize("S,K", [(300, 64), (1024, 256)])
 def test_mla_prefill_reduced(S, K):
     _say(f"mla_prefill bf16 Hq=128 d_qk=576 d_v=512 S={S} K={K} (MFMA T=32 path)")
