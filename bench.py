@@ -47,6 +47,16 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# vector L1 / texture path: one 64-byte line per clock per CU, 256 CUs at 2.4 GHz
+PEAK_TEX_GBS = 256 * 64 * 2.4
+
+
+def texture(gather_gbs):
+    """The d = 128 kernels' binding resource: the gathered K / V row bytes
+    against the texture path's nominal rate (their counters show TD 0.87-0.94
+    busy while MFMA is 0.1-0.4 busy)."""
+    return {"gather_gbs": gather_gbs, "peak_gbs": PEAK_TEX_GBS, "frac": gather_gbs / PEAK_TEX_GBS,
+            "bytes_per_cu_clk_at_2p4ghz": gather_gbs * 1e9 / (256 * 2.4e9)}
 METRIC = "SFA fwd/bwd effective TFLOP/s (top-k FLOPs) + decode gather GB/s, % roofline"
 
 
@@ -290,6 +300,7 @@ def bench_prefill(args):
     res = {"metric": "fwd effective TFLOP/s", "value": tf, "unit": "TFLOP/s", "ms": ms, "valid_pairs": pairs,
            "frac_of_peak": tf / PEAK_BF16_TFLOPS, "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
            "config": {"B": 1, "S": 4096, "Hq": 16, "Hkv": 1, "d": 128, "topk": 512}}
+    res["texture"] = texture(res["gather_gbs"])
     if not args.no_cpu:
         _CPU_PENDING.append((res, "prefill", w))
     return res
@@ -308,6 +319,7 @@ def bench_train_gqa(args):
            "gather_gbs": gathered_bytes(w, pairs) / (ms * 1e-3) / 1e9,
            "config": {"B": 2, "S": 8192, "Hq": 32, "Hkv": 2, "d": 128, "topk": 1024}}
     res["frac_of_peak"] = res["value"] / PEAK_BF16_TFLOPS
+    res["texture"] = texture(res["gather_gbs"])
     if not args.no_bwd:
         out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
         bf = bwd_flops(w, pairs)
@@ -318,6 +330,9 @@ def bench_train_gqa(args):
             bms = sum(bt) / len(bt)
             res["bwd"][mode] = {"value": bf / (bms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": bms,
                                 "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+            if mode == "csr":
+                # the dQ pass re-gathers the K and V rows of every pair (bwd_dq_kernel)
+                res["bwd"][mode]["dq_pass_gather_bytes"] = gathered_bytes(w, pairs)
         res["bwd"]["note"] = ("TFLOP/s over valid pairs (pairs * G * 2 (3 d_qk + 2 d_v)); 'csr' = deterministic "
                               "dK/dV (the default), 'atomic' = fp32 atomics")
     if not args.no_cpu:
@@ -436,6 +451,7 @@ def bench_shim(args):
     return {"metric": "fwd / bwd effective TFLOP/s (reference signature)", "value": ff / (fms * 1e-3) / 1e12,
             "unit": "TFLOP/s", "fwd_ms": fms, "frac_of_peak": ff / (fms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
             "gather_gbs": pairs * 2 * 128 * 2 * 4 / (fms * 1e-3) / 1e9,
+            "texture": texture(pairs * 2 * 128 * 2 * 4 / (fms * 1e-3) / 1e9),
             "bwd": {"value": bf / (bms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": bms,
                     "frac_of_peak": bf / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
             "valid_pairs": pairs,
@@ -716,13 +732,14 @@ def trace_summary(root):
                     continue
                 wg = int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 1)) or 1)
                 grid = int(r.get("Grid_Size_X", r.get("Grid_Size", 0)) or 0) // max(wg, 1)
-                key = (name, grid, wg, r.get("Arch_VGPR_Count", r.get("VGPR_Count", "")),
-                       r.get("Accum_VGPR_Count", ""), r.get("LDS_Block_Size", r.get("Group_Segment_Size", "")))
+                # (registers, spills and occupancy: `python -m ops_amd.build --resource-usage`, from
+                # the compiler; the trace's register columns leave out the accumulation registers)
+                key = (name, grid, wg, r.get("LDS_Block_Size", r.get("Group_Segment_Size", "")))
                 groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    lines = ["| kernel | workgroups x threads | VGPR | AGPR | LDS B | launches | total ms | avg us | min | median | max |",
-             "|" + "---|" * 11]
-    for (name, grid, wg, vg, ag, lds), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"| {name} | {grid} x {wg} | {vg} | {ag} | {lds} | {len(d)} | {sum(d) / 1e3:.2f} | "
+    lines = ["| kernel | workgroups x threads | LDS B | launches | total ms | avg us | min | median | max |",
+             "|" + "---|" * 9]
+    for (name, grid, wg, lds), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {name} | {grid} x {wg} | {lds} | {len(d)} | {sum(d) / 1e3:.2f} | "
                      f"{statistics.mean(d):.1f} | {min(d):.1f} | {statistics.median(d):.1f} | {max(d):.1f} |")
     return "\n".join(lines)
 

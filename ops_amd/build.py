@@ -52,5 +52,41 @@ def build(verbose: bool = False, extra=None) -> Path:
     return LIB
 
 
+def resource_usage() -> str:
+    """Markdown table of every kernel's registers, scratch (spills), LDS and
+    occupancy as the compiler reports them (-Rpass-analysis=kernel-resource-usage,
+    one device-only compile per source)."""
+    import re
+    rows = []
+    for src in sources():
+        cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")], "--cuda-device-only", "-c",
+               "-Rpass-analysis=kernel-resource-usage", "-I", str(HERE.parent / "include"), src, "-o", os.devnull]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stderr)
+            raise subprocess.CalledProcessError(res.returncode, cmd)
+        cur = None
+        for line in res.stderr.splitlines():
+            m = re.search(r"remark: (?:\S+: )?\s*([A-Za-z ]+?)(?: \[[^]]*\])?: (\S+)(?: \[-Rpass)", line)
+            if not m:
+                continue
+            key, val = m.group(1).strip(), m.group(2)
+            if key == "Function Name":
+                cur = {"kernel": val, "file": os.path.basename(src)}
+                rows.append(cur)
+            elif cur is not None:
+                cur[key] = val
+    out = ["| kernel (mangled) | file | VGPRs | AGPRs | SGPRs | scratch B/lane | LDS B | waves/SIMD |",
+           "|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        out.append(f"| `{r['kernel']}` | {r['file']} | {r.get('VGPRs', '?')} | {r.get('AGPRs', '?')} | "
+                   f"{r.get('TotalSGPRs', '?')} | {r.get('ScratchSize', '?')} | {r.get('LDS Size', '?')} | "
+                   f"{r.get('Occupancy', '?')} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if "--resource-usage" in sys.argv:
+        print(resource_usage())
+    else:
+        print(build(verbose=True))

@@ -400,6 +400,59 @@ __global__ __launch_bounds__(kThreads) void combine512_kernel(Params p) {
   if (lane == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
 }
 
+// The same merge for NS splits and d_v = 128 (the d = 128 kernel splits a
+// top-k set longer than its 1024-slot index window): four rows per wave, a
+// 16-lane group per row, 8 dims (16 bytes) per lane; lane s of a group reads
+// split s's LSE, and every lane its NS partial-row pieces, all issued before
+// the weights are formed (one memory round trip).
+template <typename T, int NS>
+__global__ __launch_bounds__(kThreads) void combine128_kernel(Params p) {
+  const int lane = threadIdx.x & 63, gl = lane & 15;
+  const int64_t nrows = (int64_t)p.B * p.Sq * p.Hq;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+  const bool ok = row < nrows;
+  const int64_t r = ok ? row : nrows - 1;  // (rows past the end compute on the last row, store nothing)
+  const int h = r % p.Hq;
+  const int t = (r / p.Hq) % p.Sq;
+  const int b = r / ((int64_t)p.Hq * p.Sq);
+  const uint32_t lse_bytes = (uint32_t)((int64_t)NS * nrows * 4);
+  const float ls_raw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(p.part_lse, lse_bytes), gl < NS ? (uint32_t)((gl * nrows + r) * 4) : lse_bytes, 0, 0));
+  const float sink_raw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(p.sink, p.sink ? 4u * (uint32_t)p.Hq : 0u), 4u * (uint32_t)h, 0, 0));
+  bf16x8 pv[NS];
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) pv[sp] = *reinterpret_cast<const bf16x8*>(p.part_o + (sp * nrows + r) * 128 + 8 * gl);
+  __builtin_amdgcn_sched_barrier(0);
+  const float ls = gl < NS ? ls_raw : kNegInf;
+  const float sink2 = p.sink ? sink_raw * kLog2e : kNegInf;
+  float m = ls;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+  const float mm = fmaxf(m, sink2);
+  const float e = (ls == kNegInf || mm == kNegInf) ? 0.f : exp2f(ls - mm);
+  float l = e;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
+  if (p.sink && mm != kNegInf) l += exp2f(sink2 - mm);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float wl = e * inv;  // weight of split gl of this row
+  float acc[8] = {};
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) {
+    const float w = __shfl(wl, (lane & 48) | sp, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += w * (float)pv[sp][j];
+  }
+  if (!ok) return;
+  T* orow = reinterpret_cast<T*>(p.out) + b * p.o_sb + t * p.o_ss + h * p.o_sh;
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = (bf16)acc[j];
+  *reinterpret_cast<bf16x8*>(orow + 8 * gl) = o;
+  if (gl == 0) p.lse[b * p.l_sb + t * p.l_ss + h * p.l_sh] = (l > 0.f) ? (mm + log2f(l)) * kLn2 : kNegInf;
+}
+
 // dsink[h] = -Σ_{b,t} 2^(sink·log2e - lse2)·δ over the rows of head h
 // (SFA.py:964-970).  One workgroup per head; each thread sums a fixed
 // stride of rows and the block reduction adds in a fixed order, so the result
@@ -534,6 +587,16 @@ hipError_t launch_combine(const Params& p, int dtype, hipStream_t s) {
     SFA_COMBINE512(4)
     SFA_COMBINE512(8)
 #undef SFA_COMBINE512
+  }
+  if (p.Dv == 128 && dtype == SFA_DTYPE_BF16 && (p.num_splits == 2 || p.num_splits == 4 || p.num_splits == 8)) {
+    const dim3 grid128((unsigned)((rows + kThreads / 16 - 1) / (kThreads / 16)));
+    if (p.num_splits == 2)
+      hipLaunchKernelGGL((combine128_kernel<bf16, 2>), grid128, dim3(kThreads), 0, s, p);
+    else if (p.num_splits == 4)
+      hipLaunchKernelGGL((combine128_kernel<bf16, 4>), grid128, dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((combine128_kernel<bf16, 8>), grid128, dim3(kThreads), 0, s, p);
+    return hipGetLastError();
   }
   if (dtype == SFA_DTYPE_F32)
     hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(kThreads), 0, s, p);

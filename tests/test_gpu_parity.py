@@ -4,6 +4,7 @@ on identical seeded inputs.
 Bars (from the task): O max-abs <= 2e-2, LSE abs <= 1e-3, dQ/dK/dV
 relative-L2 <= 1e-2; index handling exact (bitwise-identical results when
 only invalid entries change)."""
+import ctypes
 import math
 import sys
 
@@ -174,8 +175,9 @@ def test_train_gqa_bwd_full():
 
 @pytest.mark.parametrize("D", [64, 256])
 def test_generic_bf16_bwd_large_group(D):
-    """G = 32 has no MFMA backward variant: the generic bf16 kernels run
-    (d = 64: the per-element δ kernel; d = 256: the 16-byte δ kernel)."""
+    """Head dims other than 128 (and the MLA 576 / 512) have no MFMA backward
+    variant: at G = 32 the generic bf16 kernels run (d = 64: the per-element
+    δ kernel; d = 256: the 16-byte δ kernel)."""
     _say(f"bf16 bwd G=32 d={D} (generic kernels)")
     w = make_workload("train_gqa", device=DEV, S=256, K=64, Hq=64, Hkv=2, Dqk=D, Dv=D)
     out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
@@ -576,3 +578,34 @@ def test_mla_decode_splits_sink(splits):
     o_ref, l_ref = ref_forward(w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), w.scale, kv_lens=w.kv_lens.cpu(),
                                sink=sink.cpu())
     _check_fwd(out, lse, o_ref, l_ref)
+
+
+@pytest.mark.parametrize("splits", [2, 4, 8])
+def test_mla_decode_any_workspace_contents(splits):
+    """The C ABI's workspace is scratch: with a workspace pre-filled with
+    random bytes, 13 sequences (an item count that is not a multiple of 8:
+    the splits of one sequence run on different XCDs), then a second call on
+    the same workspace: both within the oracle's bars, bitwise equal to each
+    other."""
+    _say(f"mla_decode B=13 Skv=4096 Hq=128 K=1024 splits={splits}, random workspace bytes")
+    from ops_amd import _lib
+    w = make_workload("mla_decode", device=DEV, B=13, Skv=4096, K=1024, ctx_lo=1500, seed=3)
+    lib = _lib.load()
+    B, _, Hq, _ = w.q.shape
+    res = []
+    wbuf = None
+    for call in range(2):
+        out = torch.full((B, 1, Hq, 512), float("nan"), dtype=w.q.dtype, device=DEV)
+        lse = torch.full((B, 1, Hq), float("nan"), dtype=torch.float32, device=DEV)
+        a = sfa._fwd_args(w.q, w.k, w.v, w.idx, out, lse, w.scale, w.kv_lens, None, splits)
+        ws = lib.sfa_fwd_workspace_size(ctypes.byref(a))
+        if wbuf is None:
+            wbuf = torch.randint(0, 256, (ws,), dtype=torch.uint8, device=DEV)
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.sfa_fwd(ctypes.byref(a), ctypes.c_void_p(wbuf.data_ptr()), ws, stream))
+        torch.cuda.synchronize()
+        res.append((out, lse))
+    o_ref, l_ref = ref_forward(w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), w.scale, kv_lens=w.kv_lens.cpu())
+    for out, lse in res:
+        _check_fwd(out, lse, o_ref, l_ref)
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
