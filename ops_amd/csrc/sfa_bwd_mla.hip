@@ -596,37 +596,55 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
     // 16 nt + lt: 8-byte row pieces for the staged rows); atomics: keys as
     // rows (lane: keys 16 nt + 4 hq + i of dim dim0 + 16 n + lt: each atomic
     // instruction covers 4 keys x 16 contiguous dims)
+    // The B operands (P and dS of a (key half, head step)) of step st + 1 are
+    // read into the other register set after the second MFMA of step st, so
+    // their LDS latency runs under step st's MFMAs; the first two MFMAs take
+    // the other set (step st - 1's operands) as keep-alive inputs, so at
+    // least two MFMAs issue between the last one reading them and the reads
+    // that overwrite them (the old per-step s_nop 7 kept that distance).
+    // The dO^T operands of dims >= 512 (wave 3) are zeros: their MFMAs run
+    // too, which keeps the stream free of branches (wave 3 then does as
+    // many MFMAs per step as the others, which the barrier waits for anyway).
     Mfma16A::acc_t acc[kDN][2];
+    constexpr int kSteps = 2 * kHS;
+    bf16x8 bsv[2], bpv[2];
+    bsv[0] = read_pd(tb, 1, 0, 0);
+    bpv[0] = read_pd(tb, 0, 0, 0);
+    bsv[1] = bf16x8{};
+    bpv[1] = bf16x8{};
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int st = 0; st < kSteps; ++st) {
+      const int nt = st / kHS, ks = st % kHS, cur = st & 1, nxt = cur ^ 1;
+      const bf16x8 bs = bsv[cur], bp = bpv[cur];
 #pragma unroll
-      for (int ks = 0; ks < kHS; ++ks) {
-        const bf16x8 bs = read_pd(tb, 1, nt, ks);
-        const bf16x8 bp = read_pd(tb, 0, nt, ks);
-#pragma unroll
-        for (int n = 0; n < kDN; ++n) {
-          if constexpr (DET) {
-            if (ks == 0)
-              Mfma16A::mma0(qB[n][ks], bs, acc[n][nt], bp, bs);
-            else
-              Mfma16A::mma<false>(qB[n][ks], bs, acc[n][nt], bp, bs);
-          } else {
-            if (ks == 0)
-              Mfma16A::mma0(bs, qB[n][ks], acc[n][nt], bp, bs);
-            else
-              Mfma16A::mma<false>(bs, qB[n][ks], acc[n][nt], bp, bs);
-          }
+      for (int n = 0; n < kDN; ++n) {
+        // (n < 2: keep the other set alive up to here; then read step st + 1 into it)
+        const bf16x8& ka = n < 2 ? bpv[nxt] : bp;
+        const bf16x8& kb = n < 2 ? bsv[nxt] : bs;
+        if constexpr (DET) {
+          if (ks == 0)
+            Mfma16A::mma0(qB[n][ks], bs, acc[n][nt], ka, kb);
+          else
+            Mfma16A::mma<false>(qB[n][ks], bs, acc[n][nt], ka, kb);
+        } else {
+          if (ks == 0)
+            Mfma16A::mma0(bs, qB[n][ks], acc[n][nt], ka, kb);
+          else
+            Mfma16A::mma<false>(bs, qB[n][ks], acc[n][nt], ka, kb);
         }
-#pragma unroll
-        for (int n = 0; n < kDN; ++n)
-          if (n < ndv) {
-            if constexpr (DET)
-              Mfma16A::mma_a_agpr(dB[n][ks], bp, acc[n][nt], bs);
-            else
-              Mfma16A::mma_b_agpr(bp, dB[n][ks], acc[n][nt], bs);
-          }
-        Mfma16A::tail(bs, bp);
+        if (n == 1 && st + 1 < kSteps) {
+          bsv[nxt] = read_pd(tb, 1, (st + 1) / kHS, (st + 1) % kHS);
+          bpv[nxt] = read_pd(tb, 0, (st + 1) / kHS, (st + 1) % kHS);
+        }
       }
+#pragma unroll
+      for (int n = 0; n < kDN; ++n) {
+        if constexpr (DET)
+          Mfma16A::mma_a_agpr(dB[n][ks], bp, acc[n][nt], bs);
+        else
+          Mfma16A::mma_b_agpr(bp, dB[n][ks], acc[n][nt], bs);
+      }
+      if (st + 1 == kSteps) Mfma16A::tail(bs, bp);
     }
 #pragma unroll
     for (int n = 0; n < kDN; ++n)
