@@ -48,3 +48,27 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("SFA_LIB", str(tmp_path / "nope.so"))
     with pytest.raises(_lib.SFAError):
         _lib.load()
+
+
+def test_kv_merge_only_for_views_autograd_tracks():
+    """The autograd Function returns dK + dV as k's gradient (None for v)
+    only where autograd itself would add v's gradient into k's rows: v is k,
+    or a prefix view of k (or of k's base) that autograd tracks, and both
+    want a gradient.  Same-memory aliases that autograd does not see (a
+    detached view, a second leaf over one storage, a view taken under
+    no_grad) keep separate gradients; so do prefixes whose memory differs."""
+    kv = torch.randn(2, 6, 1, 12, requires_grad=True)
+    m = sfa._merge_in_autograd
+    assert m(kv, kv[..., :8], True, True)                      # MLA: v = kv[..., :512]
+    assert m(kv, kv, True, True)                               # v is k
+    k2 = kv.view(2, 6, 1, 12)
+    assert m(k2, kv[..., :8], True, True)                      # k and v views of one base
+    assert not m(kv, kv[..., :8].detach(), True, False)        # detached alias
+    other = kv.detach().requires_grad_(True)
+    assert not m(kv, other[..., :8], True, True)               # second leaf over the same storage
+    with torch.no_grad():
+        vng = kv[..., :8]
+    assert not m(kv, vng, True, False)                         # view without a gradient
+    assert not m(kv, kv[..., :8], True, False)                 # v's gradient not wanted
+    assert not m(kv, kv[..., 4:12], True, True)                # not a prefix of the rows
+    assert not m(kv, kv[:, :3, :, :8], True, True)             # fewer rows than k
