@@ -334,10 +334,11 @@ int fwd_mfma_tile_keys(const Params& p);
 int fwd_mfma_idx_cap(const Params& p);  // index slots one work item (split) stages
 bool fwd_mfma_persistent(const Params& p);  // needs Params::sched (8 ints of workspace)
 int fwd_mfma_head_groups(const Params& p);  // workgroups per (work item, split): head groups
-int fwd_d128_idx_cap();
+int fwd_d128_idx_cap(const Params& p);
 // d = 128: register-direct gather, 16 heads per wave (sfa_fwd_d128.hip)
 bool fwd_d128_supported(const Params& p);
-int fwd_d128_head_groups(const Params& p);  // ceil(G / 16)
+bool fwd_d128g_supported(const Params& p);  // 16 < G <= 128, contiguous: one workgroup per item, a shared tile
+int fwd_d128_head_groups(const Params& p);  // workgroups per (item, split): ceil(G / 16), or 1 (shared tile)
 hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);

@@ -879,7 +879,7 @@ int fwd_mfma_tile_keys(const Params& p) {
   return 32;  // d = 128 kernel: 32-key tiles
 }
 
-int fwd_mfma_idx_cap(const Params& p) { return mla_supported(p) ? kIdxCap : fwd_d128_idx_cap(); }
+int fwd_mfma_idx_cap(const Params& p) { return mla_supported(p) ? kIdxCap : fwd_d128_idx_cap(p); }
 
 // Whether the forward of p runs persistent (its Params then need sched, 8
 // zeroed ints): the MLA kernel without split-k over enough items to keep
