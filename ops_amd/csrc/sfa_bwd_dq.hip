@@ -226,6 +226,179 @@ __global__ __launch_bounds__(64, 2) void bwd_dq_kernel(Params p) {
   }
 }
 
+// dQ with 16 < G <= 128 on contiguous rows: the head groups of a work item
+// are the NW waves of one workgroup (wave w: heads 16 w .. 16 w + 15, NW = G /
+// 16 rounded up to a power of two), which gather each 32-key tile together
+// (wave w its rows w R .. w R + R - 1, R = 32 / NW, whole rows one tile ahead
+// in VGPRs) into double-buffered LDS tiles that all waves read their
+// operands from, one LDS-only barrier per tile: a gathered row serves all G
+// heads; with VK (v rows are the k rows: the reference's single kv) one
+// gather serves K and V.  The per-wave math is bwd_dq_kernel's.
+constexpr int kIdxCapQG = 2048;
+constexpr int kMaxGroupQG = 128;
+
+template <int NW, bool VK>
+__global__ __launch_bounds__(64 * NW, 2) void bwd_dq_g_kernel(Params p) {
+  constexpr int R = 32 / NW, RI = R / 4, THR = 64 * NW, TS = 32 * kPK;
+  static_assert(R % 4 == 0 && NW * R == 32, "whole 4-row load instructions");
+  __shared__ __attribute__((aligned(16))) int s_idx[kIdxCapQG];
+  __shared__ u32x4 s_k[2][TS];
+  __shared__ u32x4 s_v[2][VK ? 1 : TS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lt = lane & 15, hq = lane >> 4;
+
+  int wi = blockIdx.x;
+  const int g = wi % p.Hkv;
+  wi /= p.Hkv;
+  const int t = wi % p.Sq;
+  const int b = wi / p.Sq;
+  const int nslots = p.topk;
+  const int ntiles = (nslots + 31) / 32;
+  const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
+  const int bound = bound_of(p, b);
+  for (int i = tid; i < ntiles * 32; i += THR) {
+    const int id = (i < nslots) ? irow[i] : -1;
+    s_idx[i] = (id >= 0 && id < bound) ? id : -1;
+  }
+
+  const int hl = 16 * wave + lt;  // head within the kv group
+  const bool hvalid = hl < p.G;
+  const int h = g * p.G + (hvalid ? hl : 0);
+  const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
+  const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+  const bool live = hvalid && lse != kNegInf;
+  const float lse2 = live ? lse * kLog2e : __builtin_huge_valf();
+  const float delta = live ? p.delta[row] : 0.f;
+  const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh;
+  const bf16* dorow = reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh;
+  bf16x8 qb[kQS], dob[kQS];
+#pragma unroll
+  for (int s = 0; s < kQS; ++s) {
+    bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * hq);
+    bf16x8 y = *reinterpret_cast<const bf16x8*>(dorow + 32 * s + 8 * hq);
+    if (!hvalid) {
+      x = bf16x8{};
+      y = bf16x8{};
+    }
+    qb[s] = x;
+    dob[s] = y;
+  }
+  const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
+  const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
+  const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss), vrow_bytes = (uint32_t)(2 * p.v_ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
+
+  // rows of tile j this lane loads: instruction i, chunk lt of tile row
+  // wave R + RI hq + i; invalid keys read zeros
+  const int row0 = wave * R + RI * hq;
+  auto load_rows = [&](int j, bf16x8 (&kr)[RI], bf16x8 (&vr)[RI]) {
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+      const int id = s_idx[32 * j + row0 + i];
+      const uint32_t ko = id >= 0 ? __umul24((uint32_t)id, krow_bytes) + 16u * (uint32_t)lt : kOOB;
+      kr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
+      if constexpr (!VK) {
+        const uint32_t vo = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) + 16u * (uint32_t)lt : kOOB;
+        vr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+      }
+    }
+  };
+  auto write_rows = [&](int buf, const bf16x8 (&kr)[RI], const bf16x8 (&vr)[RI]) {
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+      *reinterpret_cast<bf16x8*>(&s_k[buf][(row0 + i) * kPK + lt]) = kr[i];
+      if constexpr (!VK) *reinterpret_cast<bf16x8*>(&s_v[buf][(row0 + i) * kPK + lt]) = vr[i];
+    }
+  };
+  auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  f32x4 dqacc[kDT];
+#pragma unroll
+  for (int i = 0; i < kDT; ++i) dqacc[i] = f32x4{};
+  const int rr = lt >> 2, cc = lt & 3;
+  const uint32_t r0 = (uint32_t)((4 * hq + rr) * kPK) * 16u + (uint32_t)(4 * cc) * 2u;
+  const uint32_t r1 = r0 + (uint32_t)(16 * kPK) * 16u;
+
+  __syncthreads();  // ids staged
+  bf16x8 kr[RI], vr[RI];
+  if (ntiles > 0) {
+    load_rows(0, kr, vr);
+    write_rows(0, kr, vr);
+  }
+  if (ntiles > 1) load_rows(1, kr, vr);
+  lds_barrier();
+  for (int j = 0; j < ntiles; ++j) {
+    const int cur = j & 1;
+    const u32x4* kt = s_k[cur];
+    const u32x4* vt = VK ? s_k[cur] : s_v[cur];
+    const int* ib = s_idx + 32 * j;
+    const uint32_t vmask = (uint32_t)__ballot(ib[lane & 31] >= 0);
+    if (vmask != 0u) {  // (uniform over the workgroup: every wave sees the same ids)
+      // S^T and dP^T: two 16-key M tiles; A operands (row 16 mt + lt,
+      // chunk 4 s + hq) read one contraction step ahead of their MFMAs
+      f32x4 sacc[2] = {f32x4{}, f32x4{}}, dpacc[2] = {f32x4{}, f32x4{}};
+      auto read_ops = [&](int s, bf16x8 (&kc)[2], bf16x8 (&vc)[2]) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          kc[mt] = *reinterpret_cast<const bf16x8*>(&kt[(16 * mt + lt) * kPK + 4 * s + hq]);
+          vc[mt] = *reinterpret_cast<const bf16x8*>(&vt[(16 * mt + lt) * kPK + 4 * s + hq]);
+        }
+      };
+      bf16x8 kc[2][2], vc[2][2];
+      read_ops(0, kc[0], vc[0]);
+#pragma unroll
+      for (int s = 0; s < kQS; ++s) {
+        if (s + 1 < kQS) read_ops(s + 1, kc[(s + 1) & 1], vc[(s + 1) & 1]);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          sacc[mt] = mma16x32(kc[s & 1][mt], qb[s], sacc[mt]);
+          dpacc[mt] = mma16x32(vc[s & 1][mt], dob[s], dpacc[mt]);
+        }
+        asm volatile("" ::: "memory");
+      }
+      bf16x8 dsb;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = mt * 16 + 4 * hq + e;
+          const bool valid = (vmask >> key) & 1u;
+          const float pr = valid ? exp2f(sacc[mt][e] * p.scale_log2 - lse2) : 0.f;
+          dsb[4 * mt + e] = (bf16)(pr * (dpacc[mt][e] - delta));
+        }
+      // dQ^T += K^T dS^T: A = K^T from the staged tile (transposing reads)
+#pragma unroll
+      for (int ot = 0; ot < kDT; ++ot) {
+        const bf16x4 lo = lds_read_tr16(kt, r0 + (uint32_t)(ot * 16) * 2u);
+        const bf16x4 hi = lds_read_tr16(kt, r1 + (uint32_t)(ot * 16) * 2u);
+        const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        dqacc[ot] = mma16x32(a, dsb, dqacc[ot]);
+      }
+    }
+    // tile j + 1's rows into the other buffer (read by nobody since the last
+    // barrier), then tile j + 2's loads
+    if (j + 1 < ntiles) {
+      write_rows(cur ^ 1, kr, vr);
+      if (j + 2 < ntiles) load_rows(j + 2, kr, vr);
+    }
+    lds_barrier();
+  }
+
+  if (!hvalid) return;
+  bf16* dqrow = reinterpret_cast<bf16*>(p.dq) + b * p.dq_sb + t * p.dq_ss + (int64_t)h * p.dq_sh;
+#pragma unroll
+  for (int ot = 0; ot < kDT; ++ot) {
+    const bf16x4 v4 = {(bf16)(dqacc[ot][0] * p.scale), (bf16)(dqacc[ot][1] * p.scale), (bf16)(dqacc[ot][2] * p.scale),
+                       (bf16)(dqacc[ot][3] * p.scale)};
+    *reinterpret_cast<bf16x4*>(dqrow + 16 * ot + 4 * hq) = v4;
+  }
+}
+
+bool dq_g_supported(const Params& p) { return p.G > 16 && p.G <= kMaxGroupQG && p.topk <= kIdxCapQG; }
+
 // dK/dV of index slots that repeat an earlier slot's key in their row (p.dup,
 // written by the index inversion; the key-major pass counts each key once
 // per row).  Such slots are absent from ordinary index sets, so this is
@@ -314,6 +487,23 @@ bool bwd_dq_supported(const Params& p) {
 }
 
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s) {
+  if (dq_g_supported(p)) {
+    const int64_t n = (int64_t)p.B * p.Sq * p.Hkv;
+    const bool vk = p.v == p.k && p.v_sb == p.k_sb && p.v_ss == p.k_ss && p.v_sh == p.k_sh;
+    const int nw = p.G <= 32 ? 2 : p.G <= 64 ? 4 : 8;
+#define SFA_DQG(NW)                                                                                \
+  if (nw == NW) {                                                                                  \
+    if (vk)                                                                                        \
+      hipLaunchKernelGGL((bwd_dq_g_kernel<NW, true>), dim3((unsigned)n), dim3(64 * NW), 0, s, p);  \
+    else                                                                                           \
+      hipLaunchKernelGGL((bwd_dq_g_kernel<NW, false>), dim3((unsigned)n), dim3(64 * NW), 0, s, p); \
+    return hipGetLastError();                                                                      \
+  }
+    SFA_DQG(2)
+    SFA_DQG(4)
+    SFA_DQG(8)
+#undef SFA_DQG
+  }
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * ((p.G + 15) / 16);
   hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)n), dim3(64), 0, s, p);
   return hipGetLastError();
