@@ -562,6 +562,84 @@ def profile_targets(name):
     raise SystemExit(f"unknown --profile target {name!r}")
 
 
+def run_probe(name, args):
+    """Hardware ceilings the design's decisions rest on, from committed code
+    (one JSON line per measurement):
+      gemm           the vendor bf16 GEMM (hipBLASLt via torch.matmul) on
+                     N(0,1) operands at 4096^3, 8192^3, 16384^3: the dense
+                     MFMA rate this power-limited part sustains;
+      decode_gather  the 64 x 64K decode's data movement without its MFMA
+                     work (libsfa_probe.so: the library's row gather, LDS
+                     DMA, two 32-row tiles in flight, one barrier per tile),
+                     caches flushed before each step as in the decode bench,
+                     in the work layouts the decode design compares; the
+                     real decode step (prepared sfa_fwd call) is timed
+                     beside them."""
+    import ctypes
+    import torch
+    if name == "gemm":
+        for n in (4096, 8192, 16384):
+            g = torch.Generator(device="cuda").manual_seed(n)
+            a = torch.randn(n, n, device="cuda", generator=g).bfloat16()
+            b = torch.randn(n, n, device="cuda", generator=g).bfloat16()
+            t, _ = time_steps(lambda: torch.matmul(a, b), max(3, args.steps), 2)
+            ms = statistics.median(t)
+            print(json.dumps({"probe": "gemm_bf16", "n": n, "ms": round(ms, 4),
+                              "tflops": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1),
+                              "frac_of_peak": round(2 * n ** 3 / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}),
+                  flush=True)
+            del a, b
+        return
+    if name != "decode_gather":
+        raise SystemExit(f"unknown --probe {name!r} (gemm, decode_gather)")
+    from ops_amd.workloads import make_workload
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ops_amd", "libsfa_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is not built: python -m ops_amd.build")
+    lib = ctypes.CDLL(path)
+    lib.sfa_probe_gather.restype = ctypes.c_int
+    lib.sfa_probe_gather.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    w = make_workload("mla_decode", device="cuda")
+    B, _, Hq, Dqk = w.q.shape
+    Skv, K = w.k.shape[1], w.idx.shape[-1]
+    assert w.k.is_contiguous() and w.q.is_contiguous() and w.k.shape[2] == 1 and Dqk == 576
+    idx = w.idx.reshape(B, K).contiguous()
+    gathered = valid_pairs(w) * Dqk * 2
+    flush = decode_flush()
+    part = torch.empty(B * 4 * 128 * 1024, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    qrow = Hq * Dqk * 2
+    layouts = [  # (what, key splits, head groups, Q bytes per workgroup, partial rows per workgroup)
+        ("4 key splits x 128 heads: gather only", 4, 1, 0, 0),
+        ("4 key splits x 128 heads: gather + Q", 4, 1, qrow, 0),
+        ("4 key splits x 128 heads: gather + Q + bf16 partial rows", 4, 1, qrow, 128),
+        ("2 key splits x 2 groups of 64 heads: gather + Q + partial rows", 2, 2, qrow // 2, 64),
+        ("1 split x 4 groups of 32 heads (no partials): gather + Q", 1, 4, qrow // 4, 0),
+    ]
+    for what, splits, hg, qb, rows in layouts:
+        fn = lambda: lib.sfa_probe_gather(ctypes.c_void_p(w.k.data_ptr()), ctypes.c_void_p(w.q.data_ptr()), qrow,
+                                          ctypes.c_void_p(idx.data_ptr()), ctypes.c_void_p(part.data_ptr()), B, Skv,
+                                          K, splits, hg, qb, rows, ctypes.c_void_p(stream))
+        rc = fn()
+        if rc != 0:
+            raise SystemExit(f"sfa_probe_gather failed: {rc}")
+        t, _ = time_steps(fn, args.steps * 4, args.warmup, before=flush)
+        us = sum(t) / len(t) * 1e3
+        print(json.dumps({"probe": "decode_gather", "layout": what, "workgroups": B * splits * hg,
+                          "us": round(us, 2), "us_median": round(statistics.median(t) * 1e3, 2),
+                          "gathered_gbs": round(gathered * hg / (us * 1e-6) / 1e9, 1),
+                          "algorithmic_gbs": round(gathered / (us * 1e-6) / 1e9, 1)}), flush=True)
+    out = torch.empty((B, 1, Hq, w.v.shape[3]), dtype=w.q.dtype, device="cuda")
+    lse = torch.empty((B, 1, Hq), dtype=torch.float32, device="cuda")
+    fn = prepared_forward(w, out, lse)
+    t, _ = time_steps(fn, args.steps * 4, args.warmup, before=flush)
+    print(json.dumps({"probe": "decode_gather", "layout": "the decode step itself (sfa_fwd, 4 splits + combine)",
+                      "us": round(sum(t) / len(t) * 1e3, 2), "us_median": round(statistics.median(t) * 1e3, 2)}),
+          flush=True)
+
+
 # Counter passes of the per-workload counter summaries (one rocprofv3 run
 # each; every pass stays within one run's per-block counter limits).
 PMC_PASSES = (
@@ -791,6 +869,9 @@ def main():
     ap.add_argument("--pmc-passes", action="store_true", help="print PMC_PASSES, one line each, and exit")
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="print per-(kernel, grid) durations of the --kernel-trace CSVs under DIR and exit")
+    ap.add_argument("--probe", default="", metavar="NAME",
+                    help="measure a hardware ceiling the design rests on and exit: gemm (bf16 GEMM rate), "
+                         "decode_gather (the decode's data movement without its MFMA work, per work layout)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB `steps` times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -822,6 +903,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": args.steps}), flush=True)
+        return
+    if args.probe:
+        run_probe(args.probe, args)
         return
     if args.profile:
         fn, before = profile_targets(args.profile)

@@ -52,6 +52,25 @@ def build(verbose: bool = False, extra=None) -> Path:
     return LIB
 
 
+PROBE_SRC = CSRC / "probe" / "sfa_probe.hip"
+PROBE_LIB = HERE / "libsfa_probe.so"
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """Compile the measurement-only probe library (libsfa_probe.so: the
+    decode's gathers without their MFMA work, for ``bench.py --probe``)."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(HERE.parent / "include"), str(PROBE_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise subprocess.CalledProcessError(res.returncode, cmd, res.stdout, res.stderr)
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def resource_usage() -> str:
     """Markdown table of every kernel's registers, scratch (spills), LDS and
     occupancy as the compiler reports them (-Rpass-analysis=kernel-resource-usage,
@@ -90,3 +109,4 @@ if __name__ == "__main__":
         print(resource_usage())
     else:
         print(build(verbose=True))
+        print(build_probe(verbose=True))

@@ -251,3 +251,25 @@ def test_noalloc_rejects_plans_beyond_its_scratch():
     assert b"static scratch" in lib.sfa_last_error()
     a.topk = 0
     assert lib.sfa_fwd_noalloc(ctypes.byref(a), None) == _lib.SFA_E_INVALID
+
+
+def test_probe_library_rejects_bad_arguments_without_launching():
+    """The measurement-only probe library (bench.py --probe decode_gather)
+    builds beside libsfa.so and refuses arguments outside its limits before
+    any launch (no GPU needed for these calls)."""
+    import os
+    path = os.path.join(os.path.dirname(_lib.__file__), "libsfa_probe.so")
+    if not os.path.exists(path):
+        pytest.skip("libsfa_probe.so is not built (python -m ops_amd.build)")
+    lib = ctypes.CDLL(path)
+    f = lib.sfa_probe_gather
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    ok = dict(kv=0x10000, q=0x10000, qr=147456, idx=0x10000, part=0x10000, B=64, Skv=65536, K=2048, s=4, hg=1,
+              qb=0, rows=0)
+    for bad in (dict(B=0), dict(s=0), dict(K=4096, s=1), dict(Skv=1 << 21), dict(qb=200000), dict(rows=4, part=None),
+                dict(hg=-1)):
+        a = {**ok, **bad}
+        assert f(a["kv"], a["q"], a["qr"], a["idx"], a["part"], a["B"], a["Skv"], a["K"], a["s"], a["hg"], a["qb"],
+                 a["rows"], None) == -1, bad
