@@ -278,7 +278,8 @@ def test_d128_non_power_of_two_groups(G, mode):
 
 
 @pytest.mark.parametrize("G,Hkv,mode", [(32, 1, "auto"), (32, 2, "atomic"), (64, 1, "auto"), (64, 1, "csr"),
-                                         (64, 1, "atomic"), (48, 1, "auto"), (128, 1, "csr")])
+                                         (64, 1, "atomic"), (48, 1, "auto"), (128, 1, "csr"), (20, 1, "auto"),
+                                         (40, 2, "atomic"), (100, 1, "auto")])
 def test_d128_large_groups(G, Hkv, mode):
     """d=128 with more than 16 query heads per KV head, the reference's own
     shape class (one shared kv, query heads tiled by 32, SFA.py:35-48, 88):
@@ -286,7 +287,10 @@ def test_d128_large_groups(G, Hkv, mode):
     with interior padding, ids past Skv and past kv_lens, a fully masked row,
     a sink and a gradient into LSE; S = 320 spans several key blocks and, at
     G = 64, several 128-query-block chunks of the deterministic scheme (G = 48
-    is not a power of two: 'auto' then takes the atomic scheme)."""
+    is not a power of two: 'auto' then takes the atomic scheme).  G = 20, 40
+    and 100 leave the last head group partly empty, and at G = 100 the
+    shared-tile kernels' eighth wave has no head at all (heads 112-127): it
+    still loads its share of every tile and joins every barrier."""
     _say(f"d=128 G={G} Hkv={Hkv} B=2 S=320 Skv=384 K=96 fwd+bwd, dkv_mode={mode}")
     g = torch.Generator(device="cpu").manual_seed(300 + G + Hkv)
     B, S, Skv, K = 2, 320, 384, 96
