@@ -346,7 +346,11 @@ class SparseFlashAttentionSBHD(torch.autograd.Function):
     query t is shared by all heads (SFA.py:538).  The SBHD tensors are passed
     to the kernels as strided BSHD views, so nothing is copied; the gradient
     of the shared ``kv`` is dK + dV (the reference sums them into one buffer,
-    SFA.py:849-853).
+    SFA.py:849-853).  ``out`` and the gradients are allocated in the layout
+    of the tensor they belong to, as the reference allocates them
+    (``empty_like(q)``, ``zeros_like(q)``, ``zeros_like(kv)``, SFA.py:104,
+    184-185: a contiguous ``q`` gives a contiguous ``out``), and the kernels
+    write them through BSHD views.
     """
 
     @staticmethod
@@ -356,10 +360,11 @@ class SparseFlashAttentionSBHD(torch.autograd.Function):
         qb = q.permute(1, 0, 2, 3)
         kb = kv.permute(1, 0, 2).unsqueeze(2)
         idx = topk_idxs.permute(1, 0, 2).unsqueeze(2)
-        out, lse = sfa_forward(qb, kb, kb, idx, sm_scale, attn_sink=attn_sink)
+        out = _rows(torch.empty_like(q))
+        _, lse = sfa_forward(qb, kb, kb, idx, sm_scale, attn_sink=attn_sink, out=out.permute(1, 0, 2, 3))
         ctx.save_for_backward(q, kv, attn_sink, topk_idxs, out, lse)
         ctx.sm_scale = sm_scale
-        return out.permute(1, 0, 2, 3)
+        return out
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -367,12 +372,14 @@ class SparseFlashAttentionSBHD(torch.autograd.Function):
         qb = q.permute(1, 0, 2, 3)
         kb = kv.permute(1, 0, 2).unsqueeze(2)
         idx = topk_idxs.permute(1, 0, 2).unsqueeze(2)
-        dq, dk, _, dsink = sfa_backward(qb, kb, kb, idx, out, lse, grad_out.permute(1, 0, 2, 3), ctx.sm_scale,
-                                        attn_sink=sink, merge_kv=True)
-        grad_kv = dk.squeeze(2).permute(1, 0, 2)
+        grad_q = _rows(torch.empty_like(q))
+        grad_kv = _rows(torch.empty_like(kv))
+        _, _, _, dsink = sfa_backward(qb, kb, kb, idx, out.permute(1, 0, 2, 3), lse, grad_out.permute(1, 0, 2, 3),
+                                      ctx.sm_scale, attn_sink=sink, merge_kv=True, dq=grad_q.permute(1, 0, 2, 3),
+                                      dk=grad_kv.permute(1, 0, 2).unsqueeze(2))
         if dsink is not None and sink is not None:
             dsink = dsink.to(sink.dtype)
-        return dq.permute(1, 0, 2, 3), grad_kv, dsink, None, None
+        return grad_q, grad_kv, dsink, None, None
 
 
 # The reference's class name, for call sites that import it by name.

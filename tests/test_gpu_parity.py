@@ -528,7 +528,10 @@ def test_reference_signature_shim(H, D, dtypes):
         dout = torch.randn(S, B, H, D, device=DEV, generator=g).to(dtype)
         out = ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, 0.1)
         assert tuple(out.shape) == (S, B, H, D)
+        # contiguous like the reference's empty_like(q) (SFA.py:104): views work
+        assert out.is_contiguous() and out.view(S, B, H * D).shape == (S, B, H * D)
         out.backward(dout)
+        assert q.grad.is_contiguous() and kv.grad.is_contiguous()
         qb = q.detach().permute(1, 0, 2, 3).cpu()
         kb = kv.detach().permute(1, 0, 2).unsqueeze(2).cpu()
         ib = idx.permute(1, 0, 2).unsqueeze(2).cpu()
