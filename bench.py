@@ -559,6 +559,20 @@ def profile_targets(name):
         w = make_workload("mla_prefill", device="cuda", with_dout=True)
         out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale)
         return lambda: ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True), None
+    if name in ("shim_fwd", "shim_bwd"):
+        # the reference-signature shape of bench_shim: S = 4096, H = 64 on one
+        # kv row, D = 128, top-k 2048, a sink (SBHD views of the BSHD workload)
+        w = make_workload("prefill", device="cuda", S=4096, Hq=64, K=2048, with_dout=True)
+        q = w.q.permute(1, 0, 2, 3).contiguous()
+        kv = w.k[:, :, 0].permute(1, 0, 2).contiguous()
+        idx = w.idx[:, :, 0].permute(1, 0, 2).contiguous()
+        sink = torch.linspace(-1.0, 1.0, q.shape[2], device="cuda")
+        if name == "shim_fwd":
+            return lambda: ops_amd.SparseFlashAttentionTriton.apply(q, kv, sink, idx, w.scale), None
+        qg, kvg, sg = q.requires_grad_(True), kv.requires_grad_(True), sink.requires_grad_(True)
+        out = ops_amd.SparseFlashAttentionTriton.apply(qg, kvg, sg, idx, w.scale)
+        dout = w.dout.permute(1, 0, 2, 3).contiguous()
+        return lambda: torch.autograd.grad(out, (qg, kvg, sg), dout, retain_graph=True), None
     raise SystemExit(f"unknown --profile target {name!r}")
 
 
@@ -860,7 +874,7 @@ def main():
     ap.add_argument("--profile", default="", metavar="NAME",
                     help="only launch workload NAME's kernels `steps` times (for counter runs) and exit: "
                          "mla_prefill, prefill, train_gqa_fwd, train_gqa_bwd_csr, train_gqa_bwd_atomic, "
-                         "mla_decode, mla_decode_paged, mla_bwd")
+                         "mla_decode, mla_decode_paged, mla_bwd, shim_fwd, shim_bwd")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("DIR", "OUT_JSON"),
                     help="summarise counter CSVs under DIR/<target>_<pass>/ (passes = PMC_PASSES) into "
                          "OUT_JSON, print markdown tables, and exit (needs no GPU)")
