@@ -151,3 +151,26 @@ def test_paged_persistent_mla_prefill():
     k2, v2, i2 = paged_to_contiguous(kp.cpu(), vp.cpu(), bt.cpu(), w.idx[:, rows].cpu())
     o_r, l_r = ref_forward(w.q[:, rows].cpu().float(), k2.float(), v2.float(), i2, w.scale, None, sink.cpu())
     _check_oracle(o_p[:, rows], l_p[:, rows], o_r, l_r)
+
+
+@pytest.mark.parametrize("G", [20, 64])
+def test_paged_d128_large_groups(G):
+    """d = 128 with more than 16 query heads on one kv head (the reference's
+    shape class) over a paged pool: the paged forward runs the head-group
+    kernel (one workgroup per 16 heads), the contiguous one the shared-tile
+    kernel (the head groups as waves of one workgroup): both against the
+    oracle (with a sink and kv_lens), and bitwise equal to each other, since
+    a wave's arithmetic is the same in both kernels."""
+    _say(f"paged d=128 G={G} S=256 K=96 page=16 sink")
+    w = make_workload("prefill", device=DEV, S=256, Hq=G, K=96, seed=7)
+    sink = torch.linspace(-1.0, 2.0, G, device=DEV)
+    kv_lens = torch.tensor([200], dtype=torch.int32, device=DEV)
+    kp, vp, bt = page_kv(w.k, w.v, 16, seed=13, spare_pages=5)
+    o_c, l_c = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens, sink)
+    o_p, l_p = ops_amd.sfa_forward_paged(w.q, kp, vp, bt, w.idx, w.scale, kv_lens, sink)
+    torch.cuda.synchronize()
+    k2, v2, i2 = paged_to_contiguous(kp.cpu(), vp.cpu(), bt.cpu(), w.idx.cpu())
+    o_r, l_r = ref_forward(w.q.cpu().float(), k2.float(), v2.float(), i2, w.scale, kv_lens.cpu(), sink.cpu())
+    _check_oracle(o_p, l_p, o_r, l_r)
+    _check_oracle(o_c, l_c, o_r, l_r)
+    assert torch.equal(o_p, o_c) and torch.equal(l_p, l_c)
