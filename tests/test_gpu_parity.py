@@ -399,6 +399,27 @@ def test_mla_prefill_persistent_schedule():
     _check_fwd(out1[:, rows], lse1[:, rows], o_ref, l_ref)
 
 
+@pytest.mark.parametrize("Hq,Hkv,S", [(80, 1, 4100), (112, 1, 4100), (256, 2, 2050)])
+def test_mla_prefill_persistent_head_slices_and_kv_heads(Hq, Hkv, S):
+    """The persistent MLA forward (>= 4096 work items) with G = Hq / Hkv not a
+    multiple of the 32-head slice (the last slices hold absent heads: the
+    output rounds then wait for all their stores) or with two KV heads (work
+    items over (query, kv head)), a sink, NaN-filled outputs: every row
+    written, sampled rows against the oracle."""
+    _say(f"mla_prefill persistent Hq={Hq} Hkv={Hkv} S={S} K=256 with sink")
+    w = make_workload("mla_prefill", device=DEV, S=S, K=256, Hq=Hq, Hkv=Hkv, seed=9)
+    sink = torch.linspace(-1.5, 1.5, Hq, device=DEV)
+    out = torch.full(w.q.shape[:3] + (512,), float("nan"), dtype=w.q.dtype, device=DEV)
+    lse = torch.full(w.q.shape[:3], float("nan"), dtype=torch.float32, device=DEV)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, attn_sink=sink, out=out, lse=lse)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all()), "an output row was not written"
+    rows = torch.tensor([0, 1, 255, 1000, S // 2, S - 2, S - 1])
+    o_ref, l_ref = ref_forward(w.q[:, rows].cpu(), w.k.cpu(), w.v.cpu(), w.idx[:, rows].cpu(), w.scale,
+                               sink=sink.cpu())
+    _check_fwd(out[:, rows], lse[:, rows], o_ref, l_ref)
+
+
 def _decode_compact(w):
     """Gather the referenced rows on the GPU so the oracle sees a small KV."""
     B, K = w.idx.shape[0], w.idx.shape[3]
