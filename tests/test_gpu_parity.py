@@ -608,6 +608,26 @@ def test_mla_decode_splits_sink(splits):
     _check_fwd(out, lse, o_ref, l_ref)
 
 
+@pytest.mark.parametrize("Hq,Hkv,splits", [(100, 1, 4), (256, 2, 4), (72, 1, 2)])
+def test_mla_decode_head_counts(Hq, Hkv, splits):
+    """The split-k MLA decode and its merge at head counts other than 128 on
+    one KV head: partly empty 32-head slices (100, 72 heads) and two KV heads
+    (256 heads, work items over (sequence, kv head)), with kv_lens and a sink,
+    NaN-filled outputs: every row written, against the oracle."""
+    _say(f"mla_decode B=5 Skv=3000 Hq={Hq} Hkv={Hkv} K=512 splits={splits} sink")
+    w = make_workload("mla_decode", device=DEV, B=5, Skv=3000, K=512, Hq=Hq, Hkv=Hkv, ctx_lo=700, seed=6)
+    sink = torch.linspace(-2.0, 1.0, Hq, device=DEV)
+    out = torch.full(w.q.shape[:3] + (512,), float("nan"), dtype=w.q.dtype, device=DEV)
+    lse = torch.full(w.q.shape[:3], float("nan"), dtype=torch.float32, device=DEV)
+    out, lse = ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale, kv_lens=w.kv_lens, attn_sink=sink,
+                                   num_splits=splits, out=out, lse=lse)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all()), "an output row was not written"
+    o_ref, l_ref = ref_forward(w.q.cpu(), w.k.cpu(), w.v.cpu(), w.idx.cpu(), w.scale, kv_lens=w.kv_lens.cpu(),
+                               sink=sink.cpu())
+    _check_fwd(out, lse, o_ref, l_ref)
+
+
 @pytest.mark.parametrize("splits", [2, 4, 8])
 def test_mla_decode_any_workspace_contents(splits):
     """The C ABI's workspace is scratch: with a workspace pre-filled with
