@@ -209,8 +209,10 @@ SFA_API size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_
 SFA_API int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace,
                           size_t workspace_bytes, void* stream);
 
-/* Bytes of device workspace sfa_indexer_topk needs (the scores of a chunk of
- * queries; 0 when `logits` is given). */
+/* Bytes of device workspace sfa_indexer_topk needs (the fp32 scores of a
+ * chunk of queries: about 1 GiB, less when all Sq rows take less, more when
+ * one block of 512 / H queries of all B sequences takes more; 0 when `logits`
+ * is given). */
 SFA_API size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a);
 
 /* Scores and top-k selection (no counterpart kernel in the reference, which

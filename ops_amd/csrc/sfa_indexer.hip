@@ -43,6 +43,9 @@ namespace {
 constexpr int kD = 128;          // index head dim
 constexpr int kKT = 32;          // keys per tile
 constexpr int kLogitThreads = 256;
+constexpr int kLogitSlots = 512;       // resident scores workgroups (two per CU)
+constexpr int kLogitTargetWGs = 2048;  // workgroups a split scores launch aims for
+constexpr int kLogitMinSpan = 32;      // fewest key tiles (1024 keys) per workgroup
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
@@ -76,7 +79,8 @@ __device__ __forceinline__ int key_end(const IndexerParams& p, int b, int t) {
 }
 
 template <int H, bool F8>
-__global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(IndexerParams p, int t_begin, int t_end) {
+__global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(IndexerParams p, int t_begin, int t_end,
+                                                                           int nks, int span) {
   constexpr int QPW = 128 / H;        // queries per wave
   constexpr int HT = H / 32;          // M-tiles (32 heads) per query
   constexpr int QB = 4 * QPW;         // queries per workgroup
@@ -98,15 +102,23 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nqb = (t_end - t_begin + QB - 1) / QB;
-  // heaviest (latest) query blocks first
-  const int b = blockIdx.x / nqb;
-  const int qb = nqb - 1 - (int)(blockIdx.x % nqb);
+  // workgroup -> (sequence, query block, key split): heaviest (latest) query
+  // blocks first, the key splits of a block side by side
+  const int per_b = nqb * nks;
+  const int b = blockIdx.x / per_b;
+  const int r = (int)(blockIdx.x % per_b);
+  const int qb = nqb - 1 - r / nks;
+  const int ks = r % nks;
   const int tq0 = t_begin + qb * QB;  // first query of the workgroup
 
-  // key tiles the workgroup needs: up to the largest end among its queries
+  // key tiles of the query block: up to the largest end among its queries;
+  // this workgroup takes tiles [kt0, kt1) of them
   const int t_last = min(tq0 + QB, t_end) - 1;
   const int kend_wg = key_end(p, b, t_last);
   const int ntiles = (kend_wg + kKT - 1) / kKT;
+  const int kt0 = ks * span;
+  const int kt1 = min(kt0 + span, ntiles);
+  if (kt0 >= kt1) return;  // the whole workgroup, before any barrier
 
   // ---- q operands (A: lane l holds head 32 hg + l % 32; bf16: dims
   // 16 s + 8 (l / 32) .. + 7, fp8: dims 64 s + 32 (l / 32) .. + 31) and weights
@@ -247,22 +259,22 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
     }
   };
 
-  if (ntiles > 0) load_tile(0, s_k0);
-  // the weights go to LDS once tile 0 is in flight (a load under the lane
+  load_tile(kt0, s_k0);
+  // the weights go to LDS once tile kt0 is in flight (a load under the lane
   // test would be waited for where issued, before the tile's DMA)
   if (lg == 0) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) s_w[(wave * 4 + mt) * 32 + hl] = wv[mt];
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();                     // tile 0 and the weights are in place
-  for (int kt = 0; kt < ntiles; kt += 2) {
-    if (kt + 1 < ntiles) load_tile(kt + 1, s_k1);
+  __syncthreads();                     // tile kt0 and the weights are in place
+  for (int kt = kt0; kt < kt1; kt += 2) {
+    if (kt + 1 < kt1) load_tile(kt + 1, s_k1);
     compute(kt, s_k0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // tile kt + 1 has landed
     __syncthreads();                     // and every wave is done with tile kt
-    if (kt + 1 < ntiles) {
-      if (kt + 2 < ntiles) load_tile(kt + 2, s_k0);
+    if (kt + 1 < kt1) {
+      if (kt + 2 < kt1) load_tile(kt + 2, s_k0);
       compute(kt + 1, s_k1);
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
@@ -499,25 +511,40 @@ int indexer_query_block(const IndexerParams& p) { return 4 * (128 / p.H); }
 
 hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
   const int qb = indexer_query_block(p);
-  const int64_t n = (int64_t)p.B * ((t_end - t_begin + qb - 1) / qb);
-  if (n == 0) return hipSuccess;
-  const dim3 g((unsigned)n), blk(kLogitThreads);
+  const int64_t nblk = (int64_t)p.B * ((t_end - t_begin + qb - 1) / qb);
+  if (nblk == 0) return hipSuccess;
+  // Key splits, for launches with fewer query blocks than workgroup slots (a
+  // decode step: one query per sequence): a query block's key tiles are
+  // shared by nks workgroups of span tiles each, so that the launch holds
+  // about kLogitTargetWGs workgroups.  A split holds at least kLogitMinSpan
+  // tiles.  Launches with more query blocks than slots are not split: every
+  // split re-reads its block's q (128 KB for 64 heads) from HBM, which cost
+  // more on the S = 32768 prefill than the balance it bought.
+  const int kend_max = std::max(0, std::min(t_end + p.Skv - p.Sq, p.Skv));  // key_end of the last query, L = Skv
+  const int ntiles_max = (kend_max + kKT - 1) / kKT;
+  int nks = 1;
+  if (nblk < kLogitSlots && ntiles_max > kLogitMinSpan) {
+    const int64_t want = (kLogitTargetWGs + nblk - 1) / nblk;
+    nks = (int)std::min<int64_t>(want, (ntiles_max + kLogitMinSpan - 1) / kLogitMinSpan);
+  }
+  const int span = std::max(1, (ntiles_max + nks - 1) / nks);
+  const dim3 g((unsigned)(nblk * nks)), blk(kLogitThreads);
   if (p.fp8) {
     if (p.H == 64)
-      hipLaunchKernelGGL((indexer_logits_kernel<64, true>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<64, true>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else if (p.H == 32)
-      hipLaunchKernelGGL((indexer_logits_kernel<32, true>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<32, true>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else if (p.H == 128)
-      hipLaunchKernelGGL((indexer_logits_kernel<128, true>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<128, true>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else
       return hipErrorNotSupported;
   } else {
     if (p.H == 64)
-      hipLaunchKernelGGL((indexer_logits_kernel<64, false>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<64, false>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else if (p.H == 32)
-      hipLaunchKernelGGL((indexer_logits_kernel<32, false>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<32, false>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else if (p.H == 128)
-      hipLaunchKernelGGL((indexer_logits_kernel<128, false>), g, blk, 0, s, p, t_begin, t_end);
+      hipLaunchKernelGGL((indexer_logits_kernel<128, false>), g, blk, 0, s, p, t_begin, t_end, nks, span);
     else
       return hipErrorNotSupported;
   }

@@ -144,6 +144,38 @@ def test_indexer_decode_shape():
         assert float((sc - ref).abs().max()) <= SCORE_RTOL * float(ref.abs().max())
 
 
+@pytest.mark.parametrize("H,fp8", [(64, False), (32, False), (128, False), (64, True)],
+                         ids=["h64", "h32", "h128", "h64-fp8"])
+def test_indexer_key_splits(H, fp8):
+    """A launch with fewer query blocks than the scores kernel's 512 slots
+    splits each block's keys over several workgroups of 32 tiles (1024 keys):
+    here 3 sequences of up to 5000 keys (5 splits per block), kv_lens that
+    end one sequence inside its third split and leave another only part of
+    its first tile (the later splits exit at once), and 5 queries per
+    sequence.  Every visible score against the oracle, the selection exact."""
+    B, Sq, Skv, K = 3, 5, 5000, 100
+    _say(f"indexer key splits B={B} Sq={Sq} Skv={Skv} H={H} K={K} fp8={fp8}")
+    kv_lens = torch.tensor([5000, 2100, 40], dtype=torch.int32, device=DEV)
+    ks = None
+    if fp8:
+        q, k, w, ks = _fp8_inputs(B, Sq, Skv, H, seed=31)
+    else:
+        q, k, w = _inputs(B, Sq, Skv, H, seed=31 + H)
+    idx, logits = ops_amd.indexer_topk(q, k, w, K, kv_lens=kv_lens, return_logits=True, k_scale=ks)
+    torch.cuda.synchronize()
+    idx, logits = idx.cpu(), logits.cpu()
+    end = indexer_key_end(B, Sq, Skv, kv_lens.cpu())
+    ref = indexer_scores(q.cpu().float(), k.cpu().float(), w.cpu(), kv_lens.cpu(),
+                         k_scale=None if ks is None else ks.cpu())
+    vis = torch.arange(Skv)[None, None, :] < end[:, :, None]
+    scale = float(ref[vis].abs().max())
+    err = float((logits[vis] - ref[vis]).abs().max())
+    assert err <= SCORE_RTOL * scale, f"score error {err} vs scale {scale}"
+    own = torch.where(vis, logits, torch.full_like(logits, -math.inf))
+    assert torch.equal(idx, indexer_topk(own, K, end))
+    _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
+
+
 def test_indexer_feeds_mla_forward():
     # producer -> consumer: index rows from the indexer drive the MLA forward
     B, S, Hq, K, H = 1, 384, 128, 64, 64
