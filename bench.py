@@ -485,15 +485,32 @@ def bench_shim(args):
                        "H": 64, "D": 128, "topk": 2048}}
 
 
+def indexer_inputs(kind):
+    """Index-producer inputs (64 index heads, d = 128, bf16 q / k, fp32
+    weights): "prefill" = one causal sequence of 32768 queries over its own
+    keys; "decode" = one query for each of 64 sequences over a 65536-key
+    cache whose lengths are the decode workload's (16K-64K)."""
+    import torch
+    H = 64
+    if kind == "prefill":
+        B, Sq, Skv, kv_lens = 1, 32768, 32768, None
+    else:
+        from ops_amd.workloads import decode_context_lens
+        B, Sq, Skv = 64, 1, 65536
+        kv_lens = decode_context_lens(device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    q = torch.randn(B, Sq, H, 128, generator=g, device="cuda").bfloat16()
+    k = torch.randn(B, Skv, 128, generator=g, device="cuda").bfloat16()
+    w = torch.randn(B, Sq, H, generator=g, device="cuda") / math.sqrt(H)
+    return q, k, w, kv_lens
+
+
 def bench_indexer(args, mla=None):
     import torch
     import ops_amd
     B, S, H, K = 1, 32768, 64, 2048
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0)
-    q = torch.randn(B, S, H, 128, generator=g, device="cuda").bfloat16()
-    k = torch.randn(B, S, 128, generator=g, device="cuda").bfloat16()
-    w = torch.randn(B, S, H, generator=g, device="cuda") / math.sqrt(H)
+    q, k, w, _ = indexer_inputs("prefill")
     fn = lambda: ops_amd.indexer_topk(q, k, w, K)
     times, _ = time_steps(fn, max(2, args.steps // 2), 1)
     ms = sum(times) / len(times)
@@ -515,6 +532,19 @@ def bench_indexer(args, mla=None):
     res["fp8"] = {"value": flops / (fms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms": fms,
                   "note": "fp8 e4m3 q / k, per-token k scales; TFLOP/s over the same visible pairs"}
     del q8, k8
+    # a decode step's index rows: one query for each of 64 sequences over
+    # 16K-64K keys (HBM-bound: every visible key row is read once)
+    qd, kd, wd, lens = indexer_inputs("decode")
+    dt, _ = time_steps(lambda: ops_amd.indexer_topk(qd, kd, wd, K, kv_lens=lens), max(5, args.steps), 2,
+                       before=decode_flush())
+    dms = sum(dt) / len(dt)
+    key_bytes = int(lens.sum()) * 128 * 2
+    res["decode"] = {"ms": dms, "key_gbs": key_bytes / (dms * 1e-3) / 1e9,
+                     "frac_of_hbm": key_bytes / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "note": "key rows read (bf16, 256 B per visible key) per second; caches flushed per step",
+                     "config": {"B": 64, "Sq": 1, "Skv": 65536, "kv_lens": "16384-65536", "H_index": 64,
+                                "d_index": 128, "topk": K}}
+    del qd, kd, wd
     if mla is not None:
         out = torch.empty(mla.q.shape[:3] + (mla.v.shape[3],), dtype=mla.q.dtype, device="cuda")
         lse = torch.empty(mla.q.shape[:3], dtype=torch.float32, device="cuda")
@@ -573,6 +603,9 @@ def profile_targets(name):
         out = ops_amd.SparseFlashAttentionTriton.apply(qg, kvg, sg, idx, w.scale)
         dout = w.dout.permute(1, 0, 2, 3).contiguous()
         return lambda: torch.autograd.grad(out, (qg, kvg, sg), dout, retain_graph=True), None
+    if name in ("indexer_prefill", "indexer_decode"):
+        q, k, w, kv_lens = indexer_inputs(name.split("_")[1])
+        return lambda: ops_amd.indexer_topk(q, k, w, 2048, kv_lens=kv_lens), None
     raise SystemExit(f"unknown --profile target {name!r}")
 
 

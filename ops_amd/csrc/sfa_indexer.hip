@@ -46,8 +46,12 @@ constexpr int kLogitThreads = 256;
 constexpr int kLogitSlots = 512;       // resident scores workgroups (two per CU)
 constexpr int kLogitTargetWGs = 2048;  // workgroups a split scores launch aims for
 constexpr int kLogitMinSpan = 32;      // fewest key tiles (1024 keys) per workgroup
+constexpr int kOneQMaxSq = 2;          // queries per sequence up to which the one-query kernel runs
+constexpr int kOneQTargetWGs = 4096;   // workgroups a one-query launch aims for
+constexpr int kOneQMinSpan = 16;       // fewest key tiles per one-query workgroup (4 per wave)
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // Operand geometry of the scores kernel per element type.  bf16: 32x32x16
 // MFMA, 8 contraction steps of 16 dims, a key row is 16 chunks of 16 bytes;
@@ -282,6 +286,140 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
   }
 }
 
+// One query per workgroup (the decode shape: a sequence or two of queries
+// per cache, where the 128 / H-query blocks above would compute for empty
+// query slots).  The query's H heads are the MFMA rows (H / 32 M-tiles, the
+// operands in VGPRs), and every wave streams its own 32-key tiles (tiles
+// kt0 + wave, kt0 + wave + 4, ... of the workgroup's split) straight from
+// global memory into B-operand registers, NB tiles in flight: no LDS tile,
+// no barrier after the weights are in place.  The B operand of lane l holds
+// key l % 32 and, for lane half h = l / 32, a contiguous half row: bf16 dims
+// 64 h + 8 s .. + 7 at contraction step s (16 bytes of the 128-byte half),
+// fp8 dims 64 h + 32 s .. + 31.  The q operand of head l % 32 holds the same
+// dims, so every step contracts matching dims and the eight (bf16) or two
+// (fp8) steps cover all 128.  The epilogue is the block kernel's: weighted
+// ReLU over the heads in registers, then the lane pair l, l ^ 32; lanes 0-31
+// store the tile's 32 scores.
+template <int H, bool F8, int NB>
+__global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(IndexerParams p, int t_begin, int t_end,
+                                                                              int nks, int span) {
+  constexpr int HT = H / 32;  // M-tiles
+  using M = Mfma<32>;
+  typedef typename M::acc_t acc_t;
+  typedef IdxOps<F8> O;
+  typedef typename O::op_t op_t;
+  constexpr int kHalf = F8 ? 64 : 128;  // bytes of a key row per lane half
+  __shared__ float s_w[H];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // workgroup -> (sequence, query, key split)
+  const int nq = t_end - t_begin;
+  const int per_b = nq * nks;
+  const int b = blockIdx.x / per_b;
+  const int r = (int)(blockIdx.x % per_b);
+  const int t = t_begin + r / nks;
+  const int ks = r % nks;
+  const int kend = key_end(p, b, t);
+  const int ntiles = (kend + kKT - 1) / kKT;
+  const int kt0 = ks * span;
+  const int kt1 = min(kt0 + span, ntiles);
+  if (kt0 >= kt1) return;  // the whole workgroup, before the barrier
+
+  const int hl = lane & 31, lg = lane >> 5;
+  const float* wrow = p.w + b * p.w_sb + t * p.w_ss;
+  for (int h = tid; h < H; h += kLogitThreads) s_w[h] = wrow[h];
+  op_t qa[HT][O::kSteps];
+#pragma unroll
+  for (int mt = 0; mt < HT; ++mt) {
+    const char* qrow = reinterpret_cast<const char*>(p.q) +
+                       O::kElem * (b * p.q_sb + t * p.q_ss + (int64_t)(mt * 32 + hl) * p.q_sh) + kHalf * lg;
+#pragma unroll
+    for (int s = 0; s < O::kSteps; ++s) {
+      if constexpr (F8) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(qrow + 32 * s);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 16);
+        qa[mt][s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      } else {
+        qa[mt][s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
+      }
+    }
+  }
+  __syncthreads();  // the weights are in place
+  int kt = kt0 + wave;
+  if (kt >= kt1) return;  // this wave has no tile (no barrier follows)
+
+  const char* kbase = reinterpret_cast<const char*>(p.k) + O::kElem * (b * p.k_sb);
+  const uint32_t krow = (uint32_t)(O::kElem * p.k_ss);
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(kbase, (uint32_t)(O::kElem * ((int64_t)(p.Skv - 1) * p.k_ss + kD)));
+  float* orow = p.logits + b * p.g_sb + (int64_t)(t - p.g_t0) * p.g_ss;
+
+  auto load = [&](int kt_, op_t* kb) {
+    const int key = kt_ * kKT + hl;
+    const uint32_t base = key < kend ? __umul24((uint32_t)key, krow) + (uint32_t)(kHalf * lg) : kOOB;
+#pragma unroll
+    for (int s = 0; s < O::kSteps; ++s) {
+      if constexpr (F8) {
+        const i32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 32u * s, 0, 0);
+        const i32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 32u * s + 16u, 0, 0);
+        kb[s] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      } else {
+        kb[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, base + 16u * s, 0, 0));
+      }
+    }
+  };
+  auto compute = [&](int kt_, const op_t* kb) {
+    acc_t acc[HT];
+#pragma unroll
+    for (int mt = 0; mt < HT; ++mt) acc[mt] = acc_t{};
+#pragma unroll
+    for (int s = 0; s < O::kSteps; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < HT; ++mt) {
+        if constexpr (F8)
+          acc[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mt][s], kb[s], acc[mt], 0, 0, 0, 0, 0, 0);
+        else
+          acc[mt] = M::mma(qa[mt][s], kb[s], acc[mt]);
+      }
+    }
+    // accumulator element e of M-tile mt: head 32 mt + 8 (e / 4) + 4 lg + e % 4
+    float x = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < HT; ++mt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x4 w4 = *reinterpret_cast<const f32x4*>(&s_w[mt * 32 + 8 * g4 + 4 * lg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x = fmaf(w4[e], fmaxf(acc[mt][4 * g4 + e], 0.f), x);
+      }
+    }
+    x = xor32_sum(x);
+    const int key = kt_ * kKT + hl;
+    if constexpr (F8) {
+      if (p.k_scale) x *= key < p.Skv ? p.k_scale[b * p.ks_sb + key] : 0.f;
+    }
+    if (lg == 0 && key < p.Skv) orow[key] = key < kend ? x : kNegInf;
+  };
+
+  // a ring of NB register tiles: tile i + NB - 1 is issued before tile i is used
+  op_t kb[NB][O::kSteps];
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j)
+    if (kt + 4 * j < kt1) load(kt + 4 * j, kb[j]);
+  for (; kt < kt1; kt += 4 * NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int cur = kt + 4 * j;
+      if (cur < kt1) {
+        const int nxt = cur + 4 * (NB - 1);
+        if (nxt < kt1) load(nxt, kb[(j + NB - 1) % NB]);
+        compute(cur, kb[j]);
+      }
+    }
+  }
+}
+
 // Order-preserving map of a float to u32 (larger float -> larger key).
 __device__ __forceinline__ uint32_t order_key(float x) {
   const uint32_t u = __float_as_uint(x);
@@ -509,7 +647,44 @@ __global__ __launch_bounds__(kSelThreads, MAXNG <= 8 ? 8 : 1) void topk_select_k
 
 int indexer_query_block(const IndexerParams& p) { return 4 * (128 / p.H); }
 
+namespace {
+
+// One-query scores launch: B x (t_end - t_begin) queries, each query's key
+// tiles split over workgroups of at least kOneQMinSpan tiles (4 per wave) so
+// that the launch holds about kOneQTargetWGs workgroups.
+template <int H, bool F8>
+hipError_t launch_logits_1q(const IndexerParams& p, int t_begin, int t_end, int ntiles_max, hipStream_t s) {
+  constexpr int NB = 2;  // register tiles in flight per wave
+  const int64_t nqry = (int64_t)p.B * (t_end - t_begin);
+  int nks = 1;
+  if (nqry < kOneQTargetWGs && ntiles_max > kOneQMinSpan) {
+    const int64_t want = (kOneQTargetWGs + nqry - 1) / nqry;
+    nks = (int)std::min<int64_t>(want, (ntiles_max + kOneQMinSpan - 1) / kOneQMinSpan);
+  }
+  const int span = std::max(1, (ntiles_max + nks - 1) / nks);
+  hipLaunchKernelGGL((indexer_logits_1q_kernel<H, F8, NB>), dim3((unsigned)(nqry * nks)), dim3(kLogitThreads), 0, s,
+                     p, t_begin, t_end, nks, span);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
+  if (t_end <= t_begin || p.B == 0) return hipSuccess;
+  // the one-query kernel for H <= 64 (at H = 128 its q operands alone take
+  // 128 VGPRs and the kernel spills; the block kernel's 4-query blocks serve)
+  if (p.Sq <= kOneQMaxSq && p.H <= 64) {
+    const int kend_max = std::max(0, std::min(t_end + p.Skv - p.Sq, p.Skv));
+    const int ntiles_max = (kend_max + kKT - 1) / kKT;
+    if (p.fp8) {
+      if (p.H == 64) return launch_logits_1q<64, true>(p, t_begin, t_end, ntiles_max, s);
+      if (p.H == 32) return launch_logits_1q<32, true>(p, t_begin, t_end, ntiles_max, s);
+    } else {
+      if (p.H == 64) return launch_logits_1q<64, false>(p, t_begin, t_end, ntiles_max, s);
+      if (p.H == 32) return launch_logits_1q<32, false>(p, t_begin, t_end, ntiles_max, s);
+    }
+    return hipErrorNotSupported;
+  }
   const int qb = indexer_query_block(p);
   const int64_t nblk = (int64_t)p.B * ((t_end - t_begin + qb - 1) / qb);
   if (nblk == 0) return hipSuccess;

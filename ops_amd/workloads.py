@@ -71,6 +71,20 @@ def _gen(device, seed: int, tid: int) -> torch.Generator:
     return g
 
 
+def _context_lens(spec: dict, Skv: int, device, seed: int) -> torch.Tensor:
+    """Decode context lengths: uniform in [ctx_lo, Skv] per sequence (int64)."""
+    lo = spec.get("ctx_lo", Skv // 4)
+    return torch.randint(lo, Skv + 1, (spec["B"],), generator=_gen(device, seed, 5), device=device,
+                         dtype=torch.int64)
+
+
+def decode_context_lens(device="cpu", seed: int = 0, **overrides) -> torch.Tensor:
+    """The mla_decode workload's kv_lens (int32 ``[B]``) without building its
+    cache: the same draw as ``make_workload("mla_decode", ...).kv_lens``."""
+    spec = workload_spec("mla_decode", **overrides)
+    return _context_lens(spec, spec["Skv"], device, seed).to(torch.int32)
+
+
 def _randn(shape, dtype, device, gen, chunk_rows: int = 1 << 22):
     """N(0,1) drawn in fp32 then cast, in chunks along dim 0's flattened rows."""
     out = torch.empty(shape, dtype=dtype, device=device)
@@ -280,9 +294,7 @@ def make_workload(name: str, device="cpu", seed: int = 0, with_dout: Optional[bo
             gidx = _mla_prefill_idx(S, K, win, n_recent, device, _gen(device, seed, 4))
             idx = gidx.view(1, S, 1, K).expand(B, S, Hkv, K).contiguous()
         else:
-            lo = spec.get("ctx_lo", Skv // 4)
-            gctx = _gen(device, seed, 5)
-            ctx = torch.randint(lo, Skv + 1, (B,), generator=gctx, device=device, dtype=torch.int64)
+            ctx = _context_lens(spec, Skv, device, seed)
             kv_lens = ctx.to(torch.int32)
             gidx = _decode_idx(B, K, ctx, Skv, device, _gen(device, seed, 4))
             idx = gidx.view(B, 1, 1, K).expand(B, 1, Hkv, K).contiguous()
