@@ -47,7 +47,7 @@ constexpr int kLogitSlots = 512;       // resident scores workgroups (two per CU
 constexpr int kLogitTargetWGs = 2048;  // workgroups a split scores launch aims for
 constexpr int kLogitMinSpan = 32;      // fewest key tiles (1024 keys) per workgroup
 constexpr int kOneQMaxSq = 2;          // queries per sequence up to which the one-query kernel runs
-constexpr int kOneQTargetWGs = 4096;   // workgroups a one-query launch aims for
+constexpr int kOneQTargetWGs = 16384;   // workgroups a one-query launch aims for
 constexpr int kOneQMinSpan = 16;       // fewest key tiles per one-query workgroup (4 per wave)
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -287,19 +287,19 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_kernel(Indexe
 }
 
 // One query per workgroup (the decode shape: a sequence or two of queries
-// per cache, where the 128 / H-query blocks above would compute for empty
-// query slots).  The query's H heads are the MFMA rows (H / 32 M-tiles, the
-// operands in VGPRs), and every wave streams its own 32-key tiles (tiles
-// kt0 + wave, kt0 + wave + 4, ... of the workgroup's split) straight from
-// global memory into B-operand registers, NB tiles in flight: no LDS tile,
-// no barrier after the weights are in place.  The B operand of lane l holds
-// key l % 32 and, for lane half h = l / 32, a contiguous half row: bf16 dims
-// 64 h + 8 s .. + 7 at contraction step s (16 bytes of the 128-byte half),
-// fp8 dims 64 h + 32 s .. + 31.  The q operand of head l % 32 holds the same
-// dims, so every step contracts matching dims and the eight (bf16) or two
-// (fp8) steps cover all 128.  The epilogue is the block kernel's: weighted
-// ReLU over the heads in registers, then the lane pair l, l ^ 32; lanes 0-31
-// store the tile's 32 scores.
+// per cache, where the 512 / H-query blocks above would compute for empty
+// query slots).  The query's H heads are the MFMA rows (H / 32 M-tiles): the
+// workgroup copies its q row and head weights into LDS once, and every wave
+// streams its own 32-key tiles (tiles kt0 + wave, kt0 + wave + 4, ... of the
+// workgroup's split) straight from global memory into B-operand registers,
+// NB tiles in flight, taking the q operands from LDS per tile (which keeps
+// the kernel at 126 VGPRs, four waves per SIMD, for H = 64).  Operand layout
+// as in the block kernel: lane l holds key (B) or head (A) l % 32 and, for
+// lane half h = l / 32, bf16 dims 16 s + 8 h .. + 7 at contraction step s
+// (fp8: 64 s + 32 h .. + 31), so a load instruction reads 32 contiguous
+// bytes of each of 32 key rows.  The epilogue is the block kernel's:
+// weighted ReLU over the heads in registers, then the lane pair l, l ^ 32;
+// lanes 0-31 store the tile's 32 scores.
 template <int H, bool F8, int NB>
 __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(IndexerParams p, int t_begin, int t_end,
                                                                               int nks, int span) {
@@ -308,8 +308,8 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
   typedef typename M::acc_t acc_t;
   typedef IdxOps<F8> O;
   typedef typename O::op_t op_t;
-  constexpr int kHalf = F8 ? 64 : 128;  // bytes of a key row per lane half
   __shared__ float s_w[H];
+  __shared__ u32x4 s_q[H * O::kPitch];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -327,25 +327,29 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
   if (kt0 >= kt1) return;  // the whole workgroup, before the barrier
 
   const int hl = lane & 31, lg = lane >> 5;
+  // the query's heads into LDS once (row pitch: the row's chunks + 1, so the
+  // operand reads of 16 consecutive heads hit distinct banks), the weights
+  // beside them; each wave then takes its q operands from there
   const float* wrow = p.w + b * p.w_sb + t * p.w_ss;
   for (int h = tid; h < H; h += kLogitThreads) s_w[h] = wrow[h];
-  op_t qa[HT][O::kSteps];
-#pragma unroll
-  for (int mt = 0; mt < HT; ++mt) {
-    const char* qrow = reinterpret_cast<const char*>(p.q) +
-                       O::kElem * (b * p.q_sb + t * p.q_ss + (int64_t)(mt * 32 + hl) * p.q_sh) + kHalf * lg;
-#pragma unroll
-    for (int s = 0; s < O::kSteps; ++s) {
-      if constexpr (F8) {
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(qrow + 32 * s);
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 16);
-        qa[mt][s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      } else {
-        qa[mt][s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
-      }
-    }
+  const char* qbase = reinterpret_cast<const char*>(p.q) + O::kElem * (b * p.q_sb + t * p.q_ss);
+  for (int c = tid; c < H * O::kChunks; c += kLogitThreads) {
+    const int h = c / O::kChunks, ch = c - h * O::kChunks;
+    s_q[h * O::kPitch + ch] = *reinterpret_cast<const u32x4*>(qbase + O::kElem * (int64_t)h * p.q_sh + 16 * ch);
   }
-  __syncthreads();  // the weights are in place
+  __syncthreads();  // q and the weights are in place
+  // A operand of head 32 mt + l % 32 at step s: bf16 chunk 2 s + lg (dims
+  // 16 s + 8 lg ..), fp8 chunks 4 s + 2 lg, + 1 (dims 64 s + 32 lg ..)
+  auto qop = [&](int mt, int s) -> op_t {
+    const u32x4* qrow = s_q + (mt * 32 + hl) * O::kPitch;
+    if constexpr (F8) {
+      const u32x4 lo = qrow[4 * s + 2 * lg];
+      const u32x4 hi = qrow[4 * s + 2 * lg + 1];
+      return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    } else {
+      return __builtin_bit_cast(bf16x8, qrow[2 * s + lg]);
+    }
+  };
   int kt = kt0 + wave;
   if (kt >= kt1) return;  // this wave has no tile (no barrier follows)
 
@@ -355,21 +359,25 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
       make_rsrc(kbase, (uint32_t)(O::kElem * ((int64_t)(p.Skv - 1) * p.k_ss + kD)));
   float* orow = p.logits + b * p.g_sb + (int64_t)(t - p.g_t0) * p.g_ss;
 
-  auto load = [&](int kt_, op_t* kb) {
-    const int key = kt_ * kKT + hl;
-    const uint32_t base = key < kend ? __umul24((uint32_t)key, krow) + (uint32_t)(kHalf * lg) : kOOB;
+  // tile i of this wave: kt + 4 i, i < n; the loads are issued without a
+  // branch (tiles past the wave's last read nothing: offset kOOB), so the
+  // compiler's wait counts stay exact and NB - 1 tiles stay in flight
+  const int n = (kt1 - kt + 3) / 4;
+  auto load = [&](int i, op_t* kb) {
+    const int key = (kt + 4 * i) * kKT + hl;
+    const uint32_t base = (i < n && key < kend) ? __umul24((uint32_t)key, krow) + (uint32_t)((F8 ? 32 : 16) * lg) : kOOB;
 #pragma unroll
     for (int s = 0; s < O::kSteps; ++s) {
       if constexpr (F8) {
-        const i32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 32u * s, 0, 0);
-        const i32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 32u * s + 16u, 0, 0);
+        const i32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 64u * s, 0, 0);
+        const i32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rk, base + 64u * s + 16u, 0, 0);
         kb[s] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       } else {
-        kb[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, base + 16u * s, 0, 0));
+        kb[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, base + 32u * s, 0, 0));
       }
     }
   };
-  auto compute = [&](int kt_, const op_t* kb) {
+  auto compute = [&](int i, const op_t* kb) {
     acc_t acc[HT];
 #pragma unroll
     for (int mt = 0; mt < HT; ++mt) acc[mt] = acc_t{};
@@ -378,9 +386,9 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
 #pragma unroll
       for (int mt = 0; mt < HT; ++mt) {
         if constexpr (F8)
-          acc[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mt][s], kb[s], acc[mt], 0, 0, 0, 0, 0, 0);
+          acc[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qop(mt, s), kb[s], acc[mt], 0, 0, 0, 0, 0, 0);
         else
-          acc[mt] = M::mma(qa[mt][s], kb[s], acc[mt]);
+          acc[mt] = M::mma(qop(mt, s), kb[s], acc[mt]);
       }
     }
     // accumulator element e of M-tile mt: head 32 mt + 8 (e / 4) + 4 lg + e % 4
@@ -395,7 +403,7 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
       }
     }
     x = xor32_sum(x);
-    const int key = kt_ * kKT + hl;
+    const int key = (kt + 4 * i) * kKT + hl;
     if constexpr (F8) {
       if (p.k_scale) x *= key < p.Skv ? p.k_scale[b * p.ks_sb + key] : 0.f;
     }
@@ -405,17 +413,16 @@ __global__ __launch_bounds__(kLogitThreads, 2) void indexer_logits_1q_kernel(Ind
   // a ring of NB register tiles: tile i + NB - 1 is issued before tile i is used
   op_t kb[NB][O::kSteps];
 #pragma unroll
-  for (int j = 0; j < NB - 1; ++j)
-    if (kt + 4 * j < kt1) load(kt + 4 * j, kb[j]);
-  for (; kt < kt1; kt += 4 * NB) {
+  for (int j = 0; j < NB - 1; ++j) load(j, kb[j]);
+  for (int i = 0; i < n; i += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int cur = kt + 4 * j;
-      if (cur < kt1) {
-        const int nxt = cur + 4 * (NB - 1);
-        if (nxt < kt1) load(nxt, kb[(j + NB - 1) % NB]);
-        compute(cur, kb[j]);
-      }
+      if (i + j >= n) break;
+      load(i + j + NB - 1, kb[(j + NB - 1) % NB]);
+      // keep the next tile's loads ahead of this tile's MFMAs (the scheduler
+      // would sink them below and reuse the registers of a pending load)
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i + j, kb[j]);
     }
   }
 }
@@ -494,15 +501,24 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
     for (int e = 0; e < 4; ++e) u[4 * v + e] = (4 * v + e < cnt) ? order_key(x[e]) : 0u;
   }
   // the K-th largest key, bit by bit from the top (a wave counts with
-  // ballots: one compare and a scalar popcount per score register)
+  // ballots: one compare and a scalar popcount per score register; with 64
+  // scores per thread the 64 ballot masks would not fit the SGPRs and the
+  // compiler spills them into VGPR lanes, so that instance counts per lane
+  // and sums the wave once per step)
   uint32_t thr = 0;
   auto block_steps = [&](int hi, int lo) {
 #pragma unroll 1
     for (int bit = hi; bit >= lo; --bit) {
       const uint32_t cand = thr | (1u << bit);
       int c = 0;
+      if constexpr (EPT >= 64) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) c += __popcll(__ballot(u[e] >= cand));
+        for (int e = 0; e < EPT; ++e) c += u[e] >= cand ? 1 : 0;
+        c = __builtin_amdgcn_readfirstlane(wave_sum_int(c));
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) c += __popcll(__ballot(u[e] >= cand));
+      }
       if (block_sum_waves(c, red, bit & 1) >= K) thr = cand;
     }
   };
@@ -671,17 +687,17 @@ hipError_t launch_logits_1q(const IndexerParams& p, int t_begin, int t_end, int 
 
 hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
   if (t_end <= t_begin || p.B == 0) return hipSuccess;
-  // the one-query kernel for H <= 64 (at H = 128 its q operands alone take
-  // 128 VGPRs and the kernel spills; the block kernel's 4-query blocks serve)
-  if (p.Sq <= kOneQMaxSq && p.H <= 64) {
+  if (p.Sq <= kOneQMaxSq) {
     const int kend_max = std::max(0, std::min(t_end + p.Skv - p.Sq, p.Skv));
     const int ntiles_max = (kend_max + kKT - 1) / kKT;
     if (p.fp8) {
       if (p.H == 64) return launch_logits_1q<64, true>(p, t_begin, t_end, ntiles_max, s);
       if (p.H == 32) return launch_logits_1q<32, true>(p, t_begin, t_end, ntiles_max, s);
+      if (p.H == 128) return launch_logits_1q<128, true>(p, t_begin, t_end, ntiles_max, s);
     } else {
       if (p.H == 64) return launch_logits_1q<64, false>(p, t_begin, t_end, ntiles_max, s);
       if (p.H == 32) return launch_logits_1q<32, false>(p, t_begin, t_end, ntiles_max, s);
+      if (p.H == 128) return launch_logits_1q<128, false>(p, t_begin, t_end, ntiles_max, s);
     }
     return hipErrorNotSupported;
   }

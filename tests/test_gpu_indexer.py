@@ -148,17 +148,16 @@ def test_indexer_decode_shape():
                                       (64, False, 1), (64, False, 2), (32, False, 1), (64, True, 1), (32, True, 2),
                                       (128, False, 1)],
                          ids=["h64", "h32", "h128", "h64-fp8", "1q-h64", "1q-h64-sq2", "1q-h32", "1q-h64-fp8",
-                              "1q-h32-fp8-sq2", "h128-sq1"])
+                              "1q-h32-fp8-sq2", "1q-h128"])
 def test_indexer_key_splits(H, fp8, Sq):
     """Launches with few queries split each query's (or query block's) keys
     over several workgroups: 3 sequences of up to 5000 keys, kv_lens that end
     one sequence inside its third split of 1024 keys and leave another only
     part of its first tile (the later splits exit at once).  With 5 queries
-    per sequence the block kernel runs (5 splits per block); with 1 or 2 and
-    H <= 64 the one-query kernel (splits of 16 tiles, each wave streaming its
-    own tiles, a wave with no tile idle); H = 128 with 1 query takes the
-    block kernel.  Every visible score against the oracle, the selection
-    exact."""
+    per sequence the block kernel runs (5 splits per block); with 1 or 2 the
+    one-query kernel (splits of 16 tiles, each wave streaming its own tiles,
+    a wave with no tile idle).  Every visible score against the oracle, the
+    selection exact."""
     B, Skv, K = 3, 5000, 100
     _say(f"indexer key splits B={B} Sq={Sq} Skv={Skv} H={H} K={K} fp8={fp8}")
     kv_lens = torch.tensor([5000, 2100, 40], dtype=torch.int32, device=DEV)
