@@ -181,6 +181,43 @@ def test_indexer_key_splits(H, fp8, Sq):
     _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
 
 
+@pytest.mark.parametrize("pattern", ["sawtooth", "sorted", "clustered"])
+def test_indexer_selection_position_patterns(pattern):
+    """Rows of 5000 scores whose values follow the key position (the
+    selection kernel holds them as runs of 8 per thread): a sawtooth of
+    period 8 (every run holds one score of each of 8 levels), an ascending
+    row, and runs of 8 in 8 tight clusters (many near ties around the
+    threshold, decided by the low bits).  The selection is exact against the
+    oracle's on the kernel's own scores, and the scores match the oracle."""
+    B, Sq, Skv, H, K = 2, 1, 5000, 64, 100
+    _say(f"indexer selection position patterns: {pattern}")
+    g = torch.Generator(device="cpu")
+    g.manual_seed(17)
+    d = torch.randn(128, generator=g)
+    d = d / d.norm()
+    pos = torch.arange(Skv, dtype=torch.float32)
+    if pattern == "sawtooth":
+        amp = (pos % 8) + 1.0
+    elif pattern == "sorted":
+        amp = 1.0 + pos / Skv
+    else:
+        amp = 1.0 + ((pos // 8) % 8) * 0.25
+    noise = 1e-2 * torch.randn(B, Skv, 128, generator=g)
+    k = (amp[None, :, None] * d[None, None, :] + noise).bfloat16()
+    q = (d[None, None, None, :].expand(B, Sq, H, 128) + 0.1 * torch.randn(B, Sq, H, 128, generator=g)).bfloat16()
+    w = torch.rand(B, Sq, H, generator=g) / H
+    q, k, w = q.to(DEV), k.to(DEV), w.to(DEV)
+    idx, logits = ops_amd.indexer_topk(q, k, w, K, return_logits=True)
+    torch.cuda.synchronize()
+    idx, logits = idx.cpu(), logits.cpu()
+    end = indexer_key_end(B, Sq, Skv)
+    ref = indexer_scores(q.cpu(), k.cpu(), w.cpu())
+    scale = float(ref.abs().max())
+    assert float((logits - ref).abs().max()) <= SCORE_RTOL * scale
+    assert torch.equal(idx, indexer_topk(logits, K, end))
+    _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
+
+
 def test_indexer_feeds_mla_forward():
     # producer -> consumer: index rows from the indexer drive the MLA forward
     B, S, Hq, K, H = 1, 384, 128, 64, 64
