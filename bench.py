@@ -408,6 +408,20 @@ def bench_mla_decode(args):
                     "frac_of_peak": pbytes / (pus * 1e-6) / 1e9 / PEAK_HBM_GBS, "page_size": 64,
                     "pool_bytes": kp.numel() * kp.element_size()}
     del kp, vp
+    # a decode step's sparse-attention layer: the index producer over the
+    # same contexts (64 index heads, d = 128, bf16), then this decode on the
+    # index rows it produced
+    qi, ki, wi, lens = indexer_inputs("decode")
+    assert torch.equal(lens, w.kv_lens)
+
+    def layer():
+        idx = ops_amd.indexer_topk(qi, ki, wi, w.idx.shape[-1], kv_lens=lens)
+        ops_amd.sfa_forward(w.q, w.k, w.v, idx, w.scale, kv_lens=w.kv_lens, out=out, lse=lse)
+
+    times, _ = time_steps(layer, args.steps * 2, args.warmup, before=flush)
+    res["layer_us"] = sum(times) / len(times) * 1e3
+    res["layer_note"] = "index producer (64 heads, d 128, bf16 keys) + this decode on its rows, caches flushed"
+    del qi, ki, wi
     if not args.no_cpu:
         _CPU_PENDING.append((res, "mla_decode", w))
     return res
@@ -544,7 +558,18 @@ def bench_indexer(args, mla=None):
                      "note": "key rows read (bf16, 256 B per visible key) per second; caches flushed per step",
                      "config": {"B": 64, "Sq": 1, "Skv": 65536, "kv_lens": "16384-65536", "H_index": 64,
                                 "d_index": 128, "topk": K}}
-    del qd, kd, wd
+    # the same step from fp8 index keys (128 B per key row)
+    ksd = kd.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    kd8 = (kd.float() / ksd[..., None]).to(f8)
+    qsd = qd.float().abs().amax(-1).clamp_min(1e-6) / 448.0
+    qd8 = (qd.float() / qsd[..., None]).to(f8)
+    wd8 = (wd * qsd).contiguous()
+    dt8, _ = time_steps(lambda: ops_amd.indexer_topk(qd8, kd8, wd8, K, kv_lens=lens, k_scale=ksd), max(5, args.steps),
+                        2, before=decode_flush())
+    d8 = sum(dt8) / len(dt8)
+    res["decode"]["fp8"] = {"ms": d8, "key_gbs": key_bytes / 2 / (d8 * 1e-3) / 1e9,
+                            "frac_of_hbm": key_bytes / 2 / (d8 * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    del qd, kd, wd, qd8, kd8, wd8
     if mla is not None:
         out = torch.empty(mla.q.shape[:3] + (mla.v.shape[3],), dtype=mla.q.dtype, device="cuda")
         lse = torch.empty(mla.q.shape[:3], dtype=torch.float32, device="cuda")

@@ -209,10 +209,13 @@ SFA_API size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_
 SFA_API int sfa_fwd_paged(const sfa_fwd_args* a, const sfa_kv_pages* pages, void* workspace,
                           size_t workspace_bytes, void* stream);
 
-/* Bytes of device workspace sfa_indexer_topk needs (the fp32 scores of a
- * chunk of queries: about 1 GiB, less when all Sq rows take less, more when
- * one block of 512 / H queries of all B sequences takes more; 0 when `logits`
- * is given). */
+/* Bytes of device workspace sfa_indexer_topk needs: the fp32 scores of a
+ * chunk of queries unless `logits` is given (about 1 GiB, less when all Sq
+ * rows take less, more when one block of 512 / H queries of all B sequences
+ * takes more), then, when a launch holds few long rows (B x queries < 256,
+ * Skv >= 16384: a decode step), the candidate lists of its two-phase
+ * selection (8 bytes per candidate, topk rounded up to 4 per segment, at
+ * most 8 segments per row).  May be 0. */
 SFA_API size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a);
 
 /* Scores and top-k selection (no counterpart kernel in the reference, which

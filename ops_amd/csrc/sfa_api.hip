@@ -575,8 +575,37 @@ void indexer_chunk(const sfa_indexer_args* a, int* rows, int64_t* ld) {
   int64_t r = (int64_t)(kIndexerChunkBytes / ((size_t)a->B * (size_t)*ld * sizeof(float)));
   r = r / qb * qb;
   if (r < qb) r = qb;
-  const int64_t all = (int64_t)(a->Sq + qb - 1) / qb * qb;
-  *rows = (int)(r < all ? r : all);
+  // (chunks start on query-block boundaries; one chunk when all Sq rows fit)
+  *rows = (int)(r < a->Sq ? r : a->Sq);
+}
+
+// Queries per launch (all Sq when the caller holds the scores, else a chunk)
+// and the workspace: the chunk's scores, then the candidate lists of a
+// segmented selection (launches of few long rows), sized for the largest of
+// the launches' plans.
+struct IndexerPlan {
+  int rows;
+  int64_t ld;
+  size_t score_bytes, cand_bytes;
+};
+
+IndexerPlan indexer_plan(const sfa_indexer_args* a) {
+  IndexerPlan pl{a->Sq, 0, 0, 0};
+  if (a->logits == nullptr) {
+    indexer_chunk(a, &pl.rows, &pl.ld);
+    pl.score_bytes = align_up((size_t)a->B * (size_t)pl.rows * (size_t)pl.ld * sizeof(float), 256);
+  }
+  const sfa::IndexerParams p = to_iparams(a);
+  size_t cb = 0;
+  const int first = pl.rows < a->Sq ? pl.rows : a->Sq;
+  const int last = a->Sq % first ? a->Sq % first : first;
+  for (int r : {first, last}) {
+    const int nseg = sfa::topk_segments(p, r);
+    if (nseg > 1)
+      cb = std::max(cb, (size_t)a->B * (size_t)r * (size_t)nseg * (size_t)((a->topk + 3) / 4 * 4) * sizeof(int32_t));
+  }
+  pl.cand_bytes = 2 * align_up(cb, 256);  // ids, then order keys
+  return pl;
 }
 
 }  // namespace
@@ -584,11 +613,9 @@ void indexer_chunk(const sfa_indexer_args* a, int* rows, int64_t* ld) {
 extern "C" {
 
 size_t sfa_indexer_topk_workspace_size(const sfa_indexer_args* a) {
-  if (check_indexer(a) != SFA_OK || a->logits) return 0;
-  int rows;
-  int64_t ld;
-  indexer_chunk(a, &rows, &ld);
-  return align_up((size_t)a->B * (size_t)rows * (size_t)ld * sizeof(float), 256);
+  if (check_indexer(a) != SFA_OK) return 0;
+  const IndexerPlan pl = indexer_plan(a);
+  return pl.score_bytes + pl.cand_bytes;
 }
 
 int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspace_bytes, void* stream) {
@@ -597,20 +624,22 @@ int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t workspac
   if (rc != SFA_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   sfa::IndexerParams p = to_iparams(a);
-  int rows = a->Sq;
+  const IndexerPlan pl = indexer_plan(a);
+  const size_t need = pl.score_bytes + pl.cand_bytes;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(SFA_E_WORKSPACE, "sfa_indexer_topk needs %zu workspace bytes (got %zu)", need, workspace_bytes);
   if (a->logits == nullptr) {
-    const size_t need = sfa_indexer_topk_workspace_size(a);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(SFA_E_WORKSPACE, "sfa_indexer_topk needs %zu workspace bytes (got %zu)", need, workspace_bytes);
-    int64_t ld;
-    indexer_chunk(a, &rows, &ld);
     p.logits = (float*)workspace;
-    p.g_ss = ld;
-    p.g_sb = (int64_t)rows * ld;
+    p.g_ss = pl.ld;
+    p.g_sb = (int64_t)pl.rows * pl.ld;
   }
-  for (int t0 = 0; t0 < a->Sq; t0 += rows) {
-    const int t1 = t0 + rows < a->Sq ? t0 + rows : a->Sq;
+  p.cand = pl.cand_bytes ? (int32_t*)((char*)workspace + pl.score_bytes) : nullptr;
+  p.cand_key = pl.cand_bytes ? (uint32_t*)((char*)workspace + pl.score_bytes + pl.cand_bytes / 2) : nullptr;
+  for (int t0 = 0; t0 < a->Sq; t0 += pl.rows) {
+    const int t1 = t0 + pl.rows < a->Sq ? t0 + pl.rows : a->Sq;
     p.g_t0 = a->logits ? 0 : t0;
+    p.nseg = p.cand ? sfa::topk_segments(p, t1 - t0) : 1;
+    p.seglen = p.nseg > 1 ? sfa::topk_seglen(p, p.nseg) : 0;
     hipError_t e = sfa::launch_indexer_logits(p, t0, t1, s);
     if (e == hipSuccess) e = sfa::launch_topk_select(p, t0, t1, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_indexer_topk");

@@ -309,6 +309,12 @@ struct IndexerParams {
   int g_t0;               // query of logits row 0 (the workspace holds a chunk of queries)
   int B, Sq, Skv, H, D, topk;
   bool fp8;
+  // segmented selection (nseg > 1): per launched row nseg candidate lists
+  // of topk keys (rounded up to 4) and their order keys, segments of seglen
+  // keys
+  int32_t* cand;
+  uint32_t* cand_key;
+  int nseg, seglen;
 };
 
 }  // namespace sfa
@@ -365,4 +371,8 @@ hipError_t launch_csr_dkv(const Params& p, hipStream_t s);    // key-major dK/dV
 int indexer_query_block(const IndexerParams& p);
 hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end, hipStream_t s);
 hipError_t launch_topk_select(const IndexerParams& p, int t_begin, int t_end, hipStream_t s);
+// Segments per row of the selection for a launch of `rows` queries per
+// sequence (1: one workgroup per row), and their length.
+int topk_segments(const IndexerParams& p, int rows);
+int topk_seglen(const IndexerParams& p, int nseg);
 }  // namespace sfa

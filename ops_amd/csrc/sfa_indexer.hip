@@ -71,6 +71,13 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelEpt = 64;      // most scores per thread in the selection kernel
 constexpr int kSelCap = kSelThreads * kSelEpt;  // longest score row (the API admits Skv <= 65536)
 constexpr int kCompact = 4096;   // keys still in play after the top 16 bits that one wave finishes
+// segmented selection (launches of fewer than kSegMaxRows rows of at least
+// kSegMinKeys keys): up to kSegMax segments per row, about kSegTargetWGs
+// phase-1 workgroups
+constexpr int kSegMaxRows = 256;
+constexpr int kSegMinKeys = 16384;
+constexpr int kSegMax = 8;
+constexpr int kSegTargetWGs = 256;
 static_assert(kSelCap == 65536, "selection capacity");
 
 // Keys query t of sequence b may see: [0, end).
@@ -485,20 +492,62 @@ __device__ __forceinline__ void block_exscan2(int hi, int lo, int* red, int* hi_
 // Selection over one row of n > K scores held as NG groups of 4 per thread
 // (thread tid owns keys [4 NG tid, 4 NG tid + 4 NG)); NG is fixed per
 // instantiation, so the bisection steps are straight-line code.
-template <int NG, int MAXR>
-__device__ __forceinline__ void select_row(const float* row, int n, int K, int32_t* out, int* red, uint32_t* s_c) {
+// Candidate list stride of the segmented selection: topk rounded up to 4
+// entries (16 bytes), the tail -1.
+__host__ __device__ __forceinline__ int topk_list_stride(int K) { return (K + 3) / 4 * 4; }
+
+// Key sources of select_row: position i of the selection row -> order key
+// (4 at a time, i a multiple of 4) and the index written for it.
+// A contiguous score row; position i is key base + i.
+struct RowSrc {
+  static constexpr bool kIds = false;  // ids computed, not loaded
+  const float* row;  // scores of positions 0, 1, ... (16-byte aligned)
+  int base;
+  __device__ __forceinline__ void keys4(int i, uint32_t* k) const {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) k[e] = order_key(x[e]);
+  }
+  __device__ __forceinline__ int32_t id(int i) const { return base + i; }
+};
+// A candidate list: position i is key cand[i] with order key ckey[i]
+// (cand -1, ckey 0: no candidate, below every real key).  The ids are
+// loaded with the keys and kept in registers.
+struct CandSrc {
+  static constexpr bool kIds = true;
+  const int32_t* cand;  // 16-byte aligned
+  const uint32_t* ckey;
+  __device__ __forceinline__ void keys4(int i, uint32_t* k) const {
+    const uint4 c = *reinterpret_cast<const uint4*>(ckey + i);
+    k[0] = c.x; k[1] = c.y; k[2] = c.z; k[3] = c.w;
+  }
+  __device__ __forceinline__ void ids4(int i, int32_t* d) const {
+    const int4 c = *reinterpret_cast<const int4*>(cand + i);
+    d[0] = c.x; d[1] = c.y; d[2] = c.z; d[3] = c.w;
+  }
+};
+
+// The K best positions of src (n > K) into out[0, K) in ascending position
+// order, and with kout their order keys into kout[0, K).
+template <int NG, int MAXR, bool KOUT, class Src>
+__device__ __forceinline__ void select_row(const Src& src, int n, int K, int32_t* out, uint32_t* kout, int* red,
+                                           uint32_t* s_c) {
   constexpr int EPT = 4 * NG;
   const int tid = threadIdx.x;
   const int i0 = tid * EPT;
   const int cnt = min(max(n - i0, 0), EPT);
   // order keys (0 = absent: every real key is >= order_key(-inf) > 0)
   uint32_t u[EPT];
+  int32_t idv[Src::kIds ? EPT : 1];
 #pragma unroll
   for (int v = 0; v < NG; ++v) {
-    f32x4 x = {kNegInf, kNegInf, kNegInf, kNegInf};
-    if (4 * v < cnt) x = *reinterpret_cast<const f32x4*>(row + i0 + 4 * v);
+    uint32_t k4[4] = {0u, 0u, 0u, 0u};
+    if (4 * v < cnt) {
+      src.keys4(i0 + 4 * v, k4);
+      if constexpr (Src::kIds) src.ids4(i0 + 4 * v, idv + 4 * v);
+    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) u[4 * v + e] = (4 * v + e < cnt) ? order_key(x[e]) : 0u;
+    for (int e = 0; e < 4; ++e) u[4 * v + e] = (4 * v + e < cnt) ? k4[e] : 0u;
   }
   // the K-th largest key, bit by bit from the top (a wave counts with
   // ballots: one compare and a scalar popcount per score register; with 64
@@ -616,8 +665,39 @@ __device__ __forceinline__ void select_row(const float* row, int n, int K, int32
   for (int e = 0; e < EPT; ++e) {
     const bool sel = u[e] > thr || (u[e] == thr && teq < my_eq);
     teq += (u[e] == thr) ? 1 : 0;
-    if (sel) out[w++] = i0 + e;
+    if (sel) {
+      if constexpr (Src::kIds)
+        out[w] = idv[e];
+      else
+        out[w] = src.id(i0 + e);
+      if constexpr (KOUT) kout[w] = u[e];
+      ++w;
+    }
   }
+}
+
+// MAXNG: the largest row this instance takes is 4 MAXNG kSelThreads scores.
+// Rows of up to 32768 scores are held to 64 VGPRs: two workgroups per CU, so
+// one workgroup's barrier waits overlap the other's counting.  At that bound
+// the compiler spills ~21 VGPRs to scratch; the spill-free build at one
+// workgroup per CU (84 VGPRs) was measured 7 % slower on the whole call.
+// Selection of the K best of n positions of `src` into out[0, K) (n > K),
+// with the smallest run length per thread that holds n.
+template <int MAXNG, bool KOUT, class Src>
+__device__ __forceinline__ void select_dispatch(const Src& src, int n, int K, int32_t* out, uint32_t* kout, int* red,
+                                                uint32_t* s_c) {
+  constexpr int MAXR = MAXNG <= 8 ? 8 : 16;  // in-play keys per lane of the register finish
+  const int ng = (n + 4 * kSelThreads - 1) / (4 * kSelThreads);
+  if (ng <= 1)
+    select_row<1, MAXR, KOUT>(src, n, K, out, kout, red, s_c);
+  else if (ng <= 2)
+    select_row<2, MAXR, KOUT>(src, n, K, out, kout, red, s_c);
+  else if (ng <= 4)
+    select_row<4, MAXR, KOUT>(src, n, K, out, kout, red, s_c);
+  else if (MAXNG <= 8 || ng <= 8)
+    select_row<8, MAXR, KOUT>(src, n, K, out, kout, red, s_c);
+  else if constexpr (MAXNG > 8)
+    select_row<16, MAXR, KOUT>(src, n, K, out, kout, red, s_c);
 }
 
 // MAXNG: the largest row this instance takes is 4 MAXNG kSelThreads scores.
@@ -629,7 +709,6 @@ template <int MAXNG>
 // (second bound: minimum waves per SIMD; 8 = two 16-wave workgroups per CU)
 __global__ __launch_bounds__(kSelThreads, MAXNG <= 8 ? 8 : 1) void topk_select_kernel(IndexerParams p, int t_begin,
                                                                                      int t_end) {
-  constexpr int MAXR = MAXNG <= 8 ? 8 : 16;  // in-play keys per lane of the register finish
   __shared__ int red[96];
   __shared__ uint32_t s_c[kCompact];
   const int nt = t_end - t_begin;
@@ -645,18 +724,74 @@ __global__ __launch_bounds__(kSelThreads, MAXNG <= 8 ? 8 : 1) void topk_select_k
     return;
   }
   const float* row = p.logits + b * p.g_sb + (int64_t)(t - p.g_t0) * p.g_ss;
-  // groups of 4 scores per thread: the smallest power of two that holds n
-  const int ng = (n + 4 * kSelThreads - 1) / (4 * kSelThreads);
-  if (ng <= 1)
-    select_row<1, MAXR>(row, n, K, out, red, s_c);
-  else if (ng <= 2)
-    select_row<2, MAXR>(row, n, K, out, red, s_c);
-  else if (ng <= 4)
-    select_row<4, MAXR>(row, n, K, out, red, s_c);
-  else if (MAXNG <= 8 || ng <= 8)
-    select_row<8, MAXR>(row, n, K, out, red, s_c);
-  else if constexpr (MAXNG > 8)
-    select_row<16, MAXR>(row, n, K, out, red, s_c);
+  select_dispatch<MAXNG, false>(RowSrc{row, 0}, n, K, out, nullptr, red, s_c);
+}
+
+// Segmented selection, for launches with few long rows (a decode step: one
+// workgroup per row would leave most CUs idle).  Phase 1: workgroup
+// (row, s) selects the K best keys of segment s of the row, [s seglen,
+// (s + 1) seglen) cut at the row's end, into the row's candidate list
+// p.cand[row][s][0, K) in ascending key order (all of a segment's keys when
+// it has at most K, then -1).  Phase 2 (topk_merge_kernel): one workgroup per
+// row selects the K best of the row's nseg K candidates.  The union of the
+// segments' selections holds the row's selection, ties included: a segment
+// with at least K keys at or above the row's threshold would put K keys above
+// it; so a segment's local threshold is at most the row's, and it keeps
+// every key above the row's threshold and at least as many of its lowest
+// equal keys as the row takes.  The candidates are in ascending key order
+// (segment by segment), so the merge's equal-score rule (lower position
+// first) is the row's (lower key first).
+// (4 waves per SIMD: about 256 workgroups, one per CU)
+__global__ __launch_bounds__(kSelThreads, 4) void topk_segment_kernel(IndexerParams p, int t_begin, int t_end) {
+  __shared__ int red[96];
+  __shared__ uint32_t s_c[kCompact];
+  const int nt = t_end - t_begin;
+  const int rowi = blockIdx.x / p.nseg;
+  const int seg = (int)(blockIdx.x % p.nseg);
+  const int b = rowi / nt;
+  const int t = t_begin + rowi % nt;
+  const int tid = threadIdx.x;
+  const int K = p.topk;
+  const int kpad = topk_list_stride(K);
+  const int n = __builtin_amdgcn_readfirstlane(key_end(p, b, t));
+  int32_t* out = p.cand + (int64_t)blockIdx.x * kpad;
+  uint32_t* kout = p.cand_key + (int64_t)blockIdx.x * kpad;
+  const int s0 = seg * p.seglen;
+  const int ns = min(max(n - s0, 0), p.seglen);
+  const float* row = p.logits + b * p.g_sb + (int64_t)(t - p.g_t0) * p.g_ss;
+  if (ns <= K) {
+    for (int i = tid; i < kpad; i += kSelThreads) {
+      out[i] = i < ns ? s0 + i : -1;
+      kout[i] = i < ns ? order_key(row[s0 + i]) : 0u;
+    }
+    return;
+  }
+  if (tid < kpad - K) {
+    out[K + tid] = -1;
+    kout[K + tid] = 0u;
+  }
+  select_dispatch<8, true>(RowSrc{row + s0, s0}, ns, K, out, kout, red, s_c);
+}
+
+// (4 waves per SIMD: one merge workgroup per row, few rows; the candidate
+// gathers need more than the 64 VGPRs of two workgroups per CU)
+__global__ __launch_bounds__(kSelThreads, 4) void topk_merge_kernel(IndexerParams p, int t_begin, int t_end) {
+  __shared__ int red[96];
+  __shared__ uint32_t s_c[kCompact];
+  const int nt = t_end - t_begin;
+  const int b = blockIdx.x / nt;
+  const int t = t_begin + (int)(blockIdx.x % nt);
+  const int tid = threadIdx.x;
+  const int K = p.topk;
+  const int n = __builtin_amdgcn_readfirstlane(key_end(p, b, t));
+  int32_t* out = p.idx + b * p.i_sb + t * p.i_ss;
+  if (n <= K) {
+    for (int i = tid; i < K; i += kSelThreads) out[i] = i < n ? i : -1;
+    return;
+  }
+  const int kpad = topk_list_stride(K);
+  const int64_t c0 = (int64_t)blockIdx.x * p.nseg * kpad;
+  select_dispatch<8, false>(CandSrc{p.cand + c0, p.cand_key + c0}, p.nseg * kpad, K, out, nullptr, red, s_c);
 }
 
 }  // namespace
@@ -742,9 +877,34 @@ hipError_t launch_indexer_logits(const IndexerParams& p, int t_begin, int t_end,
   return hipGetLastError();
 }
 
+int topk_segments(const IndexerParams& p, int rows) {
+  const int64_t nrow = (int64_t)p.B * rows;
+  if (nrow <= 0 || nrow >= kSegMaxRows || p.Skv < kSegMinKeys) return 1;
+  int nseg = (int)std::min<int64_t>(kSegMax, std::max<int64_t>(2, (kSegTargetWGs + nrow - 1) / nrow));
+  // the candidates fill one merge row of at most 32768 (two workgroups per
+  // CU), and a segment must be longer than K to cut anything
+  while (nseg > 1 &&
+         ((int64_t)nseg * topk_list_stride(p.topk) > 4 * 8 * kSelThreads || topk_seglen(p, nseg) <= p.topk))
+    --nseg;
+  return nseg;
+}
+
+int topk_seglen(const IndexerParams& p, int nseg) { return ((p.Skv + nseg - 1) / nseg + 31) / 32 * 32; }
+
 hipError_t launch_topk_select(const IndexerParams& p, int t_begin, int t_end, hipStream_t s) {
   const int64_t n = (int64_t)p.B * (t_end - t_begin);
   if (n == 0) return hipSuccess;
+  if (p.nseg > 1) {
+    if (p.cand == nullptr || p.cand_key == nullptr || p.seglen <= 0 || p.seglen % 4 != 0 || (int64_t)p.seglen * p.nseg < p.Skv ||
+        p.seglen > 4 * 8 * kSelThreads || (int64_t)p.nseg * topk_list_stride(p.topk) > 4 * 8 * kSelThreads)
+      return hipErrorInvalidValue;
+    // (Skv <= 65536 and at least 2 segments: a segment holds at most 32768)
+    hipLaunchKernelGGL(topk_segment_kernel, dim3((unsigned)(n * p.nseg)), dim3(kSelThreads), 0, s, p, t_begin, t_end);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);
+    return hipGetLastError();
+  }
   // a row holds at most Skv scores
   if (p.Skv <= 4 * 8 * kSelThreads)
     hipLaunchKernelGGL(topk_select_kernel<8>, dim3((unsigned)n), dim3(kSelThreads), 0, s, p, t_begin, t_end);

@@ -218,6 +218,37 @@ def test_indexer_selection_position_patterns(pattern):
     _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
 
 
+@pytest.mark.parametrize("K,kv,dup", [(301, [20000, 250], False), (300, [17000, 9000], True),
+                                       (2048, [20000, 12000], False)],
+                         ids=["k301-short-row", "k300-ties", "k2048"])
+def test_indexer_segmented_selection(K, kv, dup):
+    """Launches of few long rows (under 256 rows of at least 16384 keys) select
+    in two phases: each row cut into segments whose own top-k become the
+    row's candidate lists (padded to a multiple of 4 with -1), then the top-k
+    of the candidates.  Here 2 sequences x 3 queries of up to 20000 keys:
+    8 segments of 2528 keys, a row shorter than k (no segment selects), a
+    row ending in its fourth segment (empty segments), exact ties (keys
+    repeated 4 times), and k = 2048 (segments shorter than k: all their keys
+    are candidates).  Every visible score against the oracle, the selection
+    exact against the oracle's on the kernel's own scores."""
+    B, Sq, Skv, H = 2, 3, 20000, 64
+    _say(f"indexer segmented selection B={B} Sq={Sq} Skv={Skv} K={K} kv_lens={kv} ties={dup}")
+    q, k, w = _inputs(B, Sq, Skv, H, seed=K, dup_keys=dup)
+    kv_lens = torch.tensor(kv, dtype=torch.int32, device=DEV)
+    idx, logits = ops_amd.indexer_topk(q, k, w, K, kv_lens=kv_lens, return_logits=True)
+    torch.cuda.synchronize()
+    idx, logits = idx.cpu(), logits.cpu()
+    end = indexer_key_end(B, Sq, Skv, kv_lens.cpu())
+    ref = indexer_scores(q.cpu(), k.cpu(), w.cpu(), kv_lens.cpu())
+    vis = torch.arange(Skv)[None, None, :] < end[:, :, None]
+    scale = float(ref[vis].abs().max())
+    err = float((logits[vis] - ref[vis]).abs().max())
+    assert err <= SCORE_RTOL * scale, f"score error {err} vs scale {scale}"
+    own = torch.where(vis, logits, torch.full_like(logits, -math.inf))
+    assert torch.equal(idx, indexer_topk(own, K, end))
+    _check_rows(idx, ref, end, K, 2 * SCORE_RTOL * scale)
+
+
 def test_indexer_feeds_mla_forward():
     # producer -> consumer: index rows from the indexer drive the MLA forward
     B, S, Hq, K, H = 1, 384, 128, 64, 64

@@ -152,11 +152,33 @@ def test_indexer_workspace_is_bounded():
     a.q_ss, a.q_sb = 64 * 128, 32768 * 64 * 128
     a.k_sb = 32768 * 128
     ws = lib.sfa_indexer_topk_workspace_size(ctypes.byref(a))
-    assert 0 < ws <= (512 << 20) + 4096
+    assert 0 < ws <= (1 << 30) + 4096
     a.logits = 0x10000
     a.g_ss, a.g_sb = 32768, 32768 * 32768
     assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) == 0
     assert lib.sfa_indexer_topk(None, None, 0, None) == _lib.SFA_E_INVALID
+
+
+def test_indexer_workspace_decode_step():
+    # 64 sequences x 1 query over 65536 keys: one score row per sequence, and
+    # the candidate lists of the two-phase selection (4 segments per row,
+    # ids + order keys), also when the caller holds the scores
+    lib = _lib.load()
+    a = _valid_indexer_args()
+    a.B, a.Sq, a.Skv, a.topk = 64, 1, 65536, 2048
+    a.q_sb, a.q_ss = 64 * 128, 64 * 128
+    a.k_sb = 65536 * 128
+    a.w_sb, a.w_ss = 64, 64
+    a.i_sb, a.i_ss = 2048, 2048
+    cand = 2 * 64 * 4 * 2048 * 4
+    assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) == 64 * 65536 * 4 + cand
+    a.logits = 0x10000
+    a.g_ss, a.g_sb = 65536, 65536
+    assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) == cand
+    # a long prefill row set takes no candidates
+    a.B, a.Sq = 1, 4096
+    a.q_sb, a.w_sb, a.i_sb, a.g_sb = 4096 * 64 * 128, 4096 * 64, 4096 * 2048, 4096 * 65536
+    assert lib.sfa_indexer_topk_workspace_size(ctypes.byref(a)) == 0
 
 
 def test_fp8_key_scale_closed_form():
