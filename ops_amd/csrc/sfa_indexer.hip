@@ -48,7 +48,7 @@ constexpr int kLogitTargetWGs = 2048;  // workgroups a split scores launch aims 
 constexpr int kLogitMinSpan = 32;      // fewest key tiles (1024 keys) per workgroup
 constexpr int kOneQMaxSq = 2;          // queries per sequence up to which the one-query kernel runs
 constexpr int kOneQTargetWGs = 16384;   // workgroups a one-query launch aims for
-constexpr int kOneQMinSpan = 16;       // fewest key tiles per one-query workgroup (4 per wave)
+constexpr int kOneQMinSpan = 8;        // fewest key tiles per one-query workgroup (2 per wave)
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));

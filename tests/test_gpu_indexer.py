@@ -155,7 +155,7 @@ def test_indexer_key_splits(H, fp8, Sq):
     one sequence inside its third split of 1024 keys and leave another only
     part of its first tile (the later splits exit at once).  With 5 queries
     per sequence the block kernel runs (5 splits per block); with 1 or 2 the
-    one-query kernel (splits of 16 tiles, each wave streaming its own tiles,
+    one-query kernel (splits of 8 tiles, each wave streaming its own tiles,
     a wave with no tile idle).  Every visible score against the oracle, the
     selection exact."""
     B, Skv, K = 3, 5000, 100
