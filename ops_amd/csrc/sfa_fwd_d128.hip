@@ -1,6 +1,9 @@
 // gfx950 forward for d_qk = d_v = 128 (the MQA prefill and GQA training
 // shapes, and the reference's own single shared kv with G = 32, 64, 128 query
-// heads): register gather of whole rows.
+// heads), also instantiated for d = 64 (the reference's signature at that
+// width, SFA.py:97, 554: any power-of-two head dim): register gather of whole
+// rows.  The text below describes d = 128; at d = 64 a row is 8 lanes of 16
+// bytes and a load instruction moves 8 rows.
 //
 // Reference: `_attn_fwd` / `_inner_fwd` (SFA.py:309-587); the math is the one
 // of the MLA kernel in sfa_fwd_mfma.hip (masked base-2 online softmax with a
@@ -39,15 +42,30 @@ namespace {
 constexpr float kSlack = 8.0f;  // lazy-rescale slack (base-2 units), as in the MLA kernel
 constexpr int kIdxCapD = 1024;  // slots staged in LDS per work item (longer top-k: split-k)
 constexpr int kT = 16;          // heads per wave (MFMA N)
-constexpr int kQSteps = 4;      // 128 / 32 contraction steps of S^T
-constexpr int kOT = 8;          // 128 / 16 O^T dim tiles
-constexpr int kPV = 17;         // V staging row pitch in 16-byte slots (odd: conflict-free reads)
 constexpr int kMaxGroupD = 256; // query heads per KV head (16 groups of 16)
 
-template <bool PAGED>
+// Geometry for head dim D = d_qk = d_v (128; 64 for the reference's
+// signature at that width): contraction steps of S^T (32 dims), O^T dim
+// tiles (16 dims), 16-byte chunks per row, the LDS row pitch (odd:
+// conflict-free reads), and the whole-row load pattern: CH lanes per row,
+// RPI rows per load instruction, NI instructions per 32-row tile.
+template <int D>
+struct Dh {
+  static_assert(D == 64 || D == 128, "head dims of the register-gather kernels");
+  static constexpr int kQSteps = D / 32;
+  static constexpr int kOT = D / 16;
+  static constexpr int kCH = D / 8;
+  static constexpr int kPV = kCH + 1;
+  static constexpr int kRPI = 64 / kCH;
+  static constexpr int kNI = 32 / kRPI;
+};
+
+template <int D, bool PAGED>
 __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   using M = Mfma<16>;
   typedef M::acc_t acc_t;
+  typedef Dh<D> DH;
+  constexpr int kQSteps = DH::kQSteps, kOT = DH::kOT, kPV = DH::kPV, kNI = DH::kNI;
 
   __shared__ __align__(16) int s_idx[kIdxCapD];
   __shared__ u32x4 s_v[32 * kPV];  // the K, then the V rows of the current tile
@@ -55,6 +73,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   const int lane = threadIdx.x;
   const int lt = lane & 15;  // head (MFMA column) / key row within a 16-row M-tile
   const int hq = lane >> 4;  // lane group: 8-element slice of the contraction
+  const int lc = lane % DH::kCH, lr = lane / DH::kCH;  // row-load chunk and row group
 
   // ---- work item (same placement as the MLA kernel) ----------------------
   // A sub-item is (split, head group): the sub-items of one item go to the
@@ -113,10 +132,10 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   // the pools (the batch lives in the block table)
   const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * ((PAGED ? 0 : b * p.k_sb) + g * p.k_sh);
   const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + D)));
   const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * ((PAGED ? 0 : b * p.v_sb) + g * p.v_sh);
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, PAGED ? 0u : (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + D)));
 
   const int used = wave_max_int(istage.template store<PAGED>(p, b, bound, nslots, ntiles * 32, s_idx, lane));
   __syncthreads();  // indices staged (one wave: orders the LDS writes and reads)
@@ -124,39 +143,43 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   ntiles = (used + 31) / 32;
 
   // Loads of tile j (keys 32 j .. 32 j + 31): instruction i of a lane loads
-  // the 16 bytes at chunk lt of tile row i + 8 hq, for K into kr[i] and for V
-  // into vr[i] (4 whole rows per instruction; a lane's 8 rows are consecutive,
-  // so their ids are two 16-byte LDS reads).  Invalid keys read from an
-  // out-of-range offset (paged: the zero row) and get zeros.
-  auto load_tile = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+  // the 16 bytes at chunk lc of tile row i + NI lr, for K into kr[i] and for V
+  // into vr[i] (RPI whole rows per instruction; a lane's NI rows are
+  // consecutive, so their ids are NI / 4 16-byte LDS reads).  Invalid keys
+  // read from an out-of-range offset (paged: the zero row) and get zeros.
+  auto load_tile = [&](int j, bf16x8 (&kr)[kNI], bf16x8 (&vr)[kNI]) {
     typedef int i32x4 __attribute__((ext_vector_type(4)));
-    const i32x4 id0 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq);
-    const i32x4 id1 = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + 8 * hq + 4);
-    const int ids[8] = {id0[0], id0[1], id0[2], id0[3], id1[0], id1[1], id1[2], id1[3]};
+    int ids[kNI];
+#pragma unroll
+    for (int q = 0; q < kNI / 4; ++q) {
+      const i32x4 x = *reinterpret_cast<const i32x4*>(s_idx + 32 * j + kNI * lr + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ids[4 * q + e] = x[e];
+    }
     if constexpr (PAGED) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kNI; ++i) {
         const char* ka = ids[i] >= 0 ? kbase + pool_row_offset((uint32_t)ids[i], p.page_shift, (uint64_t)(2 * p.k_sb),
-                                                                krow_bytes) + 16 * lt
-                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lt;
+                                                                krow_bytes) + 16 * lc
+                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lc;
         kr[i] = *reinterpret_cast<const bf16x8*>(ka);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kNI; ++i) {
         const char* va = ids[i] >= 0 ? vbase + pool_row_offset((uint32_t)ids[i], p.page_shift, (uint64_t)(2 * p.v_sb),
-                                                                vrow_bytes) + 16 * lt
-                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lt;
+                                                                vrow_bytes) + 16 * lc
+                                     : reinterpret_cast<const char*>(kZeroRow) + 16 * lc;
         vr[i] = *reinterpret_cast<const bf16x8*>(va);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t ko = ids[i] >= 0 ? __umul24((uint32_t)ids[i], krow_bytes) + 16u * (uint32_t)lt : kOOB;
+      for (int i = 0; i < kNI; ++i) {
+        const uint32_t ko = ids[i] >= 0 ? __umul24((uint32_t)ids[i], krow_bytes) + 16u * (uint32_t)lc : kOOB;
         kr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t vo = ids[i] >= 0 ? __umul24((uint32_t)ids[i], vrow_bytes) + 16u * (uint32_t)lt : kOOB;
+      for (int i = 0; i < kNI; ++i) {
+        const uint32_t vo = ids[i] >= 0 ? __umul24((uint32_t)ids[i], vrow_bytes) + 16u * (uint32_t)lc : kOOB;
         vr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
       }
     }
@@ -176,21 +199,21 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   const uint32_t vb0 = (uint32_t)((4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
   const uint32_t vb1 = (uint32_t)((16 + 4 * hq + rr) * kPV) * 16u + (uint32_t)(4 * cc) * 2u;
 
-  auto step = [&](int j, bf16x8 (&kr)[8], bf16x8 (&vr)[8]) {
+  auto step = [&](int j, bf16x8 (&kr)[kNI], bf16x8 (&vr)[kNI]) {
     // K rows of this tile into the LDS tile (the previous tile's reads of it
     // are done: LDS operations of a wave complete in order), its S^T A
     // operands (row 16 mt + lt, chunk 4 s + hq) back, then the V rows over
     // them, then the loads of the next tile into the freed registers
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPV + lt]) = kr[i];
-    bf16x8 kc[8];
+    for (int i = 0; i < kNI; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + kNI * lr) * kPV + lc]) = kr[i];
+    bf16x8 kc[2 * kQSteps];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        kc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPV + 4 * s + hq]);
+      for (int s = 0; s < kQSteps; ++s)
+        kc[kQSteps * mt + s] = *reinterpret_cast<const bf16x8*>(&s_v[(16 * mt + lt) * kPV + 4 * s + hq]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + 8 * hq) * kPV + lt]) = vr[i];
+    for (int i = 0; i < kNI; ++i) *reinterpret_cast<bf16x8*>(&s_v[(i + kNI * lr) * kPV + lc]) = vr[i];
     const uint32_t vmask = (uint32_t)__ballot(s_idx[32 * j + (lane & 31)] >= 0);
     if (j + 1 < ntiles) load_tile(j + 1, kr, vr);
 
@@ -199,7 +222,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(kc[4 * mt + s], qb[s], sacc[mt]);
+      for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(kc[kQSteps * mt + s], qb[s], sacc[mt]);
 
     // softmax over this lane's 8 keys: key(mt, e) = 16 mt + 4 hq + e
     float sv[8];
@@ -249,7 +272,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   };
 
   {
-    bf16x8 kr[8], vr[8];
+    bf16x8 kr[kNI], vr[kNI];
     if (ntiles > 0) load_tile(0, kr, vr);
     for (int j = 0; j < ntiles; ++j) step(j, kr, vr);
   }
@@ -273,7 +296,7 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
   if (partial) {
     scale_o = l_sum > 0.f ? 1.f / l_sum : 0.f;
     if (hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
-    orow = p.part_o + (split * nrows + row) * 128;
+    orow = p.part_o + (split * nrows + row) * D;
   } else {
     const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
     const float mm = fmaxf(m_fin, sink2);
@@ -308,15 +331,17 @@ __global__ __launch_bounds__(64, 3) void fwd_d128_kernel(Params p) {
 constexpr int kIdxCapG = 2048;  // slots staged per work item (longer top-k: split-k)
 constexpr int kMaxGroupG = 128;
 
-template <int NW, bool VK>
+template <int D, int NW, bool VK>
 __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
   using M = Mfma<16>;
   typedef M::acc_t acc_t;
-  constexpr int R = 32 / NW;  // tile rows each wave gathers
-  constexpr int RI = R / 4;   // its load instructions per matrix (4 whole rows each)
+  typedef Dh<D> DH;
+  constexpr int kQSteps = DH::kQSteps, kOT = DH::kOT, kPV = DH::kPV;
+  constexpr int R = 32 / NW;         // tile rows each wave gathers
+  constexpr int RI = R / DH::kRPI;   // its load instructions per matrix (RPI whole rows each)
   constexpr int THR = 64 * NW;
   constexpr int TS = 32 * kPV;  // 16-byte slots of one tile (pitch kPV)
-  static_assert(R % 4 == 0 && NW * R == 32, "whole 4-row load instructions");
+  static_assert(R % DH::kRPI == 0 && NW * R == 32, "whole-row load instructions");
 
   __shared__ __align__(16) int s_idx[kIdxCapG];
   __shared__ u32x4 s_k[2][TS];
@@ -327,6 +352,7 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lt = lane & 15;  // head (MFMA column) / key row within a 16-row M-tile
   const int hq = lane >> 4;  // lane group
+  const int lc = lane % DH::kCH, lr = lane / DH::kCH;  // row-load chunk and row group
 
   // ---- work item (placement of fwd_d128_kernel) ---------------------------
   int wi = blockIdx.x;
@@ -375,10 +401,10 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
   }
   const char* kbase = reinterpret_cast<const char*>(p.k) + 2 * (b * p.k_sb + g * p.k_sh);
   const uint32_t krow_bytes = (uint32_t)(2 * p.k_ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.k_ss + D)));
   const char* vbase = reinterpret_cast<const char*>(p.v) + 2 * (b * p.v_sb + g * p.v_sh);
   const uint32_t vrow_bytes = (uint32_t)(2 * p.v_ss);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128)));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (uint32_t)(2 * ((int64_t)(p.Skv - 1) * p.v_ss + D)));
 
   {
     const int used = wave_max_int(istage.template store<false>(p, b, bound, nslots, ntiles * 32, s_idx, tid));
@@ -392,18 +418,18 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
     ntiles = (u + 31) / 32;  // tiles past the last valid slot contribute nothing
   }
 
-  // Rows of tile j this lane loads: instruction i, chunk lt of tile row
-  // wave R + RI hq + i (a lane's RI rows are consecutive).  Invalid keys read
+  // Rows of tile j this lane loads: instruction i, chunk lc of tile row
+  // wave R + RI lr + i (a lane's RI rows are consecutive).  Invalid keys read
   // from an out-of-range offset and get zeros.
-  const int row0 = wave * R + RI * hq;
+  const int row0 = wave * R + RI * lr;
   auto load_rows = [&](int j, bf16x8 (&kr)[RI], bf16x8 (&vr)[RI]) {
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
       const int id = s_idx[32 * j + row0 + i];
-      const uint32_t ko = id >= 0 ? __umul24((uint32_t)id, krow_bytes) + 16u * (uint32_t)lt : kOOB;
+      const uint32_t ko = id >= 0 ? __umul24((uint32_t)id, krow_bytes) + 16u * (uint32_t)lc : kOOB;
       kr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ko, 0, 0));
       if constexpr (!VK) {
-        const uint32_t vo = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) + 16u * (uint32_t)lt : kOOB;
+        const uint32_t vo = id >= 0 ? __umul24((uint32_t)id, vrow_bytes) + 16u * (uint32_t)lc : kOOB;
         vr[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
       }
     }
@@ -411,8 +437,8 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
   auto write_rows = [&](int buf, const bf16x8 (&kr)[RI], const bf16x8 (&vr)[RI]) {
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
-      *reinterpret_cast<bf16x8*>(&s_k[buf][(row0 + i) * kPV + lt]) = kr[i];
-      if constexpr (!VK) *reinterpret_cast<bf16x8*>(&s_v[buf][(row0 + i) * kPV + lt]) = vr[i];
+      *reinterpret_cast<bf16x8*>(&s_k[buf][(row0 + i) * kPV + lc]) = kr[i];
+      if constexpr (!VK) *reinterpret_cast<bf16x8*>(&s_v[buf][(row0 + i) * kPV + lc]) = vr[i];
     }
   };
   // (an LDS-only barrier: the next tile's row loads stay in flight across it)
@@ -440,16 +466,17 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
     const u32x4* vt = VK ? s_k[cur] : s_v[cur];
     const uint32_t vmask = (uint32_t)__ballot(s_idx[32 * j + (lane & 31)] >= 0);
     // S^T = K Q^T: two 16-key M-tiles, A operands row 16 mt + lt, chunk 4 s + hq
-    bf16x8 kc[8];
+    bf16x8 kc[2 * kQSteps];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kc[4 * mt + s] = *reinterpret_cast<const bf16x8*>(&kt[(16 * mt + lt) * kPV + 4 * s + hq]);
+      for (int s = 0; s < kQSteps; ++s)
+        kc[kQSteps * mt + s] = *reinterpret_cast<const bf16x8*>(&kt[(16 * mt + lt) * kPV + 4 * s + hq]);
     acc_t sacc[2] = {acc_t{}, acc_t{}};
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(kc[4 * mt + s], qb[s], sacc[mt]);
+      for (int mt = 0; mt < 2; ++mt) sacc[mt] = M::mma(kc[kQSteps * mt + s], qb[s], sacc[mt]);
 
     // softmax over this lane's 8 keys: key(mt, e) = 16 mt + 4 hq + e
     float sv[8];
@@ -520,7 +547,7 @@ __global__ __launch_bounds__(64 * NW, 4) void fwd_d128g_kernel(Params p) {
   if (partial) {
     scale_o = l_sum > 0.f ? 1.f / l_sum : 0.f;
     if (hq == 0) p.part_lse[split * nrows + row] = l_sum > 0.f ? m_fin + log2f(l_sum) : kNegInf;
-    orow = p.part_o + (split * nrows + row) * 128;
+    orow = p.part_o + (split * nrows + row) * D;
   } else {
     const float sink2 = p.sink ? p.sink[h] * kLog2e : kNegInf;
     const float mm = fmaxf(m_fin, sink2);
@@ -545,47 +572,63 @@ int d128g_waves(int G) { return G <= 32 ? 2 : G <= 64 ? 4 : 8; }
 }  // namespace
 
 bool fwd_d128_supported(const Params& p) {
-  const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + 128);
-  const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + 128);
+  if (!(p.Dqk == p.Dv && (p.Dqk == 128 || p.Dqk == 64))) return false;
+  const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
+  const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
   // contiguous rows use 32-bit buffer offsets, paged pools 64-bit addresses
   const bool addressable = p.block_table != nullptr || (kb < (int64_t)kOOB && vb < (int64_t)kOOB &&
                                                         fits_u24(2 * p.k_ss) && fits_u24(2 * p.v_ss));
-  return p.Dqk == 128 && p.Dv == 128 && p.G <= kMaxGroupD && p.G > 0 && addressable;
+  return p.G <= kMaxGroupD && p.G > 0 && addressable;
 }
 
 int fwd_d128_head_groups(const Params& p) { return fwd_d128g_supported(p) ? 1 : (p.G + kT - 1) / kT; }
 
-// The shared-tile kernel: contiguous rows, 16 < G <= 128.
+// The shared-tile kernel: contiguous rows, 16 < G <= 128 (d = 64: G <= 64,
+// whose waves each gather whole load instructions of 8 rows).
 bool fwd_d128g_supported(const Params& p) {
-  return fwd_d128_supported(p) && p.block_table == nullptr && p.G > kT && p.G <= kMaxGroupG;
+  return fwd_d128_supported(p) && p.block_table == nullptr && p.G > kT && p.G <= kMaxGroupG &&
+         d128g_waves(p.G) * (p.Dqk == 64 ? Dh<64>::kRPI : Dh<128>::kRPI) <= 32;
 }
 
 int fwd_d128_idx_cap(const Params& p) { return fwd_d128g_supported(p) ? kIdxCapG : kIdxCapD; }
 
-hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
+namespace {
+
+template <int D>
+hipError_t launch_fwd_dh(const Params& p, hipStream_t s) {
   if (fwd_d128g_supported(p)) {
     const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits;
     const bool vk = p.v == p.k && p.v_sb == p.k_sb && p.v_ss == p.k_ss && p.v_sh == p.k_sh;
     const int nw = d128g_waves(p.G);
-#define SFA_D128G(NW)                                                                                  \
-  if (nw == NW) {                                                                                      \
-    if (vk)                                                                                            \
-      hipLaunchKernelGGL((fwd_d128g_kernel<NW, true>), dim3((unsigned)n), dim3(64 * NW), 0, s, p);     \
-    else                                                                                               \
-      hipLaunchKernelGGL((fwd_d128g_kernel<NW, false>), dim3((unsigned)n), dim3(64 * NW), 0, s, p);    \
-    return hipGetLastError();                                                                          \
+#define SFA_D128G(NW)                                                                                   \
+  if (nw == NW) {                                                                                       \
+    if (vk)                                                                                             \
+      hipLaunchKernelGGL((fwd_d128g_kernel<D, NW, true>), dim3((unsigned)n), dim3(64 * NW), 0, s, p);   \
+    else                                                                                                \
+      hipLaunchKernelGGL((fwd_d128g_kernel<D, NW, false>), dim3((unsigned)n), dim3(64 * NW), 0, s, p);  \
+    return hipGetLastError();                                                                           \
   }
     SFA_D128G(2)
     SFA_D128G(4)
-    SFA_D128G(8)
+    if constexpr (32 / 8 % Dh<D>::kRPI == 0) {
+      SFA_D128G(8)
+    }
 #undef SFA_D128G
+    return hipErrorInvalidValue;
   }
   const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * p.num_splits * fwd_d128_head_groups(p);
   if (p.block_table)
-    hipLaunchKernelGGL(fwd_d128_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, p);
+    hipLaunchKernelGGL((fwd_d128_kernel<D, true>), dim3((unsigned)n), dim3(64), 0, s, p);
   else
-    hipLaunchKernelGGL(fwd_d128_kernel<false>, dim3((unsigned)n), dim3(64), 0, s, p);
+    hipLaunchKernelGGL((fwd_d128_kernel<D, false>), dim3((unsigned)n), dim3(64), 0, s, p);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fwd_d128(const Params& p, hipStream_t s) {
+  if (p.Dqk == 64) return launch_fwd_dh<64>(p, s);
+  return launch_fwd_dh<128>(p, s);
 }
 
 }  // namespace sfa

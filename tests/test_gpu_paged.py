@@ -47,12 +47,13 @@ CASES = [
     ("prefill", dict(S=512, K=64), 16, 0, False),
     ("train_gqa", dict(B=1, S=512, K=128), 32, 2, True),
     ("tiny", dict(), 8, 0, True),
+    ("prefill", dict(S=256, K=64, Hq=8, Dqk=64, Dv=64), 16, 2, True),
 ]
 
 
 @pytest.mark.parametrize("name,kw,page,splits,with_sink", CASES,
                          ids=["mla-decode", "mla-decode-splits3-sink", "mla-prefill-sink", "d128-mqa",
-                              "d128-gqa-splits2-sink", "generic-fp32-sink"])
+                              "d128-gqa-splits2-sink", "generic-fp32-sink", "d64-mqa-splits2-sink"])
 def test_paged_equals_contiguous(name, kw, page, splits, with_sink):
     _say(f"paged {name} {kw} page={page} splits={splits} sink={with_sink}")
     w = make_workload(name, device=DEV, **kw)

@@ -529,8 +529,53 @@ def test_autograd_function_and_dlse():
         assert _rel_l2(a.grad.cpu(), b.grad) <= GRAD_RL2
 
 
+@pytest.mark.parametrize("G,Hkv,splits,vk", [(1, 2, 0, False), (4, 1, 3, False), (16, 1, 0, True),
+                                              (32, 1, 0, True), (64, 1, 2, True), (64, 1, 0, False),
+                                              (48, 2, 0, False), (100, 1, 0, True), (20, 1, 4, False)])
+def test_d64_forward(G, Hkv, splits, vk):
+    """Head dim 64 (d_qk = d_v = 64, bf16), the width of sink-attention
+    models, on the register-gather MFMA forward: G <= 16 one wave per head
+    group of 16 (fwd_d128_kernel<64>), 16 < G <= 64 the shared-tile kernel
+    (fwd_d128g_kernel<64>: 2 or 4 waves gathering whole 8-row load
+    instructions), G > 64 head groups again.  v the same tensor as k (the
+    reference's single kv) or separate rows; split-k with the generic
+    combine; interior padding, ids past Skv and past kv_lens, a fully masked
+    row and a sink.  Against the oracle's bars; the backward at this width
+    runs the generic kernels, checked against the oracle too."""
+    _say(f"d=64 G={G} Hkv={Hkv} splits={splits} v_is_k={vk} B=2 S=160 Skv=200 K=80")
+    g = torch.Generator(device="cpu").manual_seed(640 + G + Hkv + splits)
+    B, S, Skv, K = 2, 160, 200, 80
+    Hq = G * Hkv
+    q = torch.randn(B, S, Hq, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Skv, Hkv, 64, generator=g).to(torch.bfloat16)
+    v = k if vk else torch.randn(B, Skv, Hkv, 64, generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, S, Hq, 64, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(Skv + 30, generator=g)[:K] - 15 for _ in range(B * S * Hkv)])
+    idx = idx.view(B, S, Hkv, K).to(torch.int32)
+    idx[:, :, :, K - 7:] = -1
+    idx[1, 3] = -1
+    kv_lens = torch.tensor([Skv, 151], dtype=torch.int32)
+    sink = torch.linspace(-1.0, 2.0, Hq)
+    scale = 1.0 / 8.0
+    o_ref, l_ref = ref_forward(q, k, v, idx, scale, kv_lens=kv_lens, sink=sink)
+    qd, kd, idd, kld, sd = (t.to(DEV) for t in (q, k, idx, kv_lens, sink))
+    vd = kd if vk else v.to(DEV)
+    out, lse = ops_amd.sfa_forward(qd, kd, vd, idd, scale, kv_lens=kld, attn_sink=sd, num_splits=splits)
+    _check_fwd(out, lse, o_ref, l_ref)
+    assert torch.all(out[1, 3] == 0)
+    if splits == 0 and G in (16, 64):
+        dq, dk, dv, ds = ops_amd.sfa_backward(qd, kd, vd, idd, out, lse, dout.to(DEV), scale, kv_lens=kld,
+                                              attn_sink=sd)
+        g_ref = ref_backward(q.float(), k.float(), v.float(), idx, o_ref, l_ref, dout.float(), scale,
+                             kv_lens=kv_lens, sink=sink)
+        for name, a, b in zip(("dq", "dk", "dv", "dsink"), (dq, dk, dv, ds), g_ref):
+            e = _rel_l2(a.cpu(), b)
+            assert e <= GRAD_RL2, f"{name} rel-L2 {e}"
+
+
 @pytest.mark.parametrize("H,D,dtypes", [(16, 128, (torch.float32, torch.bfloat16)), (64, 128, (torch.bfloat16,)),
-                                         (32, 576, (torch.bfloat16,))])
+                                         (32, 576, (torch.bfloat16,)), (64, 64, (torch.bfloat16,)),
+                                         (32, 64, (torch.bfloat16,))])
 def test_reference_signature_shim(H, D, dtypes):
     """SparseFlashAttentionTriton.apply(q[S,B,H,D], kv[S_kv,B,D], sink[H],
     idx[S,B,K], scale) -> out, with grads (q, kv, sink), against the oracle
