@@ -1,6 +1,7 @@
 // gfx950 MFMA backward of top-k sparse flash attention (bf16 in, fp32
-// accumulate), for head dims D = d_qk = d_v that are multiples of 32; up to
-// 16 query heads per workgroup (G > 16 is split into head groups of 16).
+// accumulate), for head dims D = d_qk = d_v that are multiples of 32
+// (instantiated for 128 and 64); up to 16 query heads per workgroup (G > 16
+// is split into head groups of 16).
 //
 // Reference: `_attn_bwd_dq_dsink` / `_inner_dq` (SFA.py:856-1002, 613-716) and
 // `_attn_bwd_dk_dv` / `_inner_dkv` (SFA.py:1005-1145, 719-853).  The reference
@@ -287,11 +288,12 @@ __global__ __launch_bounds__(C::kThreads, 1) void bwd_mfma_kernel(Params p) {
 }
 
 using CfgBwdD128 = BwdCfg<128>;
+using CfgBwdD64 = BwdCfg<64>;
 
 }  // namespace
 
 bool bwd_mfma_supported(const Params& p) {
-  if (p.Dqk != 128 || p.Dv != 128) return false;
+  if (p.Dqk != p.Dv || (p.Dqk != 128 && p.Dqk != 64)) return false;
   if (p.G > kMaxGroupB || p.topk > kBwdIdxCap) return false;
   const int64_t kb = 2 * ((int64_t)(p.Skv - 1) * p.k_ss + p.Dqk);
   const int64_t vb = 2 * ((int64_t)(p.Skv - 1) * p.v_ss + p.Dv);
@@ -299,9 +301,13 @@ bool bwd_mfma_supported(const Params& p) {
 }
 
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * ((p.G + 15) / 16);
   if (p.Dqk == 128 && p.Dv == 128) {
-    const int64_t n = (int64_t)p.B * p.Sq * p.Hkv * ((p.G + 15) / 16);
     hipLaunchKernelGGL(bwd_mfma_kernel<CfgBwdD128>, dim3((unsigned)n), dim3(CfgBwdD128::kThreads), 0, s, p);
+    return hipGetLastError();
+  }
+  if (p.Dqk == 64 && p.Dv == 64) {
+    hipLaunchKernelGGL(bwd_mfma_kernel<CfgBwdD64>, dim3((unsigned)n), dim3(CfgBwdD64::kThreads), 0, s, p);
     return hipGetLastError();
   }
   return hipErrorNotSupported;
