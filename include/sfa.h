@@ -81,6 +81,18 @@ enum {
                                slots repeating a key of their row take fp32 atomics), SFA_DKV_ATOMIC
                                adds every slot's fp32 row atomically                              */
 
+/* sfa_fwd_args.flags (the backward ignores them) */
+#define SFA_FWD_IDX_SORTED 1  /* every index row lists its valid keys in ascending order before any
+                                 padding (what sfa_indexer_topk writes).  Without it the persistent
+                                 MLA prefill (the MLA shape, no split-k, >= 4096 work items,
+                                 contiguous kv, top-k <= 2048, Skv <= 65536) first writes its rows
+                                 in that order into the workspace (valid keys ascending, then -1; a
+                                 row that repeats a key is kept as it is) and walks those: the
+                                 queries running together on an XCD then gather the same regions
+                                 of the prefix at about the same time and share them in its L2.
+                                 The result is the same softmax in another summation order
+                                 (differences at fp32 rounding).  The flag only skips that pass   */
+
 /* Error codes. */
 enum {
   SFA_OK = 0,
@@ -103,7 +115,7 @@ typedef struct sfa_fwd_args {
   void* out;       int64_t o_sb, o_ss, o_sh;
   float* lse;      int64_t l_sb, l_ss, l_sh;      /* head stride of lse             */
   int32_t num_splits;            /* split-k over the top-k set; 0 = library choice      */
-  int32_t flags;                 /* reserved, must be 0                                 */
+  int32_t flags;                 /* 0 or SFA_FWD_IDX_SORTED                             */
 } sfa_fwd_args;
 
 typedef struct sfa_bwd_args {
@@ -174,8 +186,10 @@ SFA_API const char* sfa_last_error(void);
 
 /* Bytes of device workspace sfa_fwd needs for `a` (0 when none).
  * Replaces the per-launch workspaces of SFA.py:117-120; what remains: the
- * split-k partial results of the decode shape, and 256 bytes of work-claim
- * counters for the persistent MLA prefill (>= 4096 work items). */
+ * split-k partial results of the decode shape, and for the persistent MLA
+ * prefill (>= 4096 work items) 256 bytes of work-claim counters plus, unless
+ * SFA_FWD_IDX_SORTED is set, its index rows in ascending order
+ * (B * Sq * Hkv * topk int32). */
 SFA_API size_t sfa_fwd_workspace_size(const sfa_fwd_args* a);
 
 /* Forward: out = softmax(scale * q k[idx]^T) v[idx], lse = log-sum-exp.
@@ -190,10 +204,13 @@ SFA_API int sfa_fwd(const sfa_fwd_args* a, void* workspace, size_t workspace_byt
  * callers that cannot allocate device memory (code under HIP-graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The workspace of
  * sfa_fwd (sfa_fwd_workspace_size(a) bytes: decode split-k partials, prefill
- * claim counters) goes to a static device
+ * claim counters and sorted index rows) goes to a static device
  * buffer of SFA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
  * until the process ends; a plan that needs more returns SFA_E_WORKSPACE
- * before any device work.  `stream` must belong to the current device; the
+ * before any device work, except the prefill's sorted index rows: when they
+ * do not fit, the rows are walked in their own order (the result then
+ * equals sfa_fwd's with SFA_FWD_IDX_SORTED set; bitwise equal to sfa_fwd
+ * whenever the sorted rows fit or the rows are already ascending).  `stream` must belong to the current device; the
  * first call on a device resolves the buffer's address (make it before any
  * graph capture).  All calls on one GPU share the buffer: calls that may
  * overlap on one GPU (unordered streams) race. */

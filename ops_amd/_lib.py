@@ -21,6 +21,7 @@ SFA_DKV_AUTO = 0
 SFA_DKV_ATOMIC = 1
 SFA_DKV_CSR = 2
 SFA_BWD_MERGE_KV = 1  # sfa_bwd_args.flags: dk receives dK + dV of rows k and v share
+SFA_FWD_IDX_SORTED = 1  # sfa_fwd_args.flags: index rows are ascending (no sort pass before the MLA prefill)
 
 SFA_OK = 0
 SFA_E_INVALID = -1

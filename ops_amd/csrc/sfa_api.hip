@@ -50,7 +50,7 @@ int check_fwd(const sfa_fwd_args* a) {
   if (a->Dqk <= 0 || a->Dv <= 0 || a->Dqk > kMaxHeadDim || a->Dv > kMaxHeadDim)
     return fail(SFA_E_INVALID, "head dims must be in [1, %d]", kMaxHeadDim);
   if (!a->q || !a->k || !a->v || !a->idx || !a->out || !a->lse) return fail(SFA_E_INVALID, "null tensor pointer");
-  if (a->flags != 0) return fail(SFA_E_INVALID, "flags must be 0");
+  if ((a->flags & ~SFA_FWD_IDX_SORTED) != 0) return fail(SFA_E_INVALID, "unknown flags 0x%x", (unsigned)a->flags);
   if (a->num_splits < 0) return fail(SFA_E_INVALID, "num_splits must be >= 0");
   if (!(a->scale == a->scale) || isinf(a->scale)) return fail(SFA_E_INVALID, "scale must be finite");
   return SFA_OK;
@@ -131,13 +131,17 @@ struct FwdPlan {
   size_t part_o_bytes;
   size_t part_lse_bytes;
   size_t sched_bytes;  // claim counters of the persistent forward (0 when not persistent)
-  size_t workspace() const { return part_o_bytes + part_lse_bytes + sched_bytes; }
+  size_t sort_bytes;   // the index rows in ascending key order (0 when not sorted)
+  size_t workspace() const { return part_o_bytes + part_lse_bytes + sched_bytes + sort_bytes; }
 };
 
 constexpr int kTargetWorkgroups = 512;  // 2 per CU on a 256-CU MI355X
 constexpr int kMaxSplits = 64;  // the combine kernel holds one split per lane of a wave
 
-FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
+// sort_room: the most workspace bytes the sorted index rows may take
+// (sfa_fwd_noalloc: what its static scratch leaves); rows that do not fit
+// are used in their own order.
+FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, size_t sort_room = SIZE_MAX) {
   FwdPlan pl{};
   sfa::Params p = to_params(a, pg);
   pl.mfma = mfma_layout_ok(a) && sfa::fwd_mfma_supported(p);
@@ -178,7 +182,15 @@ FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg) {
   if (pl.mfma) {
     p.num_splits = pl.num_splits;
     p.split_len = pl.split_len;
-    if (sfa::fwd_mfma_persistent(p)) pl.sched_bytes = 256;
+    if (sfa::fwd_mfma_persistent(p)) {
+      pl.sched_bytes = 256;
+      // the persistent MLA prefill walks ascending rows (L2 sharing between
+      // the queries running together on an XCD); contiguous KV only
+      if (!(a->flags & SFA_FWD_IDX_SORTED) && pg == nullptr && sfa::idx_sort_supported(p)) {
+        const size_t bytes = align_up((size_t)a->B * a->Sq * a->Hkv * a->topk * sizeof(int32_t), 256);
+        if (bytes + pl.sched_bytes <= sort_room) pl.sort_bytes = bytes;
+      }
+    }
   }
   return pl;
 }
@@ -191,9 +203,10 @@ int check_generic_fwd(const sfa_fwd_args* a) {
 }
 
 // The forward of sfa_fwd (pg == nullptr) and sfa_fwd_paged, after validation.
-int run_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, void* workspace, size_t workspace_bytes, void* stream) {
+int run_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, void* workspace, size_t workspace_bytes, void* stream,
+            size_t sort_room = SIZE_MAX) {
   hipStream_t s = (hipStream_t)stream;
-  const FwdPlan pl = plan_fwd(a, pg);
+  const FwdPlan pl = plan_fwd(a, pg, sort_room);
   sfa::Params p = to_params(a, pg);
   int rc;
   hipError_t e;
@@ -207,6 +220,15 @@ int run_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, void* workspace, size
       p.part_lse = (float*)((char*)workspace + pl.part_o_bytes);
     }
     if (pl.sched_bytes > 0) p.sched = (int*)((char*)workspace + pl.part_o_bytes + pl.part_lse_bytes);
+    if (pl.sort_bytes > 0) {
+      int32_t* sorted = (int32_t*)((char*)workspace + pl.part_o_bytes + pl.part_lse_bytes + pl.sched_bytes);
+      e = sfa::launch_idx_sort(p, sorted, s);
+      if (e != hipSuccess) return hip_fail(e, "sfa_fwd (index sort)");
+      p.idx = sorted;
+      p.i_sh = a->topk;
+      p.i_ss = (int64_t)a->Hkv * a->topk;
+      p.i_sb = (int64_t)a->Sq * a->Hkv * a->topk;
+    }
     e = sfa::launch_fwd_mfma(p, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_fwd (mfma)");
     if (pl.num_splits > 1) {
@@ -295,7 +317,9 @@ int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream) {
   g_err[0] = 0;
   const int rc = check_fwd(a);
   if (rc != SFA_OK) return rc;
-  const FwdPlan pl = plan_fwd(a, nullptr);
+  // (index rows whose sorted copy does not fit the scratch are used in their
+  // own order)
+  const FwdPlan pl = plan_fwd(a, nullptr, kNoallocBytes);
   const size_t need = pl.workspace();
   if (need > kNoallocBytes)
     return fail(SFA_E_WORKSPACE,
@@ -307,7 +331,7 @@ int sfa_fwd_noalloc(const sfa_fwd_args* a, void* stream) {
     const int r = noalloc_scratch(stream, &ws);
     if (r != SFA_OK) return r;
   }
-  return run_fwd(a, nullptr, ws, need > 0 ? kNoallocBytes : 0, stream);
+  return run_fwd(a, nullptr, ws, need > 0 ? kNoallocBytes : 0, stream, kNoallocBytes);
 }
 
 size_t sfa_fwd_paged_workspace_size(const sfa_fwd_args* a, const sfa_kv_pages* pages) {

@@ -339,6 +339,10 @@ bool fwd_mfma_supported(const Params& p);
 int fwd_mfma_tile_keys(const Params& p);
 int fwd_mfma_idx_cap(const Params& p);  // index slots one work item (split) stages
 bool fwd_mfma_persistent(const Params& p);  // needs Params::sched (8 ints of workspace)
+// index rows in ascending key order, then -1 (sfa_idx_sort.hip): out holds
+// B * Sq * Hkv rows of topk slots, contiguous
+bool idx_sort_supported(const Params& p);
+hipError_t launch_idx_sort(const Params& p, int32_t* out, hipStream_t s);
 int fwd_mfma_head_groups(const Params& p);  // workgroups per (work item, split): head groups
 int fwd_d128_idx_cap(const Params& p);
 // d = 128: register-direct gather, 16 heads per wave (sfa_fwd_d128.hip)

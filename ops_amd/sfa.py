@@ -82,7 +82,7 @@ def _validate(q, k, v, idx, kv_lens, sink):
         raise ValueError("attn_sink must be a [Hq] tensor on q's device")
 
 
-def _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits) -> _lib.FwdArgs:
+def _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits, idx_sorted=False) -> _lib.FwdArgs:
     B, Sq, Hq, Dqk = q.shape
     _, Skv, Hkv, _ = k.shape
     a = _lib.FwdArgs()
@@ -99,7 +99,7 @@ def _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits) -> _lib.
     a.out, (a.o_sb, a.o_ss, a.o_sh) = out.data_ptr(), out.stride()[:3]
     a.lse, (a.l_sb, a.l_ss, a.l_sh) = lse.data_ptr(), lse.stride()
     a.num_splits = int(num_splits)
-    a.flags = 0
+    a.flags = _lib.SFA_FWD_IDX_SORTED if idx_sorted else 0
     return a
 
 
@@ -120,12 +120,16 @@ def _prep(q, k, v, topk_idxs, kv_lens, sink, validate=True):
 
 
 def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None, num_splits: int = 0,
-                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, noalloc: bool = False):
+                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, noalloc: bool = False,
+                idx_sorted: bool = False):
     """Forward only (no autograd): ``(out, lse)``.  ``out``/``lse`` may be
     preallocated ([B, Sq, Hq, Dv] in q's dtype / [B, Sq, Hq] float32).
     ``noalloc=True`` calls ``sfa_fwd_noalloc``: the split-k partials then live
     in the library's static per-GPU scratch (64 MiB) instead of a workspace
-    tensor, so with preallocated ``out``/``lse`` nothing is allocated."""
+    tensor, so with preallocated ``out``/``lse`` nothing is allocated.
+    ``idx_sorted=True`` declares every index row ascending before its padding
+    (as :func:`ops_amd.indexer.indexer_topk` writes them): the MLA prefill
+    then skips the pass that sorts them (``SFA_FWD_IDX_SORTED``)."""
     lib = _lib.load()
     q, k, v, idx, kv_lens, sink = _prep(q, k, v, topk_idxs, kv_lens, attn_sink)
     B, Sq, Hq, Dqk = q.shape
@@ -135,7 +139,7 @@ def sfa_forward(q, k, v, topk_idxs, sm_scale=None, kv_lens=None, attn_sink=None,
         out = torch.empty((B, Sq, Hq, Dv), dtype=q.dtype, device=q.device)
     if lse is None:
         lse = torch.empty((B, Sq, Hq), dtype=torch.float32, device=q.device)
-    a = _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits)
+    a = _fwd_args(q, k, v, idx, out, lse, scale, kv_lens, sink, num_splits, idx_sorted)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     if noalloc:
         _lib.check(lib.sfa_fwd_noalloc(ctypes.byref(a), ctypes.c_void_p(stream)))

@@ -75,7 +75,7 @@ def _valid_args():
 
 @pytest.mark.parametrize("field,value", [
     ("topk", 0), ("topk", -3), ("Hkv", 3), ("B", 0), ("Dqk", 0), ("Dqk", 5000), ("dtype", 7), ("num_splits", -1),
-    ("flags", 1), ("q", None),
+    ("flags", 2), ("flags", -1), ("q", None),
 ])
 def test_invalid_arguments_are_rejected(field, value):
     lib = _lib.load()
@@ -114,6 +114,41 @@ def test_workspace_sizes_follow_the_plan():
     b.fwd = _valid_args()
     need = lib.sfa_bwd_workspace_size(ctypes.byref(b))
     assert need >= (8 * 128 * 2 + 4 * 16) * 4
+
+
+def _mla_prefill_args(S, K, Skv=None):
+    a = _valid_args()
+    Skv = S if Skv is None else Skv
+    a.B, a.Sq, a.Skv, a.Hq, a.Hkv, a.Dqk, a.Dv, a.topk = 1, S, Skv, 128, 1, 576, 512, K
+    a.k_ss = a.v_ss = a.k_sh = a.v_sh = 576
+    a.k_sb = a.v_sb = Skv * 576
+    a.q_sh, a.q_ss, a.q_sb = 576, 128 * 576, S * 128 * 576
+    a.o_sh, a.o_ss, a.o_sb = 512, 128 * 512, S * 128 * 512
+    a.v = a.k
+    a.i_sh, a.i_ss, a.i_sb = K, K, S * K
+    return a
+
+
+def test_persistent_prefill_workspace_holds_sorted_index_rows():
+    """The persistent MLA prefill (>= 4096 work items) takes 256 bytes of
+    claim counters plus its index rows in ascending order (B*Sq*Hkv*topk
+    int32) unless SFA_FWD_IDX_SORTED declares them sorted; fewer items (the
+    plain grid) or Skv beyond the sort's 65536-key bitmap take no sorted
+    copy."""
+    lib = _lib.load()
+    a = _mla_prefill_args(32768, 2048)
+    rows = 32768 * 2048 * 4
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 256 + rows
+    a.flags = _lib.SFA_FWD_IDX_SORTED
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 256
+    a = _mla_prefill_args(4096, 100)  # rows padded to 256 bytes
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 256 + (4096 * 100 * 4 + 255) // 256 * 256
+    a = _mla_prefill_args(4000, 2048)  # plain grid: no counters, no sort
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 0
+    a = _mla_prefill_args(4096, 2048, Skv=70000)
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 256
+    a = _mla_prefill_args(4096, 4096)  # top-k beyond the sort's 2048 slots (two splits of 2048)
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) > 0
 
 
 def test_bwd_rejects_missing_gradients_and_csr_mode():
