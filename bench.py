@@ -655,8 +655,12 @@ def run_probe(name, args):
                      DMA, two 32-row tiles in flight, one barrier per tile),
                      caches flushed before each step as in the decode bench,
                      in the work layouts the decode design compares; the
-                     real decode step (prepared sfa_fwd call) is timed
-                     beside them."""
+                     same rows read into registers with as many loads in
+                     flight as 1-32 waves per CU allow (no LDS, no tiles:
+                     the ceiling of random 1152-byte rows on the part), a
+                     contiguous read of the same bytes (the streaming
+                     reference); the real decode step (prepared sfa_fwd
+                     call) is timed beside them."""
     import ctypes
     import torch
     if name == "gemm":
@@ -713,6 +717,25 @@ def run_probe(name, args):
                           "us": round(us, 2), "us_median": round(statistics.median(t) * 1e3, 2),
                           "gathered_gbs": round(gathered * hg / (us * 1e-6) / 1e9, 1),
                           "algorithmic_gbs": round(gathered / (us * 1e-6) / 1e9, 1)}), flush=True)
+    lib.sfa_probe_rowread.restype = ctypes.c_int
+    lib.sfa_probe_rowread.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    sink = torch.empty(2048 * 256, dtype=torch.int32, device="cuda")
+    for contiguous in (0, 1):
+        for wgs in (256, 512, 1024, 2048):
+            fn = lambda: lib.sfa_probe_rowread(ctypes.c_void_p(w.k.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+                                               ctypes.c_void_p(sink.data_ptr()), B, Skv, K, wgs, contiguous,
+                                               ctypes.c_void_p(stream))
+            rc = fn()
+            if rc != 0:
+                raise SystemExit(f"sfa_probe_rowread failed: {rc}")
+            t, _ = time_steps(fn, args.steps * 4, args.warmup, before=flush)
+            us = sum(t) / len(t) * 1e3
+            what = ("contiguous read of the same bytes" if contiguous else
+                    "the rows into registers (ceiling: no LDS, no tiles)")
+            print(json.dumps({"probe": "decode_gather", "layout": f"{what}, {wgs // 64} waves per CU",
+                              "workgroups": wgs, "us": round(us, 2), "us_median": round(statistics.median(t) * 1e3, 2),
+                              "algorithmic_gbs": round(gathered / (us * 1e-6) / 1e9, 1)}), flush=True)
     out = torch.empty((B, 1, Hq, w.v.shape[3]), dtype=w.q.dtype, device="cuda")
     lse = torch.empty((B, 1, Hq), dtype=torch.float32, device="cuda")
     fn = prepared_forward(w, out, lse)

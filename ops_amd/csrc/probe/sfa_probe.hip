@@ -106,6 +106,47 @@ __global__ __launch_bounds__(kPThreads, 1) void probe_gather_kernel(ProbeArgs a)
   }
 }
 
+// The ceiling of the same rows' data movement: every valid row of the
+// [B][topk] index set read once, 16 bytes per lane into registers (no LDS,
+// no tiles, no barriers), with as many independent loads in flight as the
+// grid allows: thread i of the grid takes 16-byte chunks i, i + nthreads,
+// ... of the flattened list of (row, chunk) pairs, U at a time (the U index
+// loads first, then the U row loads).  contiguous = 1 reads the same number
+// of bytes from the start of the KV buffer instead (the streaming
+// reference).  Each thread folds what it read into one word it writes to
+// `sink`, so no load is dead.
+template <int U>
+__global__ __launch_bounds__(256) void probe_rowread_kernel(const u32x4* __restrict__ kv, const int32_t* __restrict__ idx,
+                                                            uint32_t* __restrict__ sink, int B, int Skv, int topk,
+                                                            int64_t nchunks, int contiguous) {
+  constexpr int kCPR = 72;  // 16-byte chunks per 1152-byte row
+  const int64_t nth = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (int64_t c0 = tid; c0 < nchunks; c0 += nth * U) {
+    int64_t off[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + (int64_t)u * nth;
+      if (contiguous) {
+        off[u] = c < nchunks ? c : -1;
+      } else {
+        const int64_t r = c / kCPR;  // (sequence, slot) pair
+        const int ch = (int)(c - r * kCPR);
+        const int b = (int)(r / topk);
+        const int key = c < nchunks ? idx[r] : -1;
+        off[u] = key >= 0 && key < Skv ? ((int64_t)b * Skv + key) * kCPR + ch : -1;
+      }
+    }
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = off[u] >= 0 ? kv[off[u]] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  sink[tid] = acc;
+}
+
 }  // namespace
 }  // namespace sfa
 
@@ -127,6 +168,26 @@ __attribute__((visibility("default"))) int sfa_probe_gather(const void* kv, cons
   sfa::ProbeArgs a{kv, q, idx, part, B, Skv, topk, splits, hgroups, q_bytes, store_rows, q_row_bytes};
   const unsigned grid = (unsigned)((int64_t)B * splits * hgroups);
   hipLaunchKernelGGL(sfa::probe_gather_kernel, dim3(grid), dim3(sfa::kPThreads), 0, (hipStream_t)stream, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+// Launches probe_rowread_kernel<8> on `stream`: `workgroups` x 256 threads
+// read every valid row of idx ([B][topk]; a slot is valid iff 0 <= id < Skv,
+// rows in order of the compacted list `rows` = the number of (b, slot) pairs
+// to read, i.e. idx is read as a flat list of `rows` ids whose batch is
+// position / topk) -- or, with contiguous, the same bytes from the start of
+// kv.  sink: workgroups * 256 words.  Returns 0, -1 for bad arguments, or
+// the HIP error of the launch.
+__attribute__((visibility("default"))) int sfa_probe_rowread(const void* kv, const int32_t* idx, void* sink, int B,
+                                                             int Skv, int topk, int workgroups, int contiguous,
+                                                             void* stream) {
+  if (kv == nullptr || sink == nullptr || B <= 0 || Skv <= 0 || topk <= 0 || workgroups <= 0) return -1;
+  if (!contiguous && idx == nullptr) return -1;
+  if (contiguous && topk > Skv) return -1;  // the contiguous bytes must lie in kv
+  const int64_t nchunks = (int64_t)B * topk * 72;
+  hipLaunchKernelGGL(sfa::probe_rowread_kernel<8>, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream,
+                     (const sfa::u32x4*)kv, idx, (uint32_t*)sink, B, Skv, topk, nchunks, contiguous);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : (int)e;
 }

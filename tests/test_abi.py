@@ -308,3 +308,12 @@ def test_probe_library_rejects_bad_arguments_without_launching():
         a = {**ok, **bad}
         assert f(a["kv"], a["q"], a["qr"], a["idx"], a["part"], a["B"], a["Skv"], a["K"], a["s"], a["hg"], a["qb"],
                  a["rows"], None) == -1, bad
+    g = lib.sfa_probe_rowread
+    g.restype = ctypes.c_int
+    g.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    ok = dict(kv=0x10000, idx=0x10000, sink=0x10000, B=64, Skv=65536, K=2048, wgs=256, cont=0)
+    for bad in (dict(kv=None), dict(sink=None), dict(B=0), dict(wgs=0), dict(idx=None),
+                dict(cont=1, Skv=1024)):
+        a = {**ok, **bad}
+        assert g(a["kv"], a["idx"], a["sink"], a["B"], a["Skv"], a["K"], a["wgs"], a["cont"], None) == -1, bad
