@@ -85,7 +85,7 @@ enum {
 #define SFA_FWD_IDX_SORTED 1  /* every index row lists its valid keys in ascending order before any
                                  padding (what sfa_indexer_topk writes).  Without it the persistent
                                  MLA prefill (the MLA shape, no split-k, >= 4096 work items,
-                                 contiguous kv, top-k <= 2048, Skv <= 65536) first writes its rows
+                                 top-k <= 2048, Skv <= 65536; contiguous or paged kv) first writes its rows
                                  in that order into the workspace (valid keys ascending, then -1; a
                                  row that repeats a key is kept as it is) and walks those: the
                                  queries running together on an XCD then gather the same regions

@@ -185,8 +185,9 @@ FwdPlan plan_fwd(const sfa_fwd_args* a, const sfa_kv_pages* pg, size_t sort_room
     if (sfa::fwd_mfma_persistent(p)) {
       pl.sched_bytes = 256;
       // the persistent MLA prefill walks ascending rows (L2 sharing between
-      // the queries running together on an XCD); contiguous KV only
-      if (!(a->flags & SFA_FWD_IDX_SORTED) && pg == nullptr && sfa::idx_sort_supported(p)) {
+      // the queries running together on an XCD); paged KV too (the rows hold
+      // logical keys), so a paged call walks the same slots as a contiguous one
+      if (!(a->flags & SFA_FWD_IDX_SORTED) && sfa::idx_sort_supported(p)) {
         const size_t bytes = align_up((size_t)a->B * a->Sq * a->Hkv * a->topk * sizeof(int32_t), 256);
         if (bytes + pl.sched_bytes <= sort_room) pl.sort_bytes = bytes;
       }

@@ -149,6 +149,14 @@ def test_persistent_prefill_workspace_holds_sorted_index_rows():
     assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) == 256
     a = _mla_prefill_args(4096, 4096)  # top-k beyond the sort's 2048 slots (two splits of 2048)
     assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) > 0
+    # paged: the rows hold logical keys, sorted the same way
+    a = _mla_prefill_args(8192, 2048)
+    a.k_sb = a.v_sb = 64 * 576  # 64-row pages
+    pg = _lib.KvPages()
+    pg.block_table, pg.bt_sb, pg.max_pages, pg.page_size, pg.num_pages, pg.flags = 0x10000, 128, 128, 64, 128, 0
+    assert lib.sfa_fwd_paged_workspace_size(ctypes.byref(a), ctypes.byref(pg)) == 256 + 8192 * 2048 * 4
+    a.flags = _lib.SFA_FWD_IDX_SORTED
+    assert lib.sfa_fwd_paged_workspace_size(ctypes.byref(a), ctypes.byref(pg)) == 256
 
 
 def test_bwd_rejects_missing_gradients_and_csr_mode():

@@ -49,18 +49,19 @@ def host_sorted(idx, bounds):
     return out
 
 
-def _case(B, S, Skv, K, seed, kv_lens=None):
+def _case(B, S, Skv, K, seed, Hkv=1):
     g = torch.Generator(device="cpu").manual_seed(seed)
-    Hq = 128
+    Hq = 128 * Hkv
     q = torch.randn(B, S, Hq, 576, generator=g).bfloat16()
-    kv = torch.randn(B, Skv, 1, 576, generator=g).bfloat16()
-    idx = torch.full((B, S, 1, K), -1, dtype=torch.int32)
+    kv = torch.randn(B, Skv, Hkv, 576, generator=g).bfloat16()
+    idx = torch.full((B, S, Hkv, K), -1, dtype=torch.int32)
     for b in range(B):
         for t in range(S):
             # causal prefix of a query placed at the end of the context
             top = Skv - S + t + 1
             n = min(K, top)
-            idx[b, t, 0, :n] = torch.randperm(top, generator=g)[:n].to(torch.int32)
+            for h in range(Hkv):
+                idx[b, t, h, :n] = torch.randperm(top, generator=g)[:n].to(torch.int32)
     return q, kv, idx
 
 
@@ -68,11 +69,11 @@ def _plant(idx, bounds, seed):
     """Rows the rule treats specially: repeats, keys >= bound, odd padding,
     empty rows, padding in the middle of a row."""
     g = torch.Generator(device="cpu").manual_seed(seed)
-    B, S, _, K = idx.shape
+    B, S, H, K = idx.shape
     rows = torch.randperm(S, generator=g)[:40].tolist()
     for j, t in enumerate(rows):
         b = j % B
-        r = idx[b, t, 0]
+        r = idx[b, t, j % H]
         kind = j % 5
         if kind == 0:    # a repeated key (row stays in its own order)
             r[5] = r[1]
@@ -119,6 +120,36 @@ def test_sorted_pass_is_bitwise_the_host_sorted_forward(B, S, Skv, K, lens):
     err_o = float((o_a[:, rows].float().cpu() - o_ref).abs().max())
     finite = torch.isfinite(l_ref)
     assert torch.equal(torch.isfinite(l_a[:, rows].cpu()), finite)
+    err_l = float((l_a[:, rows].cpu()[finite] - l_ref[finite]).abs().max())
+    assert err_o <= 2e-2 and err_l <= 1e-3, (err_o, err_l)
+
+
+def test_sorted_pass_two_kv_heads_strided_rows():
+    """Two KV heads (Hq = 256, 128 heads each) and index rows read through a
+    strided view (head stride K + 48, a padded last dimension): the pass
+    decodes (b, t, g) from its row number and reads the caller's strides;
+    bitwise the forward on host-sorted rows, sampled rows against the
+    oracle."""
+    B, S, Skv, K, H = 1, 2080, 3000, 256, 2
+    _say(f"index sort: B={B} S={S} Skv={Skv} K={K} Hkv={H}, strided index rows")
+    q, kv, idx = _case(B, S, Skv, K, seed=29, Hkv=H)
+    bounds = torch.tensor([Skv], dtype=torch.int32)
+    idx = _plant(idx, bounds, seed=9)
+    exp = host_sorted(idx, bounds)
+    wide = torch.full((B, S, H, K + 48), 7, dtype=torch.int32)
+    wide[..., :K] = idx
+    scale = 1.0 / math.sqrt(576)
+    dq, dkv, de = (t.to(DEV) for t in (q, kv, exp))
+    di = wide.to(DEV)[..., :K]
+    assert di.stride() == (S * H * (K + 48), H * (K + 48), K + 48, 1)
+    o_a, l_a = ops_amd.sfa_forward(dq, dkv, dkv[..., :512], di, scale)
+    o_b, l_b = ops_amd.sfa_forward(dq, dkv, dkv[..., :512], de, scale, idx_sorted=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_a, o_b) and torch.equal(l_a, l_b)
+    rows = torch.tensor([0, 5, S // 3, S - 1])
+    o_ref, l_ref = ref_forward(q[:, rows].float(), kv.float(), kv[..., :512].float(), idx[:, rows], scale)
+    err_o = float((o_a[:, rows].float().cpu() - o_ref).abs().max())
+    finite = torch.isfinite(l_ref)
     err_l = float((l_a[:, rows].cpu()[finite] - l_ref[finite]).abs().max())
     assert err_o <= 2e-2 and err_l <= 1e-3, (err_o, err_l)
 
