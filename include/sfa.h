@@ -57,7 +57,7 @@ enum { SFA_DTYPE_F32 = 0, SFA_DTYPE_BF16 = 1, SFA_DTYPE_FP8_E4M3 = 2 };
 /* How the backward produces dK/dV. */
 enum {
   SFA_DKV_AUTO = 0,    /* CSR where supported (bf16, d_qk = d_v = 128, G a power of two
-                          <= 16, top-k <= 2048, Skv <= 262144) and cheaper: Skv <=
+                          <= 128, top-k <= 2048, Skv <= 262144) and cheaper: Skv <=
                           64 * top-k and CSR workspace (bitmap, lists, fp32 partials,
                           which grow as Skv * Sq * G / 16 bytes per batch and kv head)
                           <= 4 GiB; otherwise ATOMIC                                   */

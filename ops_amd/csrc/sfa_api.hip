@@ -491,7 +491,7 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
   const bool csr = use_csr(a, p);
   if (a->dkv_mode == SFA_DKV_CSR && !csr)
     return fail(SFA_E_UNSUPPORTED,
-                "SFA_DKV_CSR needs bf16, d_qk = d_v = 128, G in {1, 2, 4, 8, 16}, top-k <= 2048, "
+                "SFA_DKV_CSR needs bf16, d_qk = d_v = 128, G a power of two <= 128, top-k <= 2048, "
                 "Skv <= 262144 and row offsets below 2^31 bytes");
   if (!(bwd_mfma_ok(a) && sfa::bwd_mfma_supported(p)) && f.topk > kGenericMaxTopk)
     return fail(SFA_E_UNSUPPORTED, "topk %d exceeds %d", f.topk, kGenericMaxTopk);
