@@ -406,16 +406,20 @@ bool mla_det(const sfa_bwd_args* a, const sfa::Params& p) {
 }
 
 // Its workspace holds one chunk of work items (P / dS, and the contribution
-// rows and index maps when deterministic): up to about 2 GiB, in whole rounds
-// of 256 items (one dK/dV workgroup per CU of the 256-CU part; a partial
-// last round would leave most CUs idle), at least 8 items so the dQ pass can
-// place both head groups of an item on one XCD.
+// rows and index maps when deterministic): up to about 3 GiB deterministic
+// (1024 queries at top-k 2048: each chunk costs a fixed ~40 us of launches
+// and reduction set-up, so 32 chunks of 1024 run 1.7 % faster than 64 of
+// 512 at S = 32768) or 2 GiB with atomics (larger chunks gain nothing
+// there), in whole rounds of 256 items (one dK/dV workgroup per CU of the
+// 256-CU part; a partial last round would leave most CUs idle), at least 8
+// items so the dQ pass can place both head groups of an item on one XCD.
+constexpr size_t kMlaChunkBytesDet = size_t(3) << 30;
 constexpr size_t kMlaChunkBytes = size_t(2) << 30;
 constexpr int64_t kMlaChunkRound = 256;
 
 int mla_chunk_items(const sfa::Params& p, bool det) {
   const int64_t items = (int64_t)p.B * p.Sq * p.Hkv;
-  int64_t n = (int64_t)(kMlaChunkBytes / sfa::bwd_mla_bytes_per_item(p, det));
+  int64_t n = (int64_t)((det ? kMlaChunkBytesDet : kMlaChunkBytes) / sfa::bwd_mla_bytes_per_item(p, det));
   n = n >= kMlaChunkRound ? n / kMlaChunkRound * kMlaChunkRound : (n / 8 * 8 > 8 ? n / 8 * 8 : 8);
   const int64_t cap = sfa::bwd_mla_max_chunk_items(det);  // a multiple of kMlaChunkRound
   if (n > cap) n = cap;

@@ -86,6 +86,40 @@ def test_graph_mla_decode_splitk():
         assert torch.equal(lse_g, lse_e), f"replay {r}: lse differs"
 
 
+def test_graph_mla_prefill_persistent_sorted():
+    """Persistent MLA prefill (4160 work items, 128 heads on one latent row,
+    d_qk 576 / d_v 512) on shuffled index rows: the index sort pass, the
+    claim-counter reset and the persistent forward in one graph; new index
+    rows and Q values are written in place before each replay, so every
+    replay sorts and claims afresh."""
+    S, K = 4160, 256
+    _say(f"graph: persistent MLA prefill with the index sort pass S={S} K={K}")
+    gen = torch.Generator().manual_seed(23)
+    kv = torch.randn(1, S, 1, 576, generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.empty(1, S, 128, 576, dtype=torch.bfloat16, device=DEV)
+    idx = torch.empty(1, S, 1, K, dtype=torch.int32, device=DEV)
+    v = kv[..., :512]
+
+    def step():
+        return ops_amd.sfa_forward(q, kv, v, idx, None)
+
+    def refill():
+        q.copy_(torch.randn(q.shape, generator=gen).to(torch.bfloat16))
+        idx.copy_(_idx_rows(1, S, 1, K, lambda b, t: t + 1, gen))
+
+    refill()
+    g, (out_g, lse_g) = _capture(step)
+    for r in range(3):
+        refill()
+        out_e, lse_e = step()
+        torch.cuda.synchronize()
+        _eager_noise(r)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), f"replay {r}: out differs"
+        assert torch.equal(lse_g, lse_e), f"replay {r}: lse differs"
+
+
 def test_graph_gqa_backward_deterministic():
     """GQA backward, deterministic dK/dV scheme: δ pass, index inversion, dQ,
     key-major dK/dV, chunk-ordered reduction and the bf16 finish in one graph."""

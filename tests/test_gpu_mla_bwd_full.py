@@ -2,7 +2,7 @@
 and at shapes that reach its multi-word index maps and chunk boundaries.
 
 * The full MLA prefill workload (B=1, S=32768, Hq=128, d_qk 576 / d_v 512,
-  top-k 2048) in both dK/dV modes: 64 chunks of 512 queries, 1024 bitmap
+  top-k 2048) in both dK/dV modes: 32 chunks of 1024 queries, 1024 bitmap
   words per query and a reduction over 32768 keys in the deterministic mode.
   Gradients are written into NaN-filled tensors, so every row must be
   written; dQ of sampled query rows is checked against the CPU oracle and the
@@ -112,7 +112,7 @@ def test_mla_bwd_full_workload(full_mla, mode):
 
 @pytest.mark.parametrize("mode", ["auto", "atomic"])
 def test_mla_bwd_skv8192_masking_sink_dlse(mode):
-    """Skv = 8192 (256 bitmap words per query, 16 chunks per sequence in the
+    """Skv = 8192 (256 bitmap words per query, 8 chunks per sequence in the
     deterministic mode) with interior and trailing padding, ids past Skv and
     past kv_lens, a fully masked row, a sink and a gradient on LSE."""
     _say(f"MLA bwd B=2 S=8192 Hq=128 K=2048 sink/dlse/kv_lens/masked row, dkv_mode={mode}")
@@ -168,7 +168,7 @@ def _causal_rows(B, S, Hkv, K, gen):
 @pytest.mark.parametrize("mode", ["auto", "atomic"])
 def test_mla_bwd_two_kv_heads_chunk_inside_sequence(mode):
     """B = 2, Hq = 256 over Hkv = 2 (G = 128), S = 640, top-k 2048: 2560 work
-    items, so the deterministic mode's 512-item chunks and the atomic mode's
+    items, so the deterministic mode's 1024-item chunks and the atomic mode's
     2048-item chunk both end inside a sequence, and the reduction's item range
     per (batch, kv head) starts mid-sequence with a stride of two kv heads."""
     _say(f"MLA bwd B=2 S=640 Hq=256 Hkv=2 K=2048, dkv_mode={mode}")
