@@ -903,7 +903,7 @@ def pmc_markdown(summary, targets=None):
             continue
         rows = [r for r in rows if not _is_library_kernel(r["kernel"])]
         lines += [f"### {target}", "",
-                  "| kernel | WGs x thr | VGPR/AGPR/LDS | us | GHz | waves/SIMD | MFMA busy | wait-inst | "
+                  "| kernel | WGs x thr | LDS B | us | GHz | waves/SIMD | MFMA busy | wait-inst | "
                   "MFMA / VALU / LDS / SALU / VMEM insts | fetch GB (GB/s) | RDREQ GB | write GB (GB/s) | "
                   "L2 hit | L2 lat | TA / TD busy | LDS confl |",
                   "|" + "---|" * 16]
@@ -912,7 +912,7 @@ def pmc_markdown(summary, targets=None):
                              for n in ("mfma", "valu", "lds", "salu", "vmem"))
             gb = lambda b: f"{b / 1e9:.3f}" if b is not None else "-"
             lines.append(
-                f"| {r['kernel'][:60]} | {r['workgroups']} x {r['wg_threads']} | {r['vgpr']}/{r['agpr']}/{r['lds']} | "
+                f"| {r['kernel'][:60]} | {r['workgroups']} x {r['wg_threads']} | {r['lds']} | "
                 f"{f(r.get('pass1_us'), 1)} | {f(r.get('clock_ghz'), 2)} | {f(r.get('waves_per_simd'), 2)} | "
                 f"{f(r.get('mfma_busy'))} | {f(r.get('wait_inst_frac'))} | {ins} | "
                 f"{gb(r.get('fetch_bytes'))} ({f(r.get('fetch_gbs'), 0)}) | {gb(r.get('rdreq_bytes'))} | "
