@@ -52,7 +52,7 @@ namespace {
 constexpr float kRescaleSlack = 8.0f;
 constexpr int kIdxCap = 2048;  // slots staged in LDS per work item
 #ifndef MLA_QREG
-#define MLA_QREG 18
+#define MLA_QREG 20
 #endif
 
 template <int T_, int DQK_, int DV_, int NSLICE_, int NSPLITW_, bool VK_, int QREG_, bool SWZ_ = false>
