@@ -40,14 +40,14 @@ def _decode_case(B, Skv, Hq, Hkv, Dqk, Dv, K, seed, shared_kv):
     return q, k, v, idx, kv_lens
 
 
-def _run(entry, q, k, v, idx, kv_lens, scale):
+def _run(entry, q, k, v, idx, kv_lens, scale, idx_sorted=False):
     """One call of sfa_fwd (caller workspace) or sfa_fwd_noalloc through the
     C ABI on torch's current stream; returns (out, lse, workspace bytes)."""
     lib = _lib.load()
     B, Sq, Hq, _ = q.shape
     out = torch.empty(B, Sq, Hq, v.shape[3], dtype=q.dtype, device=DEV)
     lse = torch.empty(B, Sq, Hq, dtype=torch.float32, device=DEV)
-    a = sfa_mod._fwd_args(q, k, v, idx, out, lse, scale, kv_lens, None, 0)
+    a = sfa_mod._fwd_args(q, k, v, idx, out, lse, scale, kv_lens, None, 0, idx_sorted)
     ws = lib.sfa_fwd_workspace_size(ctypes.byref(a))
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     if entry == "noalloc":
@@ -119,3 +119,29 @@ def test_noalloc_persistent_prefill_after_decode():
         err_l = float((l_na[:, rows].cpu() - l_ref).abs().max())
         assert err_o <= 2e-2 and err_l <= 1e-3, (S, err_o, err_l)
     assert sizes[0] > 0 and sizes[1] == 0
+
+
+def test_noalloc_prefill_rows_beyond_the_scratch_walk_their_own_order():
+    """MLA prefill at S = 8192, top-k 2048: its index rows in ascending order
+    (64 MiB) and the claim counters do not fit the static scratch together,
+    so sfa_fwd_noalloc skips the sort pass and walks the caller's rows in
+    their own order: bitwise sfa_fwd with SFA_FWD_IDX_SORTED set (no pass),
+    sampled rows within the oracle's bars."""
+    S, K = 8192, 2048
+    _say(f"sfa_fwd_noalloc vs sfa_fwd (rows declared sorted): mla prefill S={S} K={K} Hq=128")
+    w = make_workload("mla_prefill", device=DEV, S=S, K=K)
+    lib = _lib.load()
+    out = torch.empty(1, S, 128, 512, dtype=w.q.dtype, device=DEV)
+    lse = torch.empty(1, S, 128, dtype=torch.float32, device=DEV)
+    a = sfa_mod._fwd_args(w.q, w.k, w.v, w.idx, out, lse, w.scale, None, None, 0)
+    assert lib.sfa_fwd_workspace_size(ctypes.byref(a)) > _lib.SFA_NOALLOC_SCRATCH_BYTES
+    o_na, l_na, _ = _run("noalloc", w.q, w.k, w.v, w.idx, None, w.scale)
+    o_ws, l_ws, ws = _run("workspace", w.q, w.k, w.v, w.idx, None, w.scale, idx_sorted=True)
+    assert 0 < ws <= _lib.SFA_NOALLOC_SCRATCH_BYTES
+    assert torch.equal(o_na, o_ws) and torch.equal(l_na, l_ws)
+    rows = torch.tensor([0, 1, 2047, 2048, S // 2, S - 1])
+    o_ref, l_ref = ref_forward(w.q[:, rows].float().cpu(), w.k.float().cpu(), w.v.float().cpu(),
+                               w.idx[:, rows].cpu(), w.scale)
+    err_o = float((o_na[:, rows].float().cpu() - o_ref).abs().max())
+    err_l = float((l_na[:, rows].cpu() - l_ref).abs().max())
+    assert err_o <= 2e-2 and err_l <= 1e-3, (err_o, err_l)
