@@ -9,8 +9,8 @@ on the host-sorted rows with SFA_FWD_IDX_SORTED set (no pass): both run the
 same kernel on the same slots, so any slot the pass dropped, repeated,
 misplaced or let through out of range changes some row of the output.  The
 rows include repeated keys, keys at and beyond kv_lens, padding values other
-than -1, rows with no valid key, short causal rows, and 16-bit-range keys
-beyond the first bitmap half (Skv > 32768).  Sampled rows are also checked
+than -1, rows with no valid key, short causal rows, keys beyond the first
+bitmap half (Skv > 32768) up to Skv = 65536, and a top-k of 100.  Sampled rows are also checked
 against the CPU oracle (O max-abs 2e-2, LSE 1e-3)."""
 import math
 import sys
@@ -96,6 +96,7 @@ def _plant(idx, bounds, seed):
 @pytest.mark.parametrize("B,S,Skv,K,lens", [
     (2, 2080, 2080, 256, (2080, 1500)),   # 4160 items: persistent, kv_lens, causal short rows
     (1, 4100, 40000, 512, None),          # Skv > 32768: the 2048-word bitmap
+    (1, 4096, 65536, 100, None),          # the bitmap's last word, top-k not a multiple of the slots per thread
 ])
 def test_sorted_pass_is_bitwise_the_host_sorted_forward(B, S, Skv, K, lens):
     _say(f"index sort: B={B} S={S} Skv={Skv} K={K} kv_lens={lens}")
