@@ -246,10 +246,10 @@ SFA_API int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t 
  * chunk of queries: per query the bf16 P / dS of its slots (about 1 MiB at
  * top-k 2048, G = 128) and, in the deterministic mode, its per-slot bf16
  * gradient rows (top-k * Dqk * 2 bytes) and index maps; a chunk stays within
- * 3 GiB in the deterministic mode and 2 GiB with atomics (whole rounds of 256
- * queries when that many fit, at most 1024 in the deterministic mode, else
- * multiples of 8, at least 8 queries), so the total is about 3 GiB (2 GiB)
- * plus the accumulators at the full-size shapes.
+ * 3.5 GiB in the deterministic mode and 2 GiB with atomics (whole rounds of
+ * 256 queries when that many fit, at most 1024 in the deterministic mode,
+ * else multiples of 8, at least 8 queries), so the total is about 3.5 GiB
+ * (2 GiB) plus the accumulators at the full-size shapes.
  * Replaces the workspaces of SFA.py:184-194 and SFA.py:253-261. */
 SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
 

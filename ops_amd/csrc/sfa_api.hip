@@ -406,14 +406,14 @@ bool mla_det(const sfa_bwd_args* a, const sfa::Params& p) {
 }
 
 // Its workspace holds one chunk of work items (P / dS, and the contribution
-// rows and index maps when deterministic): up to about 3 GiB deterministic
-// (1024 queries at top-k 2048: each chunk costs a fixed ~40 us of launches
-// and reduction set-up, so 32 chunks of 1024 run 1.7 % faster than 64 of
-// 512 at S = 32768) or 2 GiB with atomics (larger chunks gain nothing
-// there), in whole rounds of 256 items (one dK/dV workgroup per CU of the
+// rows and index maps when deterministic): up to about 3.5 GiB deterministic
+// (1024 queries at top-k 2048, 3.4 MB each: every chunk costs a fixed
+// ~40 us of launches and reduction set-up, so 32 chunks of 1024 run 2.7 %
+// faster than 64 of 512 at S = 32768) or 2 GiB with atomics (larger chunks
+// gain nothing there), in whole rounds of 256 items (one dK/dV workgroup per CU of the
 // 256-CU part; a partial last round would leave most CUs idle), at least 8
 // items so the dQ pass can place both head groups of an item on one XCD.
-constexpr size_t kMlaChunkBytesDet = size_t(3) << 30;
+constexpr size_t kMlaChunkBytesDet = size_t(3584) << 20;
 constexpr size_t kMlaChunkBytes = size_t(2) << 30;
 constexpr int64_t kMlaChunkRound = 256;
 

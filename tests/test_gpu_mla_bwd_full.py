@@ -112,8 +112,8 @@ def test_mla_bwd_full_workload(full_mla, mode):
 
 @pytest.mark.parametrize("mode", ["auto", "atomic"])
 def test_mla_bwd_skv8192_masking_sink_dlse(mode):
-    """Skv = 8192 (256 bitmap words per query, 8 chunks per sequence in the
-    deterministic mode) with interior and trailing padding, ids past Skv and
+    """Skv = 8192 (256 bitmap words per query, 16 chunks of 1024 queries over
+    both sequences in the deterministic mode) with interior and trailing padding, ids past Skv and
     past kv_lens, a fully masked row, a sink and a gradient on LSE."""
     _say(f"MLA bwd B=2 S=8192 Hq=128 K=2048 sink/dlse/kv_lens/masked row, dkv_mode={mode}")
     w = make_workload("mla_prefill", device=DEV, seed=2, B=2, S=8192, with_dout=True)
