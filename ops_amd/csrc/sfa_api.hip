@@ -481,13 +481,14 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
     const bool det = mla_det(a, p);
     if (a->dkv_mode == SFA_DKV_CSR && !det)
       return fail(SFA_E_UNSUPPORTED, "the deterministic MLA backward supports Skv <= 65536 (got %d)", f.Skv);
+    // (δ is computed by the chunks' dQ passes, which load O and dO rows anyway;
+    // the sink's gradient, which needs every row's δ, follows the last chunk)
     hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
-    if (e == hipSuccess) e = sfa::launch_bwd_delta(p, f.dtype, s);
-    if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
     const int64_t items = (int64_t)f.B * f.Sq * f.Hkv;
     const int chunk = mla_chunk_items(p, det);
     for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk)
       e = sfa::launch_bwd_mla_chunk(p, i0, (int)(items - i0 < chunk ? items - i0 : chunk), pd, det, s);
+    if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
     if (e == hipSuccess) e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, false, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_bwd (mla)");
     return SFA_OK;

@@ -139,11 +139,11 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
   const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
   const bool live = hvalid && lse != kNegInf;  // rows with no valid slot contribute nothing
   const float lse2 = live ? lse * kLog2e : 0.f;
-  const float delta = live ? p.delta[row] : 0.f;
 
   // B operands over the head dims: lane holds head h, dims 32 s + 8 hq .. +7
   // (AGPRs: the VGPR file holds the dQ^T accumulators)
   bf16x8 qb[kMQS], dob[kMVS];
+  float delta_h;  // δ of the lane's row: Σ O·dO over its head dims, less the LSE gradient
   {
     const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh + 8 * hq;
     const bf16* dorow =
@@ -158,13 +158,33 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
       for (int s = 0; s < kMQS; ++s) qb[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});  // B operands read from AGPRs
     }
     {
-      bf16x8 x[kMVS];
+      // δ = Σ O·dO over the row (SFA.py:590-610's _get_delta_split) from the
+      // dO values loaded here anyway and the same lane's pieces of the O row:
+      // 128 dims per lane, then the 4 lanes of a head (lane groups hq)
+      const bf16* orow = reinterpret_cast<const bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh + 8 * hq;
+      bf16x8 x[kMVS], o[kMVS];
 #pragma unroll
-      for (int s = 0; s < kMVS; ++s) x[s] = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
+      for (int s = 0; s < kMVS; ++s) {
+        x[s] = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
+        o[s] = *reinterpret_cast<const bf16x8*>(orow + 32 * s);
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int s = 0; s < kMVS; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = fmaf((float)o[s][j], (float)x[s][j], acc);
+      acc += __shfl_xor(acc, 16, 64);
+      acc += __shfl_xor(acc, 32, 64);
+      if (p.dlse) acc -= p.dlse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+      delta_h = acc;
 #pragma unroll
       for (int s = 0; s < kMVS; ++s) dob[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});
     }
   }
+  // (δ of every row goes to the workspace for the sink's gradient, reduced
+  // after the last chunk)
+  if (hvalid && hq == 0) p.delta[row] = delta_h;
+  const float delta = live ? delta_h : 0.f;
   istage.store<false>(p, b, bound, nslots, ntiles * kMT, s_idx, tid);
 
   // Per-lane LDS byte offsets.  S^T / dP^T A operand of M-tile mt, step s:
