@@ -117,13 +117,41 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
   }
   const int32_t* irow = p.idx + b * p.i_sb + t * p.i_ss + g * p.i_sh;
   const int bound = bound_of(p, b);
+
+  // this lane's head
+  const int hl = hg * kMHG + wave * 16 + lt;  // head within the group
+  const bool hvalid = hl < p.G;
+  const int h = g * p.G + (hvalid ? hl : 0);
+  const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
+
+  // Every load of the prologue goes out before the first wait, oldest first
+  // in the order they are needed (loads complete in order, so each wait below
+  // covers only what was issued before it): the index row and tile 0's row
+  // ids, the row's lse (and LSE gradient), then the Q, dO and O rows of the
+  // lane's head (dims 32 s + 8 hq .. +7).  Waiting on each group before
+  // issuing the next made the prologue a chain of round trips.
   IdxStage<kMIdxCap, kMThreads> istage;
   istage.load(irow, nslots, tid);
+  int raw[MRG::RPW];
+#pragma unroll
+  for (int r = 0; r < MRG::RPW; ++r) raw[r] = irow[min(wave * MRG::RPW + r, nslots - 1)];
+  const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+  const float dlse = p.dlse ? p.dlse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh] : 0.f;
+  const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh + 8 * hq;
+  const bf16* dorow = reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh + 8 * hq;
+  const bf16* orow = reinterpret_cast<const bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh + 8 * hq;
+  bf16x8 xq[kMQS], xd[kMVS], xo[kMVS];
+#pragma unroll
+  for (int s = 0; s < kMQS; ++s) xq[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+#pragma unroll
+  for (int s = 0; s < kMVS; ++s) {
+    xd[s] = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
+    xo[s] = *reinterpret_cast<const bf16x8*>(orow + 32 * s);
+  }
+
+  // tile 0's gather, from the ids
   {
     MRG rg0;
-    int raw[MRG::RPW];
-#pragma unroll
-    for (int r = 0; r < MRG::RPW; ++r) raw[r] = irow[min(wave * MRG::RPW + r, nslots - 1)];
 #pragma unroll
     for (int r = 0; r < MRG::RPW; ++r)
       rg0.set_row(r, (wave * MRG::RPW + r < nslots) ? staged_id<false>(p, b, raw[r], bound) : -1, true, ksrc);
@@ -131,56 +159,30 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
     for (int k = 0; k < MRG::NI; ++k) rg0.issue(k, ksrc, s_k0, wave, lane);
   }
 
-  // this lane's head and its softmax statistics
-  const int hl = hg * kMHG + wave * 16 + lt;  // head within the group
-  const bool hvalid = hl < p.G;
-  const int h = g * p.G + (hvalid ? hl : 0);
-  const int64_t row = ((int64_t)b * p.Sq + t) * p.Hq + h;
-  const float lse = p.lse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
+  // the row's softmax statistics
   const bool live = hvalid && lse != kNegInf;  // rows with no valid slot contribute nothing
   const float lse2 = live ? lse * kLog2e : 0.f;
 
-  // B operands over the head dims: lane holds head h, dims 32 s + 8 hq .. +7
-  // (AGPRs: the VGPR file holds the dQ^T accumulators)
+  // B operands over the head dims (AGPRs: the VGPR file holds the dQ^T
+  // accumulators), and δ = Σ O·dO over the row (SFA.py:590-610's
+  // _get_delta_split) from the dO values and the same lane's pieces of the O
+  // row: 128 dims per lane, then the 4 lanes of a head (lane groups hq)
   bf16x8 qb[kMQS], dob[kMVS];
-  float delta_h;  // δ of the lane's row: Σ O·dO over its head dims, less the LSE gradient
+#pragma unroll
+  for (int s = 0; s < kMQS; ++s) qb[s] = Mfma16A::to_agpr(hvalid ? xq[s] : bf16x8{});  // B operands read from AGPRs
+  float delta_h;  // δ of the lane's row, less the LSE gradient
   {
-    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + b * p.q_sb + t * p.q_ss + (int64_t)h * p.q_sh + 8 * hq;
-    const bf16* dorow =
-        reinterpret_cast<const bf16*>(p.dout) + b * p.do_sb + t * p.do_ss + (int64_t)h * p.do_sh + 8 * hq;
-    // all loads of a row first, then the moves into AGPRs (moving each value
-    // as it arrives made every load wait for the previous one)
-    {
-      bf16x8 x[kMQS];
+    float acc = 0.f;
 #pragma unroll
-      for (int s = 0; s < kMQS; ++s) x[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+    for (int s = 0; s < kMVS; ++s)
 #pragma unroll
-      for (int s = 0; s < kMQS; ++s) qb[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});  // B operands read from AGPRs
-    }
-    {
-      // δ = Σ O·dO over the row (SFA.py:590-610's _get_delta_split) from the
-      // dO values loaded here anyway and the same lane's pieces of the O row:
-      // 128 dims per lane, then the 4 lanes of a head (lane groups hq)
-      const bf16* orow = reinterpret_cast<const bf16*>(p.out) + b * p.o_sb + t * p.o_ss + (int64_t)h * p.o_sh + 8 * hq;
-      bf16x8 x[kMVS], o[kMVS];
-#pragma unroll
-      for (int s = 0; s < kMVS; ++s) {
-        x[s] = *reinterpret_cast<const bf16x8*>(dorow + 32 * s);
-        o[s] = *reinterpret_cast<const bf16x8*>(orow + 32 * s);
-      }
-      float acc = 0.f;
-#pragma unroll
-      for (int s = 0; s < kMVS; ++s)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf((float)o[s][j], (float)x[s][j], acc);
-      acc += __shfl_xor(acc, 16, 64);
-      acc += __shfl_xor(acc, 32, 64);
-      if (p.dlse) acc -= p.dlse[b * p.l_sb + t * p.l_ss + (int64_t)h * p.l_sh];
-      delta_h = acc;
-#pragma unroll
-      for (int s = 0; s < kMVS; ++s) dob[s] = Mfma16A::to_agpr(hvalid ? x[s] : bf16x8{});
-    }
+      for (int j = 0; j < 8; ++j) acc = fmaf((float)xo[s][j], (float)xd[s][j], acc);
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    delta_h = acc - dlse;
   }
+#pragma unroll
+  for (int s = 0; s < kMVS; ++s) dob[s] = Mfma16A::to_agpr(hvalid ? xd[s] : bf16x8{});
   // (δ of every row goes to the workspace for the sink's gradient, reduced
   // after the last chunk)
   if (hvalid && hq == 0) p.delta[row] = delta_h;
