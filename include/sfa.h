@@ -248,15 +248,24 @@ SFA_API int sfa_indexer_topk(const sfa_indexer_args* a, void* workspace, size_t 
  * gradient rows (top-k * Dqk * 2 bytes) and index maps; a chunk stays within
  * 3.5 GiB in the deterministic mode and 2 GiB with atomics (whole rounds of
  * 256 queries when that many fit, at most 1024 in the deterministic mode,
- * else multiples of 8, at least 8 queries), so the total is about 3.5 GiB
- * (2 GiB) plus the accumulators at the full-size shapes.
+ * else multiples of 8, at least 8 queries).  The deterministic mode holds
+ * the gradient rows and index maps twice (one chunk's reduction reads one
+ * set while the next chunk fills the other), so the total is about 5.5 GiB
+ * (2 GiB with atomics) plus the accumulators at the full-size shapes.
  * Replaces the workspaces of SFA.py:184-194 and SFA.py:253-261. */
 SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
 
 /* Backward: dq, dk, dv (and dsink if requested) from dout, out and lse.
  * Replaces `_attn_bwd_dq_dsink` (SFA.py:856-1002 via SFA.py:199-251) and
  * `_attn_bwd_dk_dv` (SFA.py:1005-1145 via SFA.py:266-298).  dq/dk/dv are
- * fully overwritten (no accumulation into existing contents). */
+ * fully overwritten (no accumulation into existing contents).  The
+ * deterministic MLA backward also enqueues its ordered reductions on a
+ * second stream of the current device, which the library creates on its
+ * first such call (default priority, non-blocking, kept until the process
+ * ends) and orders against `stream` with events: when the call returns,
+ * `stream` waits for all of that work, and under HIP-graph capture the
+ * second stream joins the capture and is joined back.  Such calls on one
+ * device enqueue one at a time (a mutex). */
 SFA_API int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

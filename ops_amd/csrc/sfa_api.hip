@@ -1,6 +1,8 @@
 // C ABI of libsfa.so (declared in include/sfa.h): argument validation,
-// workspace sizing and kernel dispatch.  The library never allocates, frees
-// or synchronises; all work goes onto the caller's stream.
+// workspace sizing and kernel dispatch.  The library never allocates device
+// memory, frees or synchronises; all work goes onto the caller's stream,
+// except the deterministic MLA backward's reductions, which run on a second
+// stream of the device ordered against it by events (MlaSide below).
 
 #include <math.h>
 #include <stdint.h>
@@ -406,11 +408,11 @@ bool mla_det(const sfa_bwd_args* a, const sfa::Params& p) {
 }
 
 // Its workspace holds one chunk of work items (P / dS, and the contribution
-// rows and index maps when deterministic): up to about 3.5 GiB deterministic
-// (1024 queries at top-k 2048, 3.4 MB each: every chunk costs a fixed
-// ~40 us of launches and reduction set-up, so 32 chunks of 1024 run 2.7 %
-// faster than 64 of 512 at S = 32768) or 2 GiB with atomics (larger chunks
-// gain nothing there), in whole rounds of 256 items (one dK/dV workgroup per CU of the
+// rows and index maps when deterministic, those twice): a chunk is sized to
+// about 3.5 GiB deterministic (1024 queries at top-k 2048, 3.4 MB each:
+// every chunk costs a fixed ~40 us of launches and reduction set-up, so 32
+// chunks of 1024 run 2.7 % faster than 64 of 512 at S = 32768) or 2 GiB with
+// atomics (larger chunks gain nothing there), in whole rounds of 256 items (one dK/dV workgroup per CU of the
 // 256-CU part; a partial last round would leave most CUs idle), at least 8
 // items so the dQ pass can place both head groups of an item on one XCD.
 constexpr size_t kMlaChunkBytesDet = size_t(3584) << 20;
@@ -426,11 +428,45 @@ int mla_chunk_items(const sfa::Params& p, bool det) {
   return (int)(n < items ? n : items);
 }
 
-// MLA workspace: fp32 shared-row accumulators | delta | chunk
+// MLA workspace: fp32 shared-row accumulators | delta | P / dS of a chunk |
+// (det) two buffer sets, so that chunk c + 1's dK/dV pass can fill one while
+// chunk c's reduction reads the other
 size_t mla_bytes(const sfa_fwd_args& f, const sfa::Params& p, bool det) {
   const size_t dk = align_up((size_t)f.B * f.Skv * f.Hkv * f.Dqk * sizeof(float), 256);
   const size_t delta = align_up((size_t)f.B * f.Sq * f.Hq * sizeof(float), 256);
-  return dk + delta + align_up((size_t)mla_chunk_items(p, det) * sfa::bwd_mla_bytes_per_item(p, det), 256);
+  const size_t n = (size_t)mla_chunk_items(p, det);
+  size_t bytes = dk + delta + align_up(n * sfa::bwd_mla_pd_bytes_per_item(p), 256);
+  if (det) bytes += 2 * align_up(n * sfa::bwd_mla_set_bytes_per_item(p), 256);
+  return bytes;
+}
+
+// The deterministic MLA backward's reductions run on a second stream of the
+// device (default priority, non-blocking), ordered against the caller's
+// stream by events, so that chunk c's reduction (HBM-bound) overlaps chunk
+// c + 1's dQ pass (MFMA- and LDS-bound).  One per device, created on first
+// use and kept until the process ends; calls on one device enqueue under its
+// mutex, so each call's fork and join of the side stream stay together
+// (also under HIP-graph capture: the side stream joins the caller's capture
+// through the first event and is joined back before the call returns).
+struct MlaSide {
+  std::mutex mu;
+  bool ready = false;
+  hipStream_t st = nullptr;
+  hipEvent_t dkv_done = nullptr;
+  hipEvent_t red_done[2] = {nullptr, nullptr};
+  int cus = 0;
+};
+MlaSide g_side[kMaxDevices];
+
+hipError_t mla_side_init(MlaSide& m, int dev) {
+  if (m.ready) return hipSuccess;
+  hipError_t e = hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess && m.st == nullptr) e = hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking);
+  if (e == hipSuccess && m.dkv_done == nullptr) e = hipEventCreateWithFlags(&m.dkv_done, hipEventDisableTiming);
+  for (int i = 0; i < 2 && e == hipSuccess; ++i)
+    if (m.red_done[i] == nullptr) e = hipEventCreateWithFlags(&m.red_done[i], hipEventDisableTiming);
+  if (e == hipSuccess) m.ready = true;
+  return e;
 }
 
 }  // namespace
@@ -483,11 +519,44 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
       return fail(SFA_E_UNSUPPORTED, "the deterministic MLA backward supports Skv <= 65536 (got %d)", f.Skv);
     // (δ is computed by the chunks' dQ passes, which load O and dO rows anyway;
     // the sink's gradient, which needs every row's δ, follows the last chunk)
-    hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
     const int64_t items = (int64_t)f.B * f.Sq * f.Hkv;
     const int chunk = mla_chunk_items(p, det);
-    for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk)
-      e = sfa::launch_bwd_mla_chunk(p, i0, (int)(items - i0 < chunk ? items - i0 : chunk), pd, det, s);
+    void* sets[2] = {nullptr, nullptr};
+    MlaSide* side = nullptr;
+    std::unique_lock<std::mutex> lock;
+    if (det) {
+      int dev = 0;
+      hipError_t e0 = hipGetDevice(&dev);
+      if (e0 == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e0 = hipErrorInvalidDevice;
+      if (e0 == hipSuccess) {
+        side = &g_side[dev];
+        lock = std::unique_lock<std::mutex>(side->mu);
+        e0 = mla_side_init(*side, dev);
+      }
+      if (e0 != hipSuccess) return hip_fail(e0, "sfa_bwd (mla): the reduction stream");
+      const size_t set_bytes = align_up((size_t)chunk * sfa::bwd_mla_set_bytes_per_item(p), 256);
+      sets[0] = (char*)pd + align_up((size_t)chunk * sfa::bwd_mla_pd_bytes_per_item(p), 256);
+      sets[1] = (char*)sets[0] + set_bytes;
+    }
+    hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
+    int c = 0;
+    for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk, ++c) {
+      const int n = (int)(items - i0 < chunk ? items - i0 : chunk);
+      // (det: chunk c - 2's reduction read this buffer set)
+      if (det && c >= 2) e = hipStreamWaitEvent(s, side->red_done[c & 1], 0);
+      if (e == hipSuccess) e = sfa::launch_bwd_mla_chunk(p, i0, n, pd, sets[c & 1], det, s);
+      if (det && e == hipSuccess) {
+        e = hipEventRecord(side->dkv_done, s);
+        if (e == hipSuccess) e = hipStreamWaitEvent(side->st, side->dkv_done, 0);
+        if (e == hipSuccess) e = sfa::launch_bwd_mla_reduce(p, i0, n, sets[c & 1], side->cus, side->st);
+        if (e == hipSuccess) e = hipEventRecord(side->red_done[c & 1], side->st);
+      }
+    }
+    // join: the last reduction (the side stream runs them in order)
+    if (det && c > 0) {
+      const hipError_t ej = hipStreamWaitEvent(s, side->red_done[(c - 1) & 1], 0);
+      if (e == hipSuccess) e = ej;
+    }
     if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);
     if (e == hipSuccess) e = sfa::launch_bwd_finish_merged(p, f.dtype, a->dk, a->dk_sb, a->dk_ss, a->dk_sh, false, s);
     if (e != hipSuccess) return hip_fail(e, "sfa_bwd (mla)");

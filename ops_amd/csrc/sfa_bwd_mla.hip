@@ -290,8 +290,9 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dq_kernel(Params p, int6
       }
     {
       bf16* blk = pd_item + ((int64_t)((tile * 2 + 0) * nhg + hg) * 4 + wave) * pd_block_elems();
-      *reinterpret_cast<bf16x8*>(blk + 8 * ppos) = pb;
-      *reinterpret_cast<bf16x8*>(blk + (int64_t)nhg * 4 * pd_block_elems() + 8 * ppos) = dse;
+      // (non-temporal: the dK/dV pass reads each block once)
+      __builtin_nontemporal_store(pb, reinterpret_cast<bf16x8*>(blk + 8 * ppos));
+      __builtin_nontemporal_store(dse, reinterpret_cast<bf16x8*>(blk + (int64_t)nhg * 4 * pd_block_elems() + 8 * ppos));
     }
     // dQ^T += K^T dS^T
     constexpr int PD = 3;
@@ -564,12 +565,15 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   // current tile's operand reads from the next tile's DMA target, and for the
   // builtin form it waited for the DMA (and the previous tile's row stores)
   // before the first MFMA of every tile.  The loop waits for vmcnt(0) itself
-  // before the barrier that publishes a tile.
+  // before the barrier that publishes a tile.  (nt: each block is read once;
+  // with the other single-use streams of the backward marked non-temporal,
+  // the whole backward runs about 3 % faster: fewer of the dQ pass's gathered
+  // rows are evicted from the caches.)
   auto load_tile = [&](int tile, u32x4* dst) {
     for (int i = wave * 64; i < tile_slots; i += kMThreads) {
       const char* src = pd_item + ((int64_t)tile * tile_slots + i + lane) * 16;
       const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)(dst + i);
-      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds), "v"(src) : "memory", "m0");
     }
   };
   auto dma_done = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
@@ -694,14 +698,15 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
       }
       dma_next_done();
       __syncthreads();  // output rows staged; the next tile's P / dS landed
-      // rows to their rank in the item's contribution block (72 slots a row)
+      // rows to their rank in the item's contribution block (72 slots a row;
+      // non-temporal: the reduction reads each row once)
 #pragma unroll
       for (int k = 0; k < 9; ++k) {
         const int u = tid + k * kMThreads;
         const int key = u / kMCH, c = u - key * kMCH;
         const int rk = s_rank[j * kMT + key];
         const uint32_t off = rk >= 0 ? (uint32_t)rk * 1152u + 16u * (uint32_t)c : kOOB;
-        __builtin_amdgcn_raw_buffer_store_b128(orow[key * kCP + c], rcon, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(orow[key * kCP + c], rcon, off, 0, kCpolNT);
       }
     } else {
 #pragma unroll
@@ -720,113 +725,123 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
   }
 }
 
-// Deterministic reduction of a chunk's contributions: a workgroup of 16
-// waves owns 16 keys, half of one membership-bitmap word (b, g, word); it
-// stages that word and its prefix count for each of the chunk's items of
-// (b, g) in LDS (one scattered read per item for all 16 keys, instead of one
-// per item and key), then each wave sums the rows of its key in item order
-// into the fp32 accumulator row (each row owned by one wave; chunks run in
-// order).  Lane l holds dims 8 l .. 8 l + 7, lanes 0..7 also dims 512 + 8 l
-// ..; a chunk holds at most kRedItems items (host-side cap).
+// Deterministic reduction of a chunk's contributions.  A group is 16 keys,
+// half of one membership-bitmap word (b, g, word): its workgroup stages that
+// word and its prefix count for each of the chunk's items of (b, g) in LDS
+// (one scattered read per item for all 16 keys, instead of one per item and
+// key), then each of its 4 waves sums the rows of 4 of the keys, one key at
+// a time, in item order into the fp32 accumulator row (each row owned by one
+// wave; chunks run in order).  Lane l holds dims 8 l .. 8 l + 7, lanes 0..7
+// also dims 512 + 8 l ..; a chunk holds at most kRedItems items (host-side
+// cap).
+// The kernel runs on a second stream beside the next chunk's dQ pass, so it
+// is persistent (one workgroup per CU, groups strided over the grid) and
+// small: its 120 registers per lane next to the dQ pass's 392 (256 + 136
+// accumulation registers) fill the 512 of a SIMD lane, and its 6.4 KB of LDS
+// fit beside the dQ pass's 80 KB.
 constexpr int kRedItems = 1024;
-constexpr int kRedThreads = 1024;
-__global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(Params p, int64_t item0, int nitems, int b0,
-                                                                     int nb, const bf16* contrib,
-                                                                     const uint32_t* kmap, const uint16_t* prefix,
-                                                                     int W) {
+constexpr int kRedThreads = 256;
+constexpr int kRedWaves = kRedThreads / 64;
+__global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(
+    Params p, int64_t item0, int nitems, int b0, int64_t groups, const bf16* contrib, const uint32_t* kmap,
+    const uint16_t* prefix, int W) {
   __shared__ uint32_t s_word[kRedItems];
   __shared__ uint16_t s_pre[kRedItems];
-  __shared__ int2 s_hits[kRedThreads / 64][8];  // per wave: queued hits (item, rank)
+  __shared__ int2 s_hits[kRedWaves][8];  // per wave: queued hits (item, rank)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nw = (p.Skv + 31) / 32;
-  const int wsel = (int)((blockIdx.x >> 1) % nw);
-  const int half = (int)(blockIdx.x & 1);
-  const int64_t r = (blockIdx.x >> 1) / nw;
-  const int g = (int)(r % p.Hkv);
-  const int b = b0 + (int)(r / p.Hkv);
-  if (r >= (int64_t)nb * p.Hkv) return;  // the whole workgroup
-  // this (b, g)'s items of the chunk: item = (b Sq + t) Hkv + g, stride Hkv
-  const int64_t first = ((int64_t)b * p.Sq) * p.Hkv + g;
-  const int64_t lo = first < item0 ? item0 + ((g - item0 % p.Hkv) + p.Hkv) % p.Hkv : first;
-  const int64_t hi_b = ((int64_t)(b + 1) * p.Sq) * p.Hkv;
-  const int64_t hi = hi_b < item0 + nitems ? hi_b : item0 + nitems;
-  const int nit = lo < hi ? (int)((hi - lo + p.Hkv - 1) / p.Hkv) : 0;  // <= kRedItems
-  const int li0 = (int)(lo - item0);
-  for (int i = tid; i < nit; i += kRedThreads) {
-    const int li = li0 + i * p.Hkv;
-    s_word[i] = kmap[(int64_t)li * W + wsel];
-    s_pre[i] = prefix[(int64_t)li * W + wsel];
-  }
-  __syncthreads();
-  const int bound = bound_of(p, b);
-  {
-    const int kbit = 16 * half + wave;
-    const int key = 32 * wsel + kbit;
-    if (key >= p.Skv) return;  // the whole wave
-    const uint32_t bit = 1u << kbit;
-    float a0[8] = {}, a1[8] = {};
-    bool any = false;
-    // Items in batches of 64 (one per lane).  A key has only a few hits per
-    // batch, so the hits are queued across batches (item and rank, in item
-    // order, in the wave's LDS list) and their rows are loaded U at a time,
-    // then added in item order: full rounds of loads in flight instead of
-    // one short round per batch.
-    constexpr int U = 8;
-    int2* q = s_hits[wave];
-    int nq = 0;  // queued hits (wave-uniform)
-    auto flush = [&](int n) {
-      u32x4 v0[U], v1[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (u < n) {
-          const int2 h = q[u];
-          const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
-          v0[u] = row[lane];
-          v1[u] = lane < 8 ? row[64 + lane] : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (u >= n) continue;
-        const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
-        const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          a0[e] += (float)x0[e];
-          a1[e] += (float)x1[e];
-        }
-      }
-      any = true;
-    };
-    for (int ib = 0; ib < nit; ib += 64) {
-      const int i = ib + lane;
-      const uint32_t word = i < nit ? s_word[i] : 0u;
-      const int rank = i < nit ? (int)s_pre[i] + __builtin_popcount(word & (bit - 1u)) : 0;
-      uint64_t hits = __ballot((word & bit) != 0u);
-      while (hits) {
-        // queue up to U - nq of this batch's hits (lane order = item order)
-        const int take = min(__popcll(hits), U - nq);
-        const uint64_t below = ((1ull << lane) - 1ull);
-        const bool mine = ((hits >> lane) & 1ull) && __popcll(hits & below) < take;
-        if (mine) q[nq + __popcll(hits & below)] = int2{li0 + i * p.Hkv, rank};
-        for (int t = 0; t < take; ++t) hits &= hits - 1;
-        nq += take;
-        __builtin_amdgcn_wave_barrier();
-        if (nq == U) {
-          flush(U);
-          nq = 0;
-          __builtin_amdgcn_wave_barrier();
-        }
-      }
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int wsel = (int)((gi >> 1) % nw);
+    const int half = (int)(gi & 1);
+    const int64_t r = (gi >> 1) / nw;
+    const int g = (int)(r % p.Hkv);
+    const int b = b0 + (int)(r / p.Hkv);
+    // this (b, g)'s items of the chunk: item = (b Sq + t) Hkv + g, stride Hkv
+    const int64_t first = ((int64_t)b * p.Sq) * p.Hkv + g;
+    const int64_t lo = first < item0 ? item0 + ((g - item0 % p.Hkv) + p.Hkv) % p.Hkv : first;
+    const int64_t hi_b = ((int64_t)(b + 1) * p.Sq) * p.Hkv;
+    const int64_t hi = hi_b < item0 + nitems ? hi_b : item0 + nitems;
+    const int nit = lo < hi ? (int)((hi - lo + p.Hkv - 1) / p.Hkv) : 0;  // <= kRedItems
+    const int li0 = (int)(lo - item0);
+    __syncthreads();  // the previous group's reads of the staged words are done
+    for (int i = tid; i < nit; i += kRedThreads) {
+      const int li = li0 + i * p.Hkv;
+      s_word[i] = kmap[(int64_t)li * W + wsel];
+      s_pre[i] = prefix[(int64_t)li * W + wsel];
     }
-    if (nq > 0) flush(nq);
-    if (!any || key >= bound) return;
-    float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
+    __syncthreads();
+    const int bound = bound_of(p, b);
+    for (int kk = 0; kk < 16 / kRedWaves; ++kk) {
+      const int kbit = 16 * half + kRedWaves * kk + wave;
+      const int key = 32 * wsel + kbit;
+      if (key >= p.Skv) continue;  // the whole wave
+      const uint32_t bit = 1u << kbit;
+      float a0[8] = {}, a1[8] = {};
+      bool any = false;
+      // Items in batches of 64 (one per lane).  A key has only a few hits per
+      // batch, so the hits are queued across batches (item and rank, in item
+      // order, in the wave's LDS list) and their rows are loaded U at a time,
+      // then added in item order: full rounds of loads in flight instead of
+      // one short round per batch.
+      constexpr int U = 8;
+      int2* q = s_hits[wave];
+      int nq = 0;  // queued hits (wave-uniform)
+      auto flush = [&](int n) {
+        u32x4 v0[U], v1[U];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
-    if (lane < 8) {
+        for (int u = 0; u < U; ++u) {
+          if (u < n) {
+            const int2 h = q[u];
+            const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
+            // (non-temporal: each row is read once, beside the dQ pass's gathers)
+            v0[u] = __builtin_nontemporal_load(row + lane);
+            v1[u] = lane < 8 ? __builtin_nontemporal_load(row + 64 + lane) : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
+        for (int u = 0; u < U; ++u) {
+          if (u >= n) continue;
+          const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
+          const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            a0[e] += (float)x0[e];
+            a1[e] += (float)x1[e];
+          }
+        }
+        any = true;
+      };
+      for (int ib = 0; ib < nit; ib += 64) {
+        const int i = ib + lane;
+        const uint32_t word = i < nit ? s_word[i] : 0u;
+        const int rank = i < nit ? (int)s_pre[i] + __builtin_popcount(word & (bit - 1u)) : 0;
+        uint64_t hits = __ballot((word & bit) != 0u);
+        while (hits) {
+          // queue up to U - nq of this batch's hits (lane order = item order)
+          const int take = min(__popcll(hits), U - nq);
+          const uint64_t below = ((1ull << lane) - 1ull);
+          const bool mine = ((hits >> lane) & 1ull) && __popcll(hits & below) < take;
+          if (mine) q[nq + __popcll(hits & below)] = int2{li0 + i * p.Hkv, rank};
+          for (int t = 0; t < take; ++t) hits &= hits - 1;
+          nq += take;
+          __builtin_amdgcn_wave_barrier();
+          if (nq == U) {
+            flush(U);
+            nq = 0;
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+      }
+      if (nq > 0) flush(nq);
+      __builtin_amdgcn_wave_barrier();  // the queue's last reads before the next key's writes
+      if (!any || key >= bound) continue;
+      float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
+      if (lane < 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
+      }
     }
   }
 }
@@ -846,49 +861,80 @@ int bwd_mla_max_chunk_items(bool det) { return det ? kRedItems : 1 << 30; }
 
 int bwd_mla_map_words(const Params& p) { return (p.Skv + 2047) / 2048 * 64; }
 
-size_t bwd_mla_bytes_per_item(const Params& p, bool det) {
+size_t bwd_mla_pd_bytes_per_item(const Params& p) {
   const int64_t ntiles = (p.topk + kMT - 1) / kMT;
   const int64_t nhg = (p.G + kMHG - 1) / kMHG;
-  size_t n = (size_t)(ntiles * 2 * nhg * 4 * pd_block_elems() * 2);
-  if (det) n += (size_t)p.topk * 576 * 2 + (size_t)bwd_mla_map_words(p) * 6 + (size_t)p.topk;
-  return n;
+  return (size_t)(ntiles * 2 * nhg * 4 * pd_block_elems() * 2);
 }
 
-// Work items (b, t, kv-head) [item0, item0 + n) of one chunk: dQ pass, then
-// dK/dV pass (and for det the index maps before and the reduction after).
-// ws: P / dS of the chunk, then (det) contributions, bitmaps, prefixes and
-// repeat flags.  p.dk_acc holds [B, Skv, Hkv, 576] fp32.
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s) {
-  const int nhg = (p.G + kMHG - 1) / kMHG;
-  const int64_t ntiles = (p.topk + kMT - 1) / kMT;
-  bf16* pd = (bf16*)ws;
-  char* c = (char*)ws + (size_t)n * ntiles * 2 * nhg * 4 * pd_block_elems() * 2;
+size_t bwd_mla_set_bytes_per_item(const Params& p) {
+  return (size_t)p.topk * 576 * 2 + (size_t)bwd_mla_map_words(p) * 6 + (size_t)p.topk;
+}
+
+size_t bwd_mla_bytes_per_item(const Params& p, bool det) {
+  return bwd_mla_pd_bytes_per_item(p) + (det ? bwd_mla_set_bytes_per_item(p) : 0);
+}
+
+namespace {
+// a deterministic chunk's buffer set: contributions, bitmaps, prefixes and
+// repeat flags of n items, in that order
+struct MlaSet {
+  bf16* contrib;
+  uint32_t* kmap;
+  uint16_t* prefix;
+  uint8_t* dup;
+};
+MlaSet mla_set(const Params& p, int n, void* set) {
+  char* c = (char*)set;
   const int W = bwd_mla_map_words(p);
-  bf16* contrib = (bf16*)c;
+  MlaSet m;
+  m.contrib = (bf16*)c;
   c += (size_t)n * p.topk * 576 * 2;
-  uint32_t* kmap = (uint32_t*)c;
+  m.kmap = (uint32_t*)c;
   c += (size_t)n * W * 4;
-  uint16_t* prefix = (uint16_t*)c;
+  m.prefix = (uint16_t*)c;
   c += (size_t)n * W * 2;
-  uint8_t* dup = (uint8_t*)c;
+  m.dup = (uint8_t*)c;
+  return m;
+}
+}  // namespace
+
+// Work items (b, t, kv-head) [item0, item0 + n) of one chunk: dQ pass, then
+// dK/dV pass (and for det the index maps before).  pd: P / dS of the chunk;
+// set (det): the chunk's buffer set, which launch_bwd_mla_reduce then sums.
+// p.dk_acc holds [B, Skv, Hkv, 576] fp32.
+hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd_ws, void* set, bool det,
+                                hipStream_t s) {
+  const int nhg = (p.G + kMHG - 1) / kMHG;
+  bf16* pd = (bf16*)pd_ws;
+  const int W = bwd_mla_map_words(p);
   if (det) {
-    hipLaunchKernelGGL(mla_map_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p, item0, n, W, kmap, prefix,
-                       dup);
-  }
-  hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
-  if (det) {
+    const MlaSet m = mla_set(p, n, set);
+    hipLaunchKernelGGL(mla_map_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p, item0, n, W, m.kmap,
+                       m.prefix, m.dup);
+    hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
     hipLaunchKernelGGL(mla_bwd_dkv_kernel<true>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
-                       (const bf16*)pd, contrib, (const uint32_t*)kmap, (const uint16_t*)prefix,
-                       (const uint8_t*)dup, W);
-    const int b0 = (int)(item0 / ((int64_t)p.Hkv * p.Sq));
-    const int b1 = (int)((item0 + n - 1) / ((int64_t)p.Hkv * p.Sq));
-    const int64_t groups = (int64_t)(b1 - b0 + 1) * p.Hkv * ((p.Skv + 31) / 32) * 2;
-    hipLaunchKernelGGL(mla_bwd_reduce_kernel, dim3((unsigned)groups), dim3(kRedThreads), 0, s, p, item0, n, b0,
-                       b1 - b0 + 1, (const bf16*)contrib, (const uint32_t*)kmap, (const uint16_t*)prefix, W);
+                       (const bf16*)pd, m.contrib, (const uint32_t*)m.kmap, (const uint16_t*)m.prefix,
+                       (const uint8_t*)m.dup, W);
   } else {
+    hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
     hipLaunchKernelGGL(mla_bwd_dkv_kernel<false>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
                        (const bf16*)pd, nullptr, nullptr, nullptr, nullptr, W);
   }
+  return hipGetLastError();
+}
+
+// The ordered reduction of a deterministic chunk's buffer set into
+// p.dk_acc; chunks must be reduced in order.  One workgroup per CU.
+hipError_t launch_bwd_mla_reduce(const Params& p, int64_t item0, int n, void* set, int cus, hipStream_t s) {
+  const MlaSet m = mla_set(p, n, set);
+  const int W = bwd_mla_map_words(p);
+  const int b0 = (int)(item0 / ((int64_t)p.Hkv * p.Sq));
+  const int b1 = (int)((item0 + n - 1) / ((int64_t)p.Hkv * p.Sq));
+  const int64_t groups = (int64_t)(b1 - b0 + 1) * p.Hkv * ((p.Skv + 31) / 32) * 2;
+  const unsigned grid = (unsigned)(groups < cus ? groups : cus);
+  hipLaunchKernelGGL(mla_bwd_reduce_kernel, dim3(grid), dim3(kRedThreads), 0, s, p, item0, n, b0, groups,
+                     (const bf16*)m.contrib, (const uint32_t*)m.kmap, (const uint16_t*)m.prefix, W);
   return hipGetLastError();
 }
 

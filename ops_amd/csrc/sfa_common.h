@@ -284,6 +284,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always reads 0
+// cache-policy operand of the buffer load/store builtins on gfx950: nt
+// (non-temporal), for data one pass writes and another reads exactly once
+constexpr int kCpolNT = 2;
 
 // The contiguous-row gathers form row offsets with __umul24(row id, row
 // bytes), which multiplies the low 24 bits of each operand: a kernel that
@@ -353,13 +356,18 @@ hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
 // MLA shared-KV backward (sfa_bwd_mla.hip): dQ pass + dK/dV pass over a chunk
-// of work items (det: plus index maps and the ordered reduction); the chunk's
-// workspace holds bwd_mla_bytes_per_item per item
+// of work items (det: plus index maps, and the ordered reduction, launched on
+// its own so that it can run beside the next chunk's dQ pass); a chunk needs
+// P / dS (bwd_mla_pd_bytes_per_item per item) and, det, a buffer set
+// (bwd_mla_set_bytes_per_item per item)
 bool bwd_mla_supported(const Params& p);
-bool bwd_mla_det_supported(const Params& p);
-int bwd_mla_max_chunk_items(bool det);  // the deterministic reduction stages a chunk's items in LDS  // deterministic dK/dV: Skv <= 65536
+bool bwd_mla_det_supported(const Params& p);  // deterministic dK/dV: Skv <= 65536
+int bwd_mla_max_chunk_items(bool det);  // the deterministic reduction stages a chunk's items in LDS
 size_t bwd_mla_bytes_per_item(const Params& p, bool det);
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* ws, bool det, hipStream_t s);
+size_t bwd_mla_pd_bytes_per_item(const Params& p);   // P / dS
+size_t bwd_mla_set_bytes_per_item(const Params& p);  // deterministic: contributions and index maps
+hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd, void* set, bool det, hipStream_t s);
+hipError_t launch_bwd_mla_reduce(const Params& p, int64_t item0, int n, void* set, int cus, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
 bool bwd_dq_supported(const Params& p);
 hipError_t launch_bwd_dq(const Params& p, hipStream_t s);   // dQ of the deterministic scheme

@@ -149,6 +149,41 @@ def test_graph_gqa_backward_deterministic():
             assert torch.equal(a, e), f"replay {r}: {name} differs"
 
 
+def test_graph_mla_backward_deterministic_three_chunks():
+    """MLA shared-KV backward, deterministic: 2304 work items run as three
+    chunks (1024, 1024, 256), so the graph holds the fork of each chunk's
+    ordered reduction onto the library's second stream, the wait of chunk 2's
+    dK/dV pass for chunk 0's reduction (the buffer set they share) and the
+    join before the sink gradient and the finish."""
+    B, S, Hq, K = 1, 2304, 128, 256
+    _say(f"graph: MLA backward (deterministic) B={B} S={S} Hq={Hq} K={K}, three chunks")
+    gen = torch.Generator().manual_seed(21)
+    q = torch.randn(B, S, Hq, 576, generator=gen).to(torch.bfloat16).to(DEV)
+    kv = torch.randn(B, S, 1, 576, generator=gen).to(torch.bfloat16).to(DEV)
+    idx = _idx_rows(B, S, 1, K, lambda b, t: t + 1, gen).to(DEV)
+    sink = torch.linspace(-1.0, 1.0, Hq).to(DEV)
+    scale = 576 ** -0.5
+    out, lse = ops_amd.sfa_forward(q, kv, kv[..., :512], idx, scale, attn_sink=sink)
+    dout = torch.empty(B, S, Hq, 512, dtype=torch.bfloat16, device=DEV)
+
+    def step():
+        return ops_amd.sfa_backward(q, kv, kv[..., :512], idx, out, lse, dout, scale, attn_sink=sink,
+                                    merge_kv=True, dkv_mode="csr")
+
+    dout.copy_(torch.randn(dout.shape, generator=gen).to(torch.bfloat16))
+    g, grads_g = _capture(step)
+    for r in range(4):
+        dout.copy_(torch.randn(dout.shape, generator=gen).to(torch.bfloat16))
+        grads_e = step()
+        torch.cuda.synchronize()
+        _eager_noise(r)
+        g.replay()
+        torch.cuda.synchronize()
+        for name, a, e in zip(("dq", "dkv", "dsink"), (grads_g[0], grads_g[1], grads_g[3]),
+                              (grads_e[0], grads_e[1], grads_e[3])):
+            assert torch.equal(a, e), f"replay {r}: {name} differs"
+
+
 def test_graph_indexer_topk():
     """Index producer (scores kernel + selection kernel per query chunk)."""
     B, S, H, topk = 1, 1024, 64, 256
