@@ -730,15 +730,17 @@ __global__ __launch_bounds__(kMThreads, 1) void mla_bwd_dkv_kernel(Params p, int
 // word and its prefix count for each of the chunk's items of (b, g) in LDS
 // (one scattered read per item for all 16 keys, instead of one per item and
 // key), then each of its 4 waves sums the rows of 4 of the keys, one key at
-// a time, in item order into the fp32 accumulator row (each row owned by one
-// wave; chunks run in order).  Lane l holds dims 8 l .. 8 l + 7, lanes 0..7
-// also dims 512 + 8 l ..; a chunk holds at most kRedItems items (host-side
-// cap).
+// a time, into the fp32 accumulator row (each row owned by one wave; chunks
+// run in order) in a fixed order: dims 0..511 in item order, the last 64
+// dims in 8 item-ordered partial sums combined by a fixed tree (see flush).
+// A chunk holds at most kRedItems items (host-side cap).
 // The kernel runs on a second stream beside the next chunk's dQ pass, so it
 // is persistent (one workgroup per CU, groups strided over the grid) and
-// small: its 120 registers per lane next to the dQ pass's 392 (256 + 136
-// accumulation registers) fill the 512 of a SIMD lane, and its 6.4 KB of LDS
-// fit beside the dQ pass's 80 KB.
+// small: its 95 registers per lane fit beside the dQ pass's 392 (256 + 136
+// accumulation registers) in the 512 of a SIMD lane (at most 120 would), and
+// its 6.4 KB of LDS beside the dQ pass's 80 KB.  Its VALU work competes with
+// the dQ pass's on the shared SIMDs, which is why the tail dims are split
+// by rows.
 constexpr int kRedItems = 1024;
 constexpr int kRedThreads = 256;
 constexpr int kRedWaves = kRedThreads / 64;
@@ -786,8 +788,15 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(
       constexpr int U = 8;
       int2* q = s_hits[wave];
       int nq = 0;  // queued hits (wave-uniform)
+      // Row dims 0..511 are lane l's dims 8 l .. 8 l + 7 of every row; the
+      // 64 dims past them are split by rows: lane group r = l / 8 loads dims
+      // 512 + 8 (l % 8) .. of the flush's row r, so a flush of up to 8 rows
+      // takes 9 loads instead of 16, and half the conversions and adds.
+      // a1 holds group r's partial sums of the tail dims over the rows it
+      // took (in item order); they are combined in a fixed order at the end.
+      static_assert(U == 8, "8 lane groups take one row each per flush");
       auto flush = [&](int n) {
-        u32x4 v0[U], v1[U];
+        u32x4 v0[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           if (u < n) {
@@ -795,19 +804,26 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(
             const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
             // (non-temporal: each row is read once, beside the dQ pass's gathers)
             v0[u] = __builtin_nontemporal_load(row + lane);
-            v1[u] = lane < 8 ? __builtin_nontemporal_load(row + 64 + lane) : u32x4{0u, 0u, 0u, 0u};
           }
+        }
+        const int r = lane >> 3;
+        u32x4 vt = {0u, 0u, 0u, 0u};
+        if (r < n) {
+          const int2 h = q[r];
+          const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
+          vt = __builtin_nontemporal_load(row + 64 + (lane & 7));
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           if (u >= n) continue;
           const bf16x8 x0 = __builtin_bit_cast(bf16x8, v0[u]);
-          const bf16x8 x1 = __builtin_bit_cast(bf16x8, v1[u]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            a0[e] += (float)x0[e];
-            a1[e] += (float)x1[e];
-          }
+          for (int e = 0; e < 8; ++e) a0[e] += (float)x0[e];
+        }
+        if (r < n) {
+          const bf16x8 xt = __builtin_bit_cast(bf16x8, vt);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a1[e] += (float)xt[e];
         }
         any = true;
       };
@@ -835,12 +851,24 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(
       if (nq > 0) flush(nq);
       __builtin_amdgcn_wave_barrier();  // the queue's last reads before the next key's writes
       if (!any || key >= bound) continue;
+      // the tail dims' total over the 8 groups' partials, a fixed tree
+      // ((g0 + g1) + (g2 + g3)) + ((g4 + g5) + (g6 + g7)) (the whole wave is
+      // active here)
+      float tail[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float t = a1[e];
+        t += __shfl_xor(t, 8);
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        tail[e] = t;
+      }
       float* dst = p.dk_acc + (((int64_t)b * p.Skv + key) * p.Hkv + g) * 576;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dst[8 * lane + e] += a0[e];
       if (lane < 8) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += a1[e];
+        for (int e = 0; e < 8; ++e) dst[512 + 8 * lane + e] += tail[e];
       }
     }
   }
