@@ -800,8 +800,10 @@ __global__ __launch_bounds__(kRedThreads) void mla_bwd_reduce_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           if (u < n) {
+            // (the queue entry is the wave's: its row address is scalar)
             const int2 h = q[u];
-            const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)h.x * p.topk + h.y) * 576);
+            const int hx = __builtin_amdgcn_readfirstlane(h.x), hy = __builtin_amdgcn_readfirstlane(h.y);
+            const u32x4* row = reinterpret_cast<const u32x4*>(contrib + ((int64_t)hx * p.topk + hy) * 576);
             // (non-temporal: each row is read once, beside the dQ pass's gathers)
             v0[u] = __builtin_nontemporal_load(row + lane);
           }
