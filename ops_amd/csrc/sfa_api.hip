@@ -440,10 +440,11 @@ size_t mla_bytes(const sfa_fwd_args& f, const sfa::Params& p, bool det) {
   return bytes;
 }
 
-// The deterministic MLA backward's reductions run on a second stream of the
-// device (default priority, non-blocking), ordered against the caller's
-// stream by events, so that chunk c's reduction (HBM-bound) overlaps chunk
-// c + 1's dQ pass (MFMA- and LDS-bound).  One per device, created on first
+// The deterministic MLA backward's reductions (and the index maps of the
+// chunk two ahead) run on a second stream of the device (default priority,
+// non-blocking), ordered against the caller's stream by events, so that
+// chunk c's reduction (HBM-bound) overlaps chunk c + 1's dQ pass (MFMA- and
+// LDS-bound).  One per device, created on first
 // use and kept until the process ends; calls on one device enqueue under its
 // mutex, so each call's fork and join of the side stream stay together
 // (also under HIP-graph capture: the side stream joins the caller's capture
@@ -453,7 +454,8 @@ struct MlaSide {
   bool ready = false;
   hipStream_t st = nullptr;
   hipEvent_t dkv_done = nullptr;
-  hipEvent_t red_done[2] = {nullptr, nullptr};
+  hipEvent_t map_done[2] = {nullptr, nullptr};
+  hipEvent_t done = nullptr;
   int cus = 0;
 };
 MlaSide g_side[kMaxDevices];
@@ -463,8 +465,9 @@ hipError_t mla_side_init(MlaSide& m, int dev) {
   hipError_t e = hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess && m.st == nullptr) e = hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking);
   if (e == hipSuccess && m.dkv_done == nullptr) e = hipEventCreateWithFlags(&m.dkv_done, hipEventDisableTiming);
+  if (e == hipSuccess && m.done == nullptr) e = hipEventCreateWithFlags(&m.done, hipEventDisableTiming);
   for (int i = 0; i < 2 && e == hipSuccess; ++i)
-    if (m.red_done[i] == nullptr) e = hipEventCreateWithFlags(&m.red_done[i], hipEventDisableTiming);
+    if (m.map_done[i] == nullptr) e = hipEventCreateWithFlags(&m.map_done[i], hipEventDisableTiming);
   if (e == hipSuccess) m.ready = true;
   return e;
 }
@@ -538,23 +541,36 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
       sets[0] = (char*)pd + align_up((size_t)chunk * sfa::bwd_mla_pd_bytes_per_item(p), 256);
       sets[1] = (char*)sets[0] + set_bytes;
     }
+    const int nchunks = (int)((items + chunk - 1) / chunk);
+    auto chunk_len = [&](int c) { return (int)(items - (int64_t)c * chunk < chunk ? items - (int64_t)c * chunk : chunk); };
     hipError_t e = sfa::launch_zero_f32(p.dk_acc, nk, s);
-    int c = 0;
-    for (int64_t i0 = 0; e == hipSuccess && i0 < items; i0 += chunk, ++c) {
-      const int n = (int)(items - i0 < chunk ? items - i0 : chunk);
-      // (det: chunk c - 2's reduction read this buffer set)
-      if (det && c >= 2) e = hipStreamWaitEvent(s, side->red_done[c & 1], 0);
-      if (e == hipSuccess) e = sfa::launch_bwd_mla_chunk(p, i0, n, pd, sets[c & 1], det, s);
+    // det: the index maps of chunks 0 and 1 first; chunk c + 2's are built on
+    // the side stream right after chunk c's reduction, in the buffer set that
+    // reduction frees, so only the dK/dV pass waits for them
+    for (int c = 0; det && c < 2 && c < nchunks && e == hipSuccess; ++c)
+      e = sfa::launch_bwd_mla_map(p, (int64_t)c * chunk, chunk_len(c), sets[c & 1], s);
+    bool forked = false;
+    for (int c = 0; e == hipSuccess && c < nchunks; ++c) {
+      const int64_t i0 = (int64_t)c * chunk;
+      const int n = chunk_len(c);
+      e = sfa::launch_bwd_mla_dq(p, i0, n, pd, s);
+      if (det && c >= 2 && e == hipSuccess) e = hipStreamWaitEvent(s, side->map_done[c & 1], 0);
+      if (e == hipSuccess) e = sfa::launch_bwd_mla_dkv(p, i0, n, pd, sets[c & 1], det, s);
       if (det && e == hipSuccess) {
         e = hipEventRecord(side->dkv_done, s);
         if (e == hipSuccess) e = hipStreamWaitEvent(side->st, side->dkv_done, 0);
+        forked = forked || e == hipSuccess;
         if (e == hipSuccess) e = sfa::launch_bwd_mla_reduce(p, i0, n, sets[c & 1], side->cus, side->st);
-        if (e == hipSuccess) e = hipEventRecord(side->red_done[c & 1], side->st);
+        if (e == hipSuccess && c + 2 < nchunks) {
+          e = sfa::launch_bwd_mla_map(p, i0 + 2 * (int64_t)chunk, chunk_len(c + 2), sets[c & 1], side->st);
+          if (e == hipSuccess) e = hipEventRecord(side->map_done[c & 1], side->st);
+        }
       }
     }
-    // join: the last reduction (the side stream runs them in order)
-    if (det && c > 0) {
-      const hipError_t ej = hipStreamWaitEvent(s, side->red_done[(c - 1) & 1], 0);
+    // join: everything the side stream ran (in order)
+    if (forked) {
+      hipError_t ej = hipEventRecord(side->done, side->st);
+      if (ej == hipSuccess) ej = hipStreamWaitEvent(s, side->done, 0);
       if (e == hipSuccess) e = ej;
     }
     if (e == hipSuccess) e = sfa::launch_bwd_dsink(p, s);

@@ -929,25 +929,35 @@ MlaSet mla_set(const Params& p, int n, void* set) {
 }
 }  // namespace
 
-// Work items (b, t, kv-head) [item0, item0 + n) of one chunk: dQ pass, then
-// dK/dV pass (and for det the index maps before).  pd: P / dS of the chunk;
-// set (det): the chunk's buffer set, which launch_bwd_mla_reduce then sums.
-// p.dk_acc holds [B, Skv, Hkv, 576] fp32.
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd_ws, void* set, bool det,
-                                hipStream_t s) {
+// Work items (b, t, kv-head) [item0, item0 + n) of one chunk.  The index
+// maps of a deterministic chunk (into its buffer set), read by its dK/dV
+// pass and its reduction.
+hipError_t launch_bwd_mla_map(const Params& p, int64_t item0, int n, void* set, hipStream_t s) {
+  const MlaSet m = mla_set(p, n, set);
+  hipLaunchKernelGGL(mla_map_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p, item0, n,
+                     bwd_mla_map_words(p), m.kmap, m.prefix, m.dup);
+  return hipGetLastError();
+}
+
+// The dQ pass of a chunk: dQ, δ, and the chunk's P / dS blocks into pd.
+hipError_t launch_bwd_mla_dq(const Params& p, int64_t item0, int n, void* pd, hipStream_t s) {
   const int nhg = (p.G + kMHG - 1) / kMHG;
-  bf16* pd = (bf16*)pd_ws;
+  hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, (bf16*)pd);
+  return hipGetLastError();
+}
+
+// The dK/dV pass of a chunk from its P / dS blocks: det, the contribution
+// rows into the chunk's buffer set (its index maps already built); else
+// fp32 atomics into p.dk_acc.  p.dk_acc holds [B, Skv, Hkv, 576] fp32.
+hipError_t launch_bwd_mla_dkv(const Params& p, int64_t item0, int n, const void* pd, void* set, bool det,
+                              hipStream_t s) {
   const int W = bwd_mla_map_words(p);
   if (det) {
     const MlaSet m = mla_set(p, n, set);
-    hipLaunchKernelGGL(mla_map_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, p, item0, n, W, m.kmap,
-                       m.prefix, m.dup);
-    hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
     hipLaunchKernelGGL(mla_bwd_dkv_kernel<true>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
                        (const bf16*)pd, m.contrib, (const uint32_t*)m.kmap, (const uint16_t*)m.prefix,
                        (const uint8_t*)m.dup, W);
   } else {
-    hipLaunchKernelGGL(mla_bwd_dq_kernel, dim3((unsigned)(n * nhg)), dim3(kMThreads), 0, s, p, item0, n, pd);
     hipLaunchKernelGGL(mla_bwd_dkv_kernel<false>, dim3((unsigned)n), dim3(kMThreads), 0, s, p, item0,
                        (const bf16*)pd, nullptr, nullptr, nullptr, nullptr, W);
   }

@@ -356,8 +356,8 @@ hipError_t launch_fwd_d128(const Params& p, hipStream_t s);
 hipError_t launch_bwd_mfma(const Params& p, hipStream_t s);
 bool bwd_mfma_supported(const Params& p);
 // MLA shared-KV backward (sfa_bwd_mla.hip): dQ pass + dK/dV pass over a chunk
-// of work items (det: plus index maps, and the ordered reduction, launched on
-// its own so that it can run beside the next chunk's dQ pass); a chunk needs
+// of work items (det: plus index maps and the ordered reduction, each
+// launched on its own so that they can run beside the dQ passes); a chunk needs
 // P / dS (bwd_mla_pd_bytes_per_item per item) and, det, a buffer set
 // (bwd_mla_set_bytes_per_item per item)
 bool bwd_mla_supported(const Params& p);
@@ -366,7 +366,10 @@ int bwd_mla_max_chunk_items(bool det);  // the deterministic reduction stages a 
 size_t bwd_mla_bytes_per_item(const Params& p, bool det);
 size_t bwd_mla_pd_bytes_per_item(const Params& p);   // P / dS
 size_t bwd_mla_set_bytes_per_item(const Params& p);  // deterministic: contributions and index maps
-hipError_t launch_bwd_mla_chunk(const Params& p, int64_t item0, int n, void* pd, void* set, bool det, hipStream_t s);
+hipError_t launch_bwd_mla_map(const Params& p, int64_t item0, int n, void* set, hipStream_t s);
+hipError_t launch_bwd_mla_dq(const Params& p, int64_t item0, int n, void* pd, hipStream_t s);
+hipError_t launch_bwd_mla_dkv(const Params& p, int64_t item0, int n, const void* pd, void* set, bool det,
+                              hipStream_t s);
 hipError_t launch_bwd_mla_reduce(const Params& p, int64_t item0, int n, void* set, int cus, hipStream_t s);
 // dQ / dsink pass of the deterministic backward, d = 128 (sfa_bwd_dq.hip)
 bool bwd_dq_supported(const Params& p);

@@ -152,9 +152,10 @@ def test_graph_gqa_backward_deterministic():
 def test_graph_mla_backward_deterministic_three_chunks():
     """MLA shared-KV backward, deterministic: 2304 work items run as three
     chunks (1024, 1024, 256), so the graph holds the fork of each chunk's
-    ordered reduction onto the library's second stream, the wait of chunk 2's
-    dK/dV pass for chunk 0's reduction (the buffer set they share) and the
-    join before the sink gradient and the finish."""
+    ordered reduction onto the library's second stream, chunk 2's index maps
+    built there after chunk 0's reduction (the buffer set they share), the
+    wait of chunk 2's dK/dV pass for them, and the join before the sink
+    gradient and the finish."""
     B, S, Hq, K = 1, 2304, 128, 256
     _say(f"graph: MLA backward (deterministic) B={B} S={S} Hq={Hq} K={K}, three chunks")
     gen = torch.Generator().manual_seed(21)
