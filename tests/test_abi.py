@@ -258,6 +258,39 @@ def test_auto_dkv_scheme_follows_the_cost_rules():
     assert _bwd_ws(1, 65536, 16, 1, 2048, _lib.SFA_DKV_CSR) > (4 << 30)
 
 
+def test_mla_backward_workspace_holds_two_buffer_sets():
+    """The MLA shared-KV backward at S = 32768, top-k 2048: fp32 accumulators
+    of the shared rows, delta, then per chunk of queries the P / dS blocks
+    (1 MiB per query at 128 heads); the deterministic modes run 1024-query
+    chunks and hold two sets of contribution rows and index maps (one
+    chunk's reduction reads one set while the next chunk fills the other),
+    the atomic mode 2048-query chunks and no set."""
+    lib = _lib.load()
+    S, K = 32768, 2048
+
+    def ws(mode):
+        b = _lib.BwdArgs()
+        b.fwd = _mla_prefill_args(S, K)
+        b.flags = _lib.SFA_BWD_MERGE_KV
+        for name in ("dout", "dq", "dk"):
+            setattr(b, name, 0x10000)
+        b.do_sh, b.do_ss, b.do_sb = 512, 128 * 512, S * 128 * 512
+        b.dq_sh, b.dq_ss, b.dq_sb = 576, 128 * 576, S * 128 * 576
+        b.dk_sh, b.dk_ss, b.dk_sb = 576, 576, S * 576
+        b.dkv_mode = mode
+        return lib.sfa_bwd_workspace_size(ctypes.byref(b))
+
+    acc = S * 576 * 4 + S * 128 * 4           # shared-row accumulators + delta (both 256-aligned here)
+    pd = (K // 32) * 2 * 2 * 4 * 512 * 2       # P / dS of one query: 1 MiB
+    assert pd == 1 << 20
+    words = (S + 2047) // 2048 * 64            # bitmap words per query
+    one_set = K * 576 * 2 + words * 6 + K      # contribution rows, bitmap + prefixes, repeat flags
+    for mode in (_lib.SFA_DKV_AUTO, _lib.SFA_DKV_CSR):
+        assert ws(mode) == acc + 1024 * pd + 2 * 1024 * one_set
+    assert 5 << 30 < ws(_lib.SFA_DKV_AUTO) < 6 << 30
+    assert ws(_lib.SFA_DKV_ATOMIC) == acc + 2048 * pd
+
+
 def test_huge_row_strides_leave_the_24_bit_gathers():
     """A K/V row stride of 16 MiB or more cannot go through the kernels whose
     gathers multiply row ids with __umul24: the backward then takes neither
