@@ -260,9 +260,10 @@ SFA_API size_t sfa_bwd_workspace_size(const sfa_bwd_args* a);
  * `_attn_bwd_dk_dv` (SFA.py:1005-1145 via SFA.py:266-298).  dq/dk/dv are
  * fully overwritten (no accumulation into existing contents).  The
  * deterministic MLA backward also enqueues its ordered reductions on a
- * second stream of the current device, which the library creates on its
- * first such call (default priority, non-blocking, kept until the process
- * ends) and orders against `stream` with events: when the call returns,
+ * second stream of the device `stream` belongs to (the current device for
+ * the null stream), which the library creates on its first such call there
+ * (default priority, non-blocking, kept until the process ends) and orders
+ * against `stream` with events: when the call returns,
  * `stream` waits for all of that work, and under HIP-graph capture the
  * second stream joins the capture and is joined back.  Such calls on one
  * device enqueue one at a time (a mutex). */

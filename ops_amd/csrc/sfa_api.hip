@@ -460,15 +460,26 @@ struct MlaSide {
 };
 MlaSide g_side[kMaxDevices];
 
+// (dev: the device of the caller's stream, which need not be the current
+// one; the stream and events are created with dev current, as they must be
+// to order work on dev's streams)
 hipError_t mla_side_init(MlaSide& m, int dev) {
   if (m.ready) return hipSuccess;
-  hipError_t e = hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, dev);
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  if (e != hipSuccess) return e;
+  e = hipDeviceGetAttribute(&m.cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess && m.st == nullptr) e = hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking);
   if (e == hipSuccess && m.dkv_done == nullptr) e = hipEventCreateWithFlags(&m.dkv_done, hipEventDisableTiming);
   if (e == hipSuccess && m.done == nullptr) e = hipEventCreateWithFlags(&m.done, hipEventDisableTiming);
   for (int i = 0; i < 2 && e == hipSuccess; ++i)
     if (m.map_done[i] == nullptr) e = hipEventCreateWithFlags(&m.map_done[i], hipEventDisableTiming);
   if (e == hipSuccess) m.ready = true;
+  if (cur != dev) {
+    const hipError_t er = hipSetDevice(cur);
+    if (e == hipSuccess) e = er;
+  }
   return e;
 }
 
@@ -528,8 +539,10 @@ int sfa_bwd(const sfa_bwd_args* a, void* workspace, size_t workspace_bytes, void
     MlaSide* side = nullptr;
     std::unique_lock<std::mutex> lock;
     if (det) {
+      // the device the caller's stream belongs to (the current one for the
+      // null stream): the reductions must run there
       int dev = 0;
-      hipError_t e0 = hipGetDevice(&dev);
+      hipError_t e0 = s != nullptr ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
       if (e0 == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e0 = hipErrorInvalidDevice;
       if (e0 == hipSuccess) {
         side = &g_side[dev];
