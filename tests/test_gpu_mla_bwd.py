@@ -135,6 +135,52 @@ def test_mla_bwd_invariant_to_invalid_encoding_and_deterministic():
     assert _rel_l2(dkv1.float(), dkv4.float()) <= GRAD_RL2
 
 
+def test_mla_bwd_concurrent_calls_on_two_streams():
+    """Two host threads run the deterministic backward (2304 queries: three
+    chunks, so each call forks its reductions and the index maps of its third
+    chunk onto the library's second stream) at once, each on its own torch
+    stream with its own inputs. The library enqueues one such call at a time
+    per device, and each call orders its work on the shared second stream
+    with its own events: both results are bitwise those of the same calls
+    made one after the other."""
+    import threading
+    _say("MLA bwd: two concurrent calls on two streams, three chunks each")
+    ws = [_inputs(1, 2304, 128, 256, seed=s) for s in (31, 32)]
+    fwd = [ops_amd.sfa_forward(w.q, w.k, w.v, w.idx, w.scale) for w in ws]
+
+    def bwd(i):
+        w, (out, lse) = ws[i], fwd[i]
+        return ops_amd.sfa_backward(w.q, w.k, w.v, w.idx, out, lse, w.dout, w.scale, merge_kv=True)
+
+    seq = [bwd(i) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    got = [None, None]
+    errs = []
+
+    def run(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                for _ in range(3):
+                    got[i] = bwd(i)
+            streams[i].synchronize()
+        except Exception as e:  # reported below
+            errs.append(e)
+
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    th = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errs, errs
+    assert all(not t.is_alive() for t in th)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(got[i][0], seq[i][0]) and torch.equal(got[i][1], seq[i][1]), i
+
+
 def test_mla_bwd_repeated_keys():
     """Index rows that select the same key more than once: every slot counts
     (the oracle sums each slot, SFA.py:386-467); the deterministic mode sends
